@@ -1,0 +1,244 @@
+"""MoE-layer forward benchmark on one MI355X.
+
+Times the whole layer (router -> dispatch plan -> row permutation -> grouped
+SwiGLU GEMMs -> weighted combine) on the full bf16 workload (16384 tokens,
+d_model 2048, 64 experts, top-8, d_ff 1024, capacity factor 1.25), with every
+input resident in HBM before the timed region.  One JSON line on stdout:
+
+  value      tokens/s of the whole layer (1 GPU)
+  roofline   grouped GEMM (gate/up + down): algorithmic 6*R_kept*D*F FLOP over
+             the two kernels' HIP-event time, against dense bf16 MFMA peak
+  kernels    every stage's HIP-event time and roofline fraction
+  cpu_baseline  the NumPy float32 restatement of the layer (oracle/) timed on
+             this host's cores on a 4096-token sample of the same workload
+
+Usage: python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+FP8_PEAK_TFLOPS = 5000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic(wl, kept_rows: int) -> dict:
+    """Per-launch algorithmic work of each stage (bytes or FLOP)."""
+    T, D, N, K, F = wl.tokens, wl.d_model, wl.n_experts, wl.top_k, wl.d_ff
+    R = T * K
+    ex = 2  # bf16 activations
+    x_in = 4 if wl.x_dtype == "f32" else 2
+    out_b = 4 if wl.out_dtype == "f32" else 2
+    w = {}
+    if wl.router_from_logits:
+        w["router"] = ("hbm", T * N * 4 + T * K * 8)
+    else:
+        w["router"] = ("hbm", T * D * x_in + D * N * 4 + T * N * 4 + T * K * 8)
+    w["plan"] = ("hbm", 2 * R * 4 + R * 4 + R * 4 + R + N * 8)
+    # dispatch: read every token once, write the kept rows, read the slot map
+    w["permute"] = ("hbm", T * D * x_in + kept_rows * D * ex + R * 4)
+    if wl.expert == "swiglu":
+        w["gate_up"] = ("mfma", 2 * 2 * kept_rows * D * F)
+        w["down"] = ("mfma", 2 * kept_rows * F * D)
+    # combine: read kept rows, write tokens, read slot map and gates
+    w["combine"] = ("hbm", kept_rows * D * ex + T * D * out_b + R * 8)
+    return w
+
+
+def cpu_baseline(wl_name: str, sample_tokens: int, seed: int) -> dict:
+    import oracle as O
+    from hanuman_amd import workloads as W
+    cores = len(os.sched_getaffinity(0))
+    wl = W.WORKLOADS[wl_name].scaled(sample_tokens)
+    inp = W.make_inputs(wl, seed=seed)
+    params = {"router": inp.router, "expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
+              "expert_w_down": inp.w_down}
+    kw = dict(top_k=wl.top_k, routing=wl.routing, capacity_factor=wl.capacity_factor,
+              expert=wl.expert, dtype="bf16" if wl.x_dtype == "bf16" else "f32",
+              precision="f32", fast_router=True,
+              logits=inp.logits if wl.router_from_logits else None)
+    O.moe_forward(inp.x, params, **kw)                      # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.moe_forward(inp.x, params, **kw)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    try:
+        model = subprocess.run(["bash", "-c", "lscpu | grep 'Model name' | head -1"],
+                               capture_output=True, text=True, timeout=10).stdout.split(":")[-1].strip()
+    except Exception:  # noqa: BLE001 -- informational only
+        model = "unknown"
+    return {"value": round(wl.tokens / t, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"{wl.tokens} tokens of the {wl_name} layer (same shape, seed {seed}), "
+                       f"NumPy float32 restatement of model/moe.py with OpenBLAS, median of 3 "
+                       f"after 1 warm-up, {cores} threads, CPU {model}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the MoE layer holds every expert in one MI355X's HBM "
+              f"and this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world})", file=sys.stderr)
+        sys.exit(2)
+    cores = len(os.sched_getaffinity(0))
+    os.environ.setdefault("OPENBLAS_NUM_THREADS", str(cores))
+
+    import torch
+    from hanuman_amd import workloads as W
+    from hanuman_amd.layer import DeviceLayer
+
+    name = args.workload or W.HEADLINE
+    wl = W.WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    log(f"[bench] workload {name}: T={wl.tokens} D={wl.d_model} N={wl.n_experts} "
+        f"K={wl.top_k} F={wl.d_ff} CF={wl.capacity_factor}")
+    inp = W.make_inputs(wl, seed=args.seed)
+    layer = DeviceLayer(inp, dev)
+    del inp
+    torch.cuda.synchronize()
+
+    stages = ["router", "plan", "permute"] + (["gate_up", "down"] if wl.expert == "swiglu" else []) + ["combine"]
+
+    def step(ev=None):
+        """One layer forward; with ``ev`` records an event after each stage."""
+        import hanuman_amd.kernels as K
+        if ev is not None:
+            ev[0].record()
+        logits, top_idx, gates = layer.route()
+        if ev is not None:
+            ev[1].record()
+        plan = K.dispatch_plan(top_idx, wl.n_experts, layer.capacity, layer.workspace)
+        if ev is not None:
+            ev[2].record()
+        xs = K.permute_rows(layer.x, plan, torch.bfloat16)
+        if ev is not None:
+            ev[3].record()
+        i = 4
+        if wl.expert == "swiglu":
+            h = K.grouped_gate_up(xs, plan.offsets, layer.w_gate_up)
+            if ev is not None:
+                ev[i].record()
+            ys = K.grouped_down(h, plan.offsets, layer.w_down)
+            if ev is not None:
+                ev[i + 1].record()
+            i += 2
+        else:
+            ys = xs
+        out = K.combine(ys, plan, gates, None, layer.out_dtype)
+        if ev is not None:
+            ev[i].record()
+        return plan, out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` layer forwards, events between stages.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+           for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    plan = None
+    for s in range(args.steps):
+        plan, _ = step(evs[s])
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_total = t_start.elapsed_time(t_end)
+    ms_per_step = ms_total / args.steps
+    stage_ms = {st: float(np.mean([evs[s][j].elapsed_time(evs[s][j + 1]) for s in range(args.steps)]))
+                for j, st in enumerate(stages)}
+    kept = int(plan.offsets[-1].item())
+    work = algorithmic(wl, kept)
+    kernels = {}
+    for st in stages:
+        kind, amount = work[st]
+        t = stage_ms[st] / 1e3
+        if kind == "hbm":
+            ach = amount / t / 1e9
+            kernels[st] = {"ms": round(stage_ms[st], 4), "bound": "hbm", "achieved": round(ach, 1),
+                           "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "bytes": amount}
+        else:
+            ach = amount / t / 1e12
+            kernels[st] = {"ms": round(stage_ms[st], 4), "bound": "mfma", "achieved": round(ach, 1),
+                           "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "flop": amount}
+    tokens_per_s = wl.tokens / (ms_per_step / 1e3)
+    if wl.expert == "swiglu":
+        flop = work["gate_up"][1] + work["down"][1]
+        t_gemm = (stage_ms["gate_up"] + stage_ms["down"]) / 1e3
+        ach = flop / t_gemm / 1e12
+        roofline = {"kernel": "grouped_gemm_kernel (gate/up + down)", "bound": "mfma",
+                    "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                    "flop_per_launch": flop, "ms": round(t_gemm * 1e3, 4)}
+    else:
+        b = work["permute"][1] + work["combine"][1]
+        t = (stage_ms["permute"] + stage_ms["combine"]) / 1e3
+        ach = b / t / 1e9
+        roofline = {"kernel": "permute_rows_kernel + combine_kernel", "bound": "hbm",
+                    "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": b,
+                    "ms": round(t * 1e3, 4)}
+    log(f"[bench] {ms_per_step:.4f} ms/step, {tokens_per_s / 1e6:.3f} M tokens/s; stages "
+        + ", ".join(f"{k} {v:.4f}" for k, v in stage_ms.items()))
+    del layer
+    torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"[bench] cpu baseline on {args.cpu_sample_tokens} tokens, {cores} cores")
+        cpu = cpu_baseline(name, args.cpu_sample_tokens, args.seed)
+        log(f"[bench] cpu baseline {cpu['value']} tokens/s")
+
+    line = {
+        "metric": "MoE layer tokens/s (1 GPU); grouped-GEMM MFMA util %; dispatch HBM GB/s",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded normal inputs and weights, fixed draw order)",
+        "config": {"workload": name, "tokens": wl.tokens, "d_model": wl.d_model,
+                   "n_experts": wl.n_experts, "top_k": wl.top_k, "d_ff": wl.d_ff,
+                   "capacity_factor": wl.capacity_factor, "routing": wl.routing,
+                   "kept_rows": kept, "parallelism": "single GPU, all experts resident"},
+        "roofline": roofline,
+        "kernels": kernels,
+        "dispatch_hbm_gbs": kernels["permute"]["achieved"],
+        "grouped_gemm_mfma_util": roofline["frac"] if wl.expert == "swiglu" else None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,206 @@
+// Router aux outputs (model/moe.py:253-292): router_z_loss, balance_loss,
+// mean_entropy and expert_counts, from the router logits and top-k indices.
+//
+// Pass 1: one workgroup per 64-token chunk of one sequence; each wave takes
+// every fourth token, lanes own experts.  Per token it forms logsumexp,
+// sigmoid scores, the normalised routing distribution p and its entropy; it
+// accumulates p per expert and lse^2 / entropy per wave, then the four waves
+// are summed in a fixed order.  The chunk's per-sequence expert histogram is
+// counted in LDS.  Pass 2: one workgroup reduces the chunk partials in chunk
+// order into the four outputs.  Every float reduction has a fixed order, so
+// results are identical from run to run.
+#include "hmoe_common.h"
+
+namespace hmoe {
+namespace {
+
+constexpr int kChunk = 64;
+constexpr int kMaxN = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Partial layout per chunk: probs[N], counts[N] (as int), z, ent.
+__host__ __device__ inline int64_t part_stride(int n) { return 2 * static_cast<int64_t>(n) + 2; }
+
+template <int EPL>
+__global__ __launch_bounds__(256) void aux_chunk_kernel(const float* __restrict__ logits,
+                                                        const int32_t* __restrict__ top_idx,
+                                                        int seq, int n_experts, int top_k,
+                                                        int chunks_per_seq,
+                                                        float* __restrict__ parts) {
+  __shared__ float wprobs[4][kMaxN];
+  __shared__ float wz[4], went[4];
+  __shared__ int32_t hist[kMaxN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int chunk = blockIdx.x;
+  const int b = chunk / chunks_per_seq;
+  const int c = chunk % chunks_per_seq;
+  const int s0 = c * kChunk;
+  const int s1 = min(seq, s0 + kChunk);
+  const int64_t tok0 = static_cast<int64_t>(b) * seq;
+  for (int e = tid; e < n_experts; e += 256) hist[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < (s1 - s0) * top_k; i += 256) {
+    const int e = top_idx[(tok0 + s0) * top_k + i];
+    if (static_cast<unsigned>(e) < static_cast<unsigned>(n_experts)) atomicAdd(&hist[e], 1);
+  }
+  float pacc[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) pacc[j] = 0.0f;
+  float zacc = 0.0f, eacc = 0.0f;
+  for (int s = s0 + wave; s < s1; s += 4) {
+    const float* row = logits + (tok0 + s) * n_experts;
+    float l[EPL], sg[EPL];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      l[j] = e < n_experts ? row[e] : -__builtin_inff();
+      m = fmaxf(m, l[j]);
+    }
+    m = wave_max(m);
+    float se = 0.0f, ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const bool ok = lane + 64 * j < n_experts;
+      se += ok ? expf(l[j] - m) : 0.0f;
+      sg[j] = ok ? sigmoid_det(l[j]) : 0.0f;
+      ss += sg[j];
+    }
+    se = wave_sum(se);
+    ss = wave_sum(ss);
+    const float lse = m + logf(se);
+    float ent = 0.0f;
+    const float inv = 1.0f / (ss + 1e-9f);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const float p = sg[j] * inv;
+      pacc[j] += p;
+      if (lane + 64 * j < n_experts) ent -= p * logf(p + 1e-9f);
+    }
+    ent = wave_sum(ent);
+    zacc += lse * lse;
+    eacc += ent;
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < n_experts) wprobs[wave][e] = pacc[j];
+  }
+  if (lane == 0) {
+    wz[wave] = zacc;
+    went[wave] = eacc;
+  }
+  __syncthreads();
+  float* out = parts + static_cast<int64_t>(chunk) * part_stride(n_experts);
+  for (int e = tid; e < n_experts; e += 256) {
+    out[e] = ((wprobs[0][e] + wprobs[1][e]) + wprobs[2][e]) + wprobs[3][e];
+    reinterpret_cast<int32_t*>(out)[n_experts + e] = hist[e];
+  }
+  if (tid == 0) {
+    out[2 * n_experts] = ((wz[0] + wz[1]) + wz[2]) + wz[3];
+    out[2 * n_experts + 1] = ((went[0] + went[1]) + went[2]) + went[3];
+  }
+}
+
+// One workgroup of 256 threads.
+__global__ __launch_bounds__(256) void aux_final_kernel(const float* __restrict__ parts, int batch,
+                                                        int seq, int n_experts, int top_k,
+                                                        int chunks_per_seq,
+                                                        float* __restrict__ losses,
+                                                        float* __restrict__ expert_counts) {
+  __shared__ float bal_terms[kMaxN];
+  __shared__ float bal_seq[1024];
+  const int tid = threadIdx.x;
+  const int64_t stride = part_stride(n_experts);
+  const int nchunks = batch * chunks_per_seq;
+  // expert_counts[n] = sum over all chunks (exact integers).
+  for (int e = tid; e < n_experts; e += 256) {
+    int64_t cnt = 0;
+    for (int ch = 0; ch < nchunks; ++ch)
+      cnt += reinterpret_cast<const int32_t*>(parts + ch * stride)[n_experts + e];
+    expert_counts[e] = static_cast<float>(cnt);
+  }
+  // balance: per sequence b, N * sum_n (count/(S*K)) * (sum_s p / S).
+  for (int b = 0; b < batch; ++b) {
+    for (int e = tid; e < n_experts; e += 256) {
+      float psum = 0.0f;
+      int64_t cnt = 0;
+      for (int c = 0; c < chunks_per_seq; ++c) {
+        const float* pp = parts + static_cast<int64_t>(b * chunks_per_seq + c) * stride;
+        psum += pp[e];
+        cnt += reinterpret_cast<const int32_t*>(pp)[n_experts + e];
+      }
+      const float frac = static_cast<float>(cnt) / static_cast<float>(seq * top_k);
+      bal_terms[e] = frac * (psum / static_cast<float>(seq));
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float acc = 0.0f;
+      for (int e = 0; e < n_experts; ++e) acc += bal_terms[e];
+      if (b < 1024) bal_seq[b] = static_cast<float>(n_experts) * acc;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    float z = 0.0f, ent = 0.0f, bal = 0.0f;
+    for (int ch = 0; ch < nchunks; ++ch) {
+      z += parts[ch * stride + 2 * n_experts];
+      ent += parts[ch * stride + 2 * n_experts + 1];
+    }
+    for (int b = 0; b < batch && b < 1024; ++b) bal += bal_seq[b];
+    const float tokens = static_cast<float>(batch) * static_cast<float>(seq);
+    losses[0] = z / tokens;
+    losses[1] = bal / static_cast<float>(batch);
+    losses[2] = ent / tokens;
+  }
+}
+
+}  // namespace
+}  // namespace hmoe
+
+extern "C" size_t hmoe_aux_workspace_bytes(int batch, int seq, int n_experts) {
+  if (batch <= 0 || seq <= 0 || n_experts <= 0) return 0;
+  const int64_t chunks = static_cast<int64_t>(batch) * hmoe::ceil_div(seq, hmoe::kChunk);
+  return static_cast<size_t>(chunks * hmoe::part_stride(n_experts) * sizeof(float));
+}
+
+extern "C" int hmoe_router_aux(const float* logits, const int32_t* top_idx, int batch, int seq,
+                               int n_experts, int top_k, float* losses, float* expert_counts,
+                               void* workspace, size_t workspace_bytes, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(batch >= 1 && batch <= 1024 && seq >= 1,
+               "router_aux: need 1 <= batch <= 1024 and seq >= 1 (got %d, %d)", batch, seq);
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxN, "router_aux: n_experts must be in [1, %d]",
+               kMaxN);
+  HMOE_REQUIRE(top_k >= 1 && top_k <= n_experts, "router_aux: bad top_k %d", top_k);
+  HMOE_REQUIRE(logits && top_idx && losses && expert_counts && workspace,
+               "router_aux: null pointer argument");
+  const size_t need = hmoe_aux_workspace_bytes(batch, seq, n_experts);
+  HMOE_REQUIRE_CODE(workspace_bytes >= need, HMOE_ERR_WORKSPACE,
+                    "router_aux: workspace of %zu bytes is smaller than the %zu required",
+                    workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int cps = static_cast<int>(ceil_div(seq, kChunk));
+  const dim3 grid(static_cast<unsigned>(batch * cps));
+  float* parts = static_cast<float*>(workspace);
+  if (n_experts <= 64)
+    hipLaunchKernelGGL(aux_chunk_kernel<1>, grid, dim3(256), 0, s, logits, top_idx, seq, n_experts, top_k, cps, parts);
+  else if (n_experts <= 128)
+    hipLaunchKernelGGL(aux_chunk_kernel<2>, grid, dim3(256), 0, s, logits, top_idx, seq, n_experts, top_k, cps, parts);
+  else
+    hipLaunchKernelGGL(aux_chunk_kernel<4>, grid, dim3(256), 0, s, logits, top_idx, seq, n_experts, top_k, cps, parts);
+  if (int rc = check_launch("router_aux/chunk")) return rc;
+  hipLaunchKernelGGL(aux_final_kernel, dim3(1), dim3(256), 0, s, parts, batch, seq, n_experts, top_k,
+                     cps, losses, expert_counts);
+  return check_launch("router_aux/final");
+}

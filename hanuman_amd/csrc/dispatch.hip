@@ -1,0 +1,320 @@
+// Dispatch plan and row permutation (model/moe.py:54-65, :80, :198).
+//
+// Plan: three deterministic passes over the R = T*K flat slots i = t*K + k.
+//   1. histogram: each block of kSlotsPerBlock slots counts its experts;
+//   2. scan: one workgroup turns the [blocks, N] histogram into per-block
+//      bases (slots of the same expert in earlier blocks), the totals
+//      (= bincount), and kept-row offsets (exclusive scan of min(count, C));
+//   3. rank: each wave walks its slots 64 at a time in ascending i; lanes that
+//      hold the same expert find each other with one ballot per expert-id bit,
+//      so a slot's rank is (base) + (earlier lanes of its expert).  The rank
+//      fixes keep (rank < C), slot_pos and perm_src; no atomic decides a value.
+// Permutation: one wave per token reads the row once and writes its kept
+// slots' rows (token-centric, so x is read exactly once).
+#include "hmoe_common.h"
+
+namespace hmoe {
+namespace {
+
+constexpr int kPlanThreads = 256;
+constexpr int kSlotsPerWave = 1024;
+constexpr int kSlotsPerBlock = 4 * kSlotsPerWave;
+constexpr int kMaxExperts = 1024;
+
+int64_t plan_blocks(int64_t rows) { return ceil_div(rows, kSlotsPerBlock); }
+
+__global__ __launch_bounds__(kPlanThreads) void plan_histogram_kernel(
+    const int32_t* __restrict__ top_idx, int64_t rows, int n_experts, int32_t* __restrict__ hist) {
+  __shared__ int32_t h[kMaxExperts];
+  for (int e = threadIdx.x; e < n_experts; e += kPlanThreads) h[e] = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSlotsPerBlock;
+  for (int i = threadIdx.x; i < kSlotsPerBlock; i += kPlanThreads) {
+    const int64_t s = base + i;
+    if (s < rows) {
+      const int e = top_idx[s];
+      if (static_cast<unsigned>(e) < static_cast<unsigned>(n_experts)) atomicAdd(&h[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < n_experts; e += kPlanThreads)
+    hist[static_cast<int64_t>(blockIdx.x) * n_experts + e] = h[e];
+}
+
+// One workgroup of 1024 threads.  hist is rewritten in place into the
+// per-block exclusive bases.
+__global__ __launch_bounds__(1024) void plan_scan_kernel(int32_t* __restrict__ hist, int nblk,
+                                                          int n_experts, int64_t capacity,
+                                                          int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets) {
+  __shared__ int32_t kept[kMaxExperts];
+  const int e = threadIdx.x;
+  int32_t total = 0;
+  if (e < n_experts) {
+    for (int b = 0; b < nblk; ++b) {
+      const int64_t idx = static_cast<int64_t>(b) * n_experts + e;
+      const int32_t c = hist[idx];
+      hist[idx] = total;
+      total += c;
+    }
+    counts[e] = total;
+  }
+  kept[e] = (e < n_experts) ? static_cast<int32_t>(total < capacity ? total : capacity) : 0;
+  __syncthreads();
+  // Inclusive Hillis-Steele scan over 1024 entries.
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t v = e >= off ? kept[e - off] : 0;
+    __syncthreads();
+    kept[e] += v;
+    __syncthreads();
+  }
+  if (e < n_experts) offsets[e + 1] = kept[e];
+  if (e == 0) offsets[0] = 0;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(
+    const int32_t* __restrict__ top_idx, int64_t rows, int n_experts, int64_t capacity,
+    const int32_t* __restrict__ bases, const int32_t* __restrict__ offsets,
+    int32_t* __restrict__ slot_pos, int32_t* __restrict__ perm_src, uint8_t* __restrict__ keep,
+    int64_t rows_cap) {
+  __shared__ int32_t whist[4][kMaxExperts];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t blk_base = static_cast<int64_t>(blockIdx.x) * kSlotsPerBlock;
+  const int64_t wave_base = blk_base + static_cast<int64_t>(wave) * kSlotsPerWave;
+
+  for (int i = tid; i < 4 * kMaxExperts; i += kPlanThreads) (&whist[0][0])[i] = 0;
+  __syncthreads();
+  for (int i = lane; i < kSlotsPerWave; i += 64) {
+    const int64_t s = wave_base + i;
+    if (s < rows) {
+      const int e = top_idx[s];
+      if (static_cast<unsigned>(e) < static_cast<unsigned>(n_experts)) atomicAdd(&whist[wave][e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < n_experts; e += kPlanThreads) {
+    int32_t run = bases[static_cast<int64_t>(blockIdx.x) * n_experts + e];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int32_t c = whist[w][e];
+      whist[w][e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+
+  const int nbits = n_experts > 1 ? 32 - __builtin_clz(static_cast<unsigned>(n_experts - 1)) : 0;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int32_t* my_hist = whist[wave];
+  for (int c = 0; c < kSlotsPerWave; c += 64) {
+    const int64_t s = wave_base + c + lane;
+    int e = s < rows ? top_idx[s] : -1;
+    const bool valid = static_cast<unsigned>(e) < static_cast<unsigned>(n_experts);
+    if (!valid) e = 0;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      peers &= bit ? bal : ~bal;
+    }
+    int32_t base = 0;
+    if (valid) base = my_hist[e];
+    const int32_t rank = base + __popcll(peers & lt_mask);
+    const bool leader = valid && ((peers & lt_mask) == 0);
+    if (leader) my_hist[e] = base + __popcll(peers);
+    if (s < rows && !valid) {  // out-of-range expert id: never dispatched
+      keep[s] = 0;
+      slot_pos[s] = -1;
+    }
+    if (valid) {
+      const bool kept = rank < capacity;
+      keep[s] = kept ? 1 : 0;
+      if (kept) {
+        const int32_t pos = offsets[e] + rank;
+        slot_pos[s] = pos;
+        perm_src[pos] = static_cast<int32_t>(s);
+      } else {
+        slot_pos[s] = -1;
+      }
+    }
+  }
+  // Rows past the kept total hold -1.
+  const int64_t total = offsets[n_experts];
+  for (int64_t j = total + static_cast<int64_t>(blockIdx.x) * kPlanThreads + tid; j < rows_cap;
+       j += static_cast<int64_t>(gridDim.x) * kPlanThreads)
+    perm_src[j] = -1;
+}
+
+// ------------------------------------------------------------ permutation --
+template <typename TI>
+struct Chunk8;
+template <>
+struct Chunk8<uint16_t> {
+  u32x4 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ float get(int i) const {
+    const uint32_t w = v[i >> 1];
+    return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+};
+template <>
+struct Chunk8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
+};
+
+template <typename TI, typename TO>
+__device__ __forceinline__ void store8(TO* dst, const Chunk8<TI>& c);
+template <>
+__device__ __forceinline__ void store8<uint16_t, uint16_t>(uint16_t* dst, const Chunk8<uint16_t>& c) {
+  *reinterpret_cast<u32x4*>(dst) = c.v;
+}
+template <>
+__device__ __forceinline__ void store8<float, uint16_t>(uint16_t* dst, const Chunk8<float>& c) {
+  u32x4 o;
+  o[0] = pack_bf16x2(c.a[0], c.a[1]);
+  o[1] = pack_bf16x2(c.a[2], c.a[3]);
+  o[2] = pack_bf16x2(c.b[0], c.b[1]);
+  o[3] = pack_bf16x2(c.b[2], c.b[3]);
+  *reinterpret_cast<u32x4*>(dst) = o;
+}
+template <>
+__device__ __forceinline__ void store8<float, float>(float* dst, const Chunk8<float>& c) {
+  *reinterpret_cast<f32x4*>(dst) = c.a;
+  *reinterpret_cast<f32x4*>(dst + 4) = c.b;
+}
+template <>
+__device__ __forceinline__ void store8<uint16_t, float>(float* dst, const Chunk8<uint16_t>& c) {
+  f32x4 a, b;
+  for (int i = 0; i < 4; ++i) {
+    a[i] = c.get(i);
+    b[i] = c.get(4 + i);
+  }
+  *reinterpret_cast<f32x4*>(dst) = a;
+  *reinterpret_cast<f32x4*>(dst + 4) = b;
+}
+
+constexpr int kPermUnroll = 4;
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void permute_rows_kernel(const TI* __restrict__ x, int64_t tokens,
+                                                           int d_model, int top_k,
+                                                           const int32_t* __restrict__ slot_pos,
+                                                           TO* __restrict__ xs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  const int32_t my_pos = lane < top_k ? slot_pos[t * top_k + lane] : -1;
+  const int chunks = d_model / 8;
+  const TI* src = x + t * d_model;
+  for (int c0 = 0; c0 < chunks; c0 += 64 * kPermUnroll) {
+    Chunk8<TI> v[kPermUnroll];
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const int c = c0 + u * 64 + lane;
+      if (c < chunks) v[u].load(src + static_cast<int64_t>(c) * 8);
+    }
+    for (int k = 0; k < top_k; ++k) {
+      const int32_t pos = __shfl(my_pos, k, 64);
+      if (pos < 0) continue;
+      TO* dst = xs + static_cast<int64_t>(pos) * d_model;
+#pragma unroll
+      for (int u = 0; u < kPermUnroll; ++u) {
+        const int c = c0 + u * 64 + lane;
+        if (c < chunks) store8<TI, TO>(dst + static_cast<int64_t>(c) * 8, v[u]);
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace hmoe
+
+extern "C" size_t hmoe_plan_workspace_bytes(int64_t tokens, int top_k, int n_experts) {
+  if (tokens <= 0 || top_k <= 0 || n_experts <= 0) return 0;
+  return static_cast<size_t>(hmoe::plan_blocks(tokens * top_k)) * n_experts * sizeof(int32_t);
+}
+
+extern "C" int hmoe_dispatch_plan(const int32_t* top_idx, int64_t tokens, int top_k,
+                                  int n_experts, int64_t capacity, int32_t* counts,
+                                  int32_t* offsets, int32_t* slot_pos, int32_t* perm_src,
+                                  uint8_t* keep, void* workspace, size_t workspace_bytes,
+                                  hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(tokens >= 0 && top_k >= 1, "dispatch_plan: need tokens >= 0 and top_k >= 1");
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "dispatch_plan: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
+  HMOE_REQUIRE(capacity >= 1, "dispatch_plan: capacity must be >= 1 (got %lld)",
+               (long long)capacity);
+  const int64_t rows = tokens * top_k;
+  HMOE_REQUIRE(rows < (int64_t(1) << 31), "dispatch_plan: T*K must fit in int32 (got %lld)",
+               (long long)rows);
+  HMOE_REQUIRE(counts && offsets, "dispatch_plan: null pointer argument");
+  const size_t need = hmoe_plan_workspace_bytes(tokens, top_k, n_experts);
+  HMOE_REQUIRE_CODE(workspace_bytes >= need, HMOE_ERR_WORKSPACE,
+                    "dispatch_plan: workspace of %zu bytes is smaller than the %zu required",
+                    workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows_cap = hmoe_rows_cap(tokens, top_k, n_experts, capacity);
+  const int64_t nblk64 = plan_blocks(rows);
+  HMOE_REQUIRE(nblk64 < (int64_t(1) << 30), "dispatch_plan: too many slots");
+  const int nblk = static_cast<int>(nblk64);
+  if (rows > 0) {
+    HMOE_REQUIRE(top_idx && slot_pos && perm_src && keep && workspace,
+                 "dispatch_plan: null pointer argument");
+    int32_t* hist = static_cast<int32_t*>(workspace);
+    hipLaunchKernelGGL(plan_histogram_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
+                       n_experts, hist);
+    if (int rc = check_launch("dispatch_plan/histogram")) return rc;
+    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, hist, nblk, n_experts, capacity,
+                       counts, offsets);
+    if (int rc = check_launch("dispatch_plan/scan")) return rc;
+    hipLaunchKernelGGL(plan_rank_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
+                       n_experts, capacity, hist, offsets, slot_pos, perm_src, keep, rows_cap);
+    return check_launch("dispatch_plan/rank");
+  }
+  // No slots: zero counts and offsets.
+  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, static_cast<int32_t*>(nullptr), 0,
+                     n_experts, capacity, counts, offsets);
+  return check_launch("dispatch_plan/scan");
+}
+
+extern "C" int hmoe_permute_rows(const void* x, int x_dtype, int64_t tokens, int d_model,
+                                 int top_k, const int32_t* slot_pos, void* xs, int xs_dtype,
+                                 hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(tokens >= 0 && top_k >= 1 && top_k <= 64,
+               "permute_rows: need tokens >= 0 and 1 <= top_k <= 64");
+  HMOE_REQUIRE(d_model >= 8 && d_model % 8 == 0, "permute_rows: d_model must be a multiple of 8 (got %d)",
+               d_model);
+  HMOE_REQUIRE((x_dtype == HMOE_F32 || x_dtype == HMOE_BF16) &&
+                   (xs_dtype == HMOE_F32 || xs_dtype == HMOE_BF16),
+               "permute_rows: dtypes must be F32 or BF16");
+  if (tokens == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && slot_pos && xs, "permute_rows: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4)));
+  if (x_dtype == HMOE_BF16 && xs_dtype == HMOE_BF16)
+    hipLaunchKernelGGL((permute_rows_kernel<uint16_t, uint16_t>), grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), tokens, d_model, top_k, slot_pos,
+                       static_cast<uint16_t*>(xs));
+  else if (x_dtype == HMOE_F32 && xs_dtype == HMOE_BF16)
+    hipLaunchKernelGGL((permute_rows_kernel<float, uint16_t>), grid, dim3(256), 0, s,
+                       static_cast<const float*>(x), tokens, d_model, top_k, slot_pos,
+                       static_cast<uint16_t*>(xs));
+  else if (x_dtype == HMOE_F32 && xs_dtype == HMOE_F32)
+    hipLaunchKernelGGL((permute_rows_kernel<float, float>), grid, dim3(256), 0, s,
+                       static_cast<const float*>(x), tokens, d_model, top_k, slot_pos,
+                       static_cast<float*>(xs));
+  else
+    hipLaunchKernelGGL((permute_rows_kernel<uint16_t, float>), grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), tokens, d_model, top_k, slot_pos,
+                       static_cast<float*>(xs));
+  return check_launch("hmoe_permute_rows");
+}

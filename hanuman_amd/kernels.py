@@ -1,0 +1,255 @@
+"""Per-stage wrappers over the C ABI on torch device tensors.
+
+torch provides device memory and the current stream; every computation runs in
+``libhanuman_moe.so``.  Each wrapper validates shapes/dtypes/devices on the
+host (so no kernel ever sees an inconsistent launch), allocates outputs with
+``torch.empty`` and enqueues the kernel on ``torch.cuda.current_stream()``.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check(t: torch.Tensor, name: str, ndim: int | None = None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a GPU device (got {t.device})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims (got shape {tuple(t.shape)})")
+
+
+def capacity(tokens: int, top_k: int, n_experts: int, capacity_factor) -> int:
+    """Capacity per expert (``ceil(CF*T*K/N)``; ``None`` = dropless)."""
+    cf = 0.0 if capacity_factor is None else float(capacity_factor)
+    return int(_lib.lib().hmoe_capacity(tokens, top_k, n_experts, cf))
+
+
+def rows_cap(tokens: int, top_k: int, n_experts: int, cap: int) -> int:
+    return int(_lib.lib().hmoe_rows_cap(tokens, top_k, n_experts, cap))
+
+
+# ---------------------------------------------------------------- router --
+
+def router(x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None, top_k: int,
+           mode: int = _lib.ROUTE_SIGMOID_BIAS, routed_scaling_factor: float = 1.0):
+    """Router logits, top-k indices and gates (``moe.py:175-192``).
+
+    ``x [T,D]``, ``router_w [D,N]``, ``bias [N]`` float32 or None.
+    Returns (logits f32 [T,N], top_idx i32 [T,K], gates f32 [T,K]).
+    """
+    _check(x, "x", 2)
+    _check(router_w, "router_w", 2)
+    T, D = x.shape
+    if router_w.shape[0] != D:
+        raise ValueError(f"router_w has {router_w.shape[0]} rows, x has d_model {D}")
+    N = router_w.shape[1]
+    if bias is not None:
+        _check(bias, "bias", 1)
+        if bias.dtype != torch.float32 or bias.shape[0] != N:
+            raise ValueError("bias must be float32 [n_experts]")
+    dev = x.device
+    logits = torch.empty((T, N), dtype=torch.float32, device=dev)
+    top_idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    gates = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    call("hmoe_router", _ptr(x), _dtype_code(x), _ptr(router_w), _dtype_code(router_w),
+         _ptr(bias), T, D, N, top_k, mode, float(routed_scaling_factor), _ptr(logits),
+         _ptr(top_idx), _ptr(gates), _stream())
+    return logits, top_idx, gates
+
+
+def router_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int,
+                       mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0):
+    """Top-k indices and gates from given float32 logits [T,N]."""
+    _check(logits, "logits", 2)
+    if logits.dtype != torch.float32:
+        raise TypeError("logits must be float32")
+    T, N = logits.shape
+    if bias is not None:
+        _check(bias, "bias", 1)
+        if bias.dtype != torch.float32 or bias.shape[0] != N:
+            raise ValueError("bias must be float32 [n_experts]")
+    top_idx = torch.empty((T, top_k), dtype=torch.int32, device=logits.device)
+    gates = torch.empty((T, top_k), dtype=torch.float32, device=logits.device)
+    call("hmoe_router_from_logits", _ptr(logits), _ptr(bias), T, N, top_k, mode,
+         float(routed_scaling_factor), _ptr(top_idx), _ptr(gates), _stream())
+    return top_idx, gates
+
+
+# ---------------------------------------------------------- dispatch plan --
+
+@dataclass
+class Plan:
+    """Dispatch plan of one call (see ``hmoe_dispatch_plan``)."""
+    counts: torch.Tensor    # [N] int32, pre-drop histogram (bincount)
+    offsets: torch.Tensor   # [N+1] int32, kept-row segment starts
+    slot_pos: torch.Tensor  # [T*K] int32, dispatched row of slot i or -1
+    perm_src: torch.Tensor  # [rows_cap] int32, slot of row j or -1
+    keep: torch.Tensor      # [T*K] uint8
+    capacity: int
+    rows_cap: int
+    n_experts: int
+    top_k: int
+
+
+def dispatch_plan(top_idx: torch.Tensor, n_experts: int, cap: int,
+                  workspace: torch.Tensor | None = None) -> Plan:
+    """Stable expert-grouped permutation with capacity drops (``moe.py:54-57,80``)."""
+    _check(top_idx, "top_idx", 2)
+    if top_idx.dtype != torch.int32:
+        raise TypeError("top_idx must be int32")
+    T, K = top_idx.shape
+    dev = top_idx.device
+    rc = rows_cap(T, K, n_experts, cap)
+    ws_bytes = int(_lib.lib().hmoe_plan_workspace_bytes(T, K, n_experts))
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    slot_pos = torch.empty(T * K, dtype=torch.int32, device=dev)
+    perm_src = torch.empty(rc, dtype=torch.int32, device=dev)
+    keep = torch.empty(T * K, dtype=torch.uint8, device=dev)
+    call("hmoe_dispatch_plan", _ptr(top_idx), T, K, n_experts, cap, _ptr(counts), _ptr(offsets),
+         _ptr(slot_pos), _ptr(perm_src), _ptr(keep), _ptr(workspace), workspace.numel(),
+         _stream())
+    return Plan(counts, offsets, slot_pos, perm_src, keep, cap, rc, n_experts, K)
+
+
+def permute_rows(x: torch.Tensor, plan: Plan, out_dtype: torch.dtype = torch.bfloat16):
+    """Dispatched rows ``xs [rows_cap, D]`` (``moe.py:56,198``); token-centric."""
+    _check(x, "x", 2)
+    T, D = x.shape
+    if plan.slot_pos.numel() != T * plan.top_k:
+        raise ValueError("plan does not match x's token count")
+    xs = torch.empty((plan.rows_cap, D), dtype=out_dtype, device=x.device)
+    call("hmoe_permute_rows", _ptr(x), _dtype_code(x), T, D, plan.top_k, _ptr(plan.slot_pos),
+         _ptr(xs), _DT[out_dtype], _stream())
+    return xs
+
+
+# ---------------------------------------------------------------- weights --
+
+def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """bf16 gate/up operand [N, 2F, D] from ``[N,D,F]`` masters (``moe.py:204-205``)."""
+    _check(w_gate, "w_gate", 3)
+    _check(w_up, "w_up", 3)
+    if w_gate.shape != w_up.shape or w_gate.dtype != w_up.dtype:
+        raise ValueError("w_gate and w_up must have the same shape and dtype")
+    N, D, F = w_gate.shape
+    out = torch.empty((N, 2 * F, D), dtype=torch.bfloat16, device=w_gate.device)
+    call("hmoe_pack_gate_up", _ptr(w_gate), _ptr(w_up), _dtype_code(w_gate), N, D, F, _ptr(out),
+         _stream())
+    return out
+
+
+def pack_down(w_down: torch.Tensor) -> torch.Tensor:
+    """bf16 down operand [N, D, F] from the ``[N,F,D]`` master (``moe.py:206``)."""
+    _check(w_down, "w_down", 3)
+    N, F, D = w_down.shape
+    out = torch.empty((N, D, F), dtype=torch.bfloat16, device=w_down.device)
+    call("hmoe_pack_down", _ptr(w_down), _dtype_code(w_down), N, F, D, _ptr(out), _stream())
+    return out
+
+
+# ------------------------------------------------------------ grouped GEMM --
+
+def grouped_gate_up(xs: torch.Tensor, offsets: torch.Tensor, w_gate_up: torch.Tensor,
+                    rows: int | None = None) -> torch.Tensor:
+    """``h = bf16(silu(xs Wg) * (xs Wu))`` per expert segment (``moe.py:70-72``)."""
+    _check(xs, "xs", 2)
+    _check(offsets, "offsets", 1)
+    _check(w_gate_up, "w_gate_up", 3)
+    if xs.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16:
+        raise TypeError("grouped_gate_up takes bf16 operands")
+    N, F2, D = w_gate_up.shape
+    if xs.shape[1] != D or offsets.numel() != N + 1 or offsets.dtype != torch.int32:
+        raise ValueError("grouped_gate_up: inconsistent shapes")
+    R = xs.shape[0] if rows is None else rows
+    h = torch.empty((xs.shape[0], F2 // 2), dtype=torch.bfloat16, device=xs.device)
+    call("hmoe_grouped_gate_up", _ptr(xs), _ptr(offsets), N, R, D, F2 // 2, _ptr(w_gate_up),
+         _ptr(h), _stream())
+    return h
+
+
+def grouped_down(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor,
+                 rows: int | None = None) -> torch.Tensor:
+    """``ys = bf16(h Wd)`` per expert segment (``moe.py:73-74``)."""
+    _check(h, "h", 2)
+    _check(offsets, "offsets", 1)
+    _check(w_down, "w_down", 3)
+    if h.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:
+        raise TypeError("grouped_down takes bf16 operands")
+    N, D, F = w_down.shape
+    if h.shape[1] != F or offsets.numel() != N + 1 or offsets.dtype != torch.int32:
+        raise ValueError("grouped_down: inconsistent shapes")
+    R = h.shape[0] if rows is None else rows
+    ys = torch.empty((h.shape[0], D), dtype=torch.bfloat16, device=h.device)
+    call("hmoe_grouped_down", _ptr(h), _ptr(offsets), N, R, F, D, _ptr(w_down), _ptr(ys),
+         _stream())
+    return ys
+
+
+# ---------------------------------------------------------------- combine --
+
+def combine(ys: torch.Tensor, plan: Plan, gates: torch.Tensor,
+            residual: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32):
+    """``y[t] = sum_k bf16(g[t,k]) ys[slot_pos[t,k]] (+ residual)`` (``moe.py:80-85``)."""
+    _check(ys, "ys", 2)
+    _check(gates, "gates", 2)
+    T, K = gates.shape
+    if gates.dtype != torch.float32 or K != plan.top_k or plan.slot_pos.numel() != T * K:
+        raise ValueError("combine: gates must be float32 [T, K] matching the plan")
+    D = ys.shape[1]
+    if residual is not None:
+        _check(residual, "residual", 2)
+        if tuple(residual.shape) != (T, D):
+            raise ValueError("combine: residual must be [T, D]")
+    out = torch.empty((T, D), dtype=out_dtype, device=ys.device)
+    call("hmoe_combine", _ptr(ys), _dtype_code(ys), _ptr(plan.slot_pos), _ptr(gates),
+         _ptr(residual), _DT[residual.dtype] if residual is not None else _lib.F32, T, K, D,
+         _ptr(out), _DT[out_dtype], _stream())
+    return out
+
+
+# -------------------------------------------------------------------- aux --
+
+def router_aux(logits: torch.Tensor, top_idx: torch.Tensor, batch: int, seq: int):
+    """Aux outputs (``moe.py:253-292``): (losses f32 [3] = z, balance, entropy;
+    expert_counts f32 [N])."""
+    _check(logits, "logits", 2)
+    _check(top_idx, "top_idx", 2)
+    T, N = logits.shape
+    if T != batch * seq or top_idx.shape[0] != T:
+        raise ValueError("router_aux: logits/top_idx must hold batch*seq tokens")
+    dev = logits.device
+    ws = int(_lib.lib().hmoe_aux_workspace_bytes(batch, seq, N))
+    work = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
+    losses = torch.empty(3, dtype=torch.float32, device=dev)
+    counts = torch.empty(N, dtype=torch.float32, device=dev)
+    call("hmoe_router_aux", _ptr(logits), _ptr(top_idx), batch, seq, N, top_idx.shape[1],
+         _ptr(losses), _ptr(counts), _ptr(work), work.numel(), _stream())
+    return losses, counts

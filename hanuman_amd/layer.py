@@ -1,0 +1,71 @@
+"""Device-resident MoE-layer forward for the measured workloads.
+
+``DeviceLayer`` uploads one workload's inputs, packs its expert weights once
+and runs the layer (router -> plan -> permute -> grouped SwiGLU -> combine)
+entirely through ``libhanuman_moe.so``; ``forward`` is the step ``bench.py``
+times and the GPU tests check.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from . import kernels as K
+from .workloads import Inputs, Workload
+
+_TORCH_DT = {"bf16": torch.bfloat16, "f32": torch.float32}
+
+
+class DeviceLayer:
+    def __init__(self, inp: Inputs, device: str | torch.device = "cuda"):
+        wl: Workload = inp.wl
+        if wl.expert_dtype != "bf16":
+            raise NotImplementedError(f"{wl.name}: expert dtype {wl.expert_dtype} is not built yet")
+        self.wl = wl
+        dev = torch.device(device)
+        self.device = dev
+        self.x = torch.from_numpy(inp.x).to(dev, _TORCH_DT[wl.x_dtype]).contiguous()
+        self.logits_in = None
+        self.router_w = None
+        if wl.router_from_logits:
+            self.logits_in = torch.from_numpy(inp.logits).to(dev).contiguous()
+        else:
+            self.router_w = torch.from_numpy(inp.router).to(dev, _TORCH_DT[wl.router_w_dtype]).contiguous()
+        self.mode = _lib.ROUTE_SOFTMAX if wl.routing == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+        self.capacity = wl.capacity
+        self.w_gate_up = None
+        self.w_down = None
+        if wl.expert == "swiglu":
+            wg = torch.from_numpy(inp.w_gate).to(dev)
+            wu = torch.from_numpy(inp.w_up).to(dev)
+            self.w_gate_up = K.pack_gate_up(wg, wu)
+            del wg, wu
+            wd = torch.from_numpy(inp.w_down).to(dev)
+            self.w_down = K.pack_down(wd)
+            del wd
+        ws = int(_lib.lib().hmoe_plan_workspace_bytes(wl.tokens, wl.top_k, wl.n_experts))
+        self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
+        self.out_dtype = _TORCH_DT[wl.out_dtype]
+
+    # ---- stages (each enqueues on the current stream) ----------------------
+    def route(self):
+        wl = self.wl
+        if self.logits_in is not None:
+            top_idx, gates = K.router_from_logits(self.logits_in, None, wl.top_k, self.mode)
+            return self.logits_in, top_idx, gates
+        return K.router(self.x, self.router_w, None, wl.top_k, self.mode)
+
+    def forward(self) -> dict:
+        wl = self.wl
+        logits, top_idx, gates = self.route()
+        plan = K.dispatch_plan(top_idx, wl.n_experts, self.capacity, self.workspace)
+        xs = K.permute_rows(self.x, plan, torch.bfloat16)
+        h = None
+        if wl.expert == "identity":
+            ys = xs
+        else:
+            h = K.grouped_gate_up(xs, plan.offsets, self.w_gate_up)
+            ys = K.grouped_down(h, plan.offsets, self.w_down)
+        out = K.combine(ys, plan, gates, None, self.out_dtype)
+        return {"logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan, "xs": xs,
+                "h": h, "ys": ys, "out": out}

@@ -1,0 +1,251 @@
+"""Drop-in MoE layer for one MI355X (reference: ``model/moe.py`` of theorionic/hanuman).
+
+``MoE`` keeps the reference constructor signature (``moe.py:126-128``), its
+parameter names -- ``router``, ``bias``, ``expert_w_gate``, ``expert_w_up``,
+``expert_w_down``, ``shared_w_gate``, ``shared_w_up``, ``shared_w_down`` --
+with the same shapes, and its call contract ``x [B,S,D] -> (out [B,S,D] f32,
+aux)`` (``moe.py:170-294``).  Parameters are torch tensors held in ``Param``
+objects (``.value``, like ``nnx.Param``).  Every stage runs in
+``libhanuman_moe.so``; torch only allocates and supplies the stream.
+
+Only the single-device branch exists (``moe.py:216-218``): all experts are
+resident in one GPU's HBM, so ``mesh`` must be None or hold one device.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from . import kernels as K
+
+
+class Param:
+    """Parameter holder with a ``.value`` tensor (the ``nnx.Param`` role)."""
+
+    __slots__ = ("value",)
+
+    def __init__(self, value: torch.Tensor):
+        self.value = value
+
+    def __repr__(self):
+        v = self.value
+        return f"Param(shape={tuple(v.shape)}, dtype={v.dtype}, device={v.device})"
+
+
+def _torch_dtype(dtype) -> torch.dtype:
+    if isinstance(dtype, torch.dtype):
+        return dtype
+    name = getattr(dtype, "name", None) or getattr(dtype, "__name__", None) or str(dtype)
+    name = name.lower().replace("jnp.", "").replace("numpy.", "")
+    if name in ("bfloat16", "bf16"):
+        return torch.bfloat16
+    if name in ("float32", "f32", "fp32"):
+        return torch.float32
+    raise TypeError(f"unsupported compute dtype {dtype!r}")
+
+
+def _generator(rngs, device) -> torch.Generator:
+    if isinstance(rngs, torch.Generator):
+        return rngs
+    if isinstance(rngs, np.random.Generator):
+        seed = int(rngs.integers(0, 2**63 - 1))
+    elif rngs is None:
+        seed = 0
+    else:
+        seed = int(rngs)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def _require_bf16_compute(dtype: torch.dtype):
+    if dtype != torch.bfloat16:
+        raise NotImplementedError(
+            "the grouped expert GEMM computes in bfloat16 (fp32 accumulation); "
+            f"compute dtype {dtype} is not built")
+
+
+class _PackCache:
+    """Packed bf16 operands of fp32 master weights, rebuilt when a master changes."""
+
+    def __init__(self):
+        self._key = None
+        self._val = None
+
+    def get(self, tensors, build):
+        key = tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype) for t in tensors)
+        if key != self._key:
+            self._val = build()
+            self._key = key
+        return self._val
+
+
+def _offsets_one_group(rows: int, device) -> torch.Tensor:
+    return torch.tensor([0, rows], dtype=torch.int32, device=device)
+
+
+def swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+           dtype) -> torch.Tensor:
+    """Dense SwiGLU ``down(silu(x@gate) * (x@up))`` -> float32 (``moe.py:23-29``).
+
+    Runs the grouped GEMMs with one group.  ``x [T,D]``; weights ``[D,F]``,
+    ``[D,F]``, ``[F,D]``.  The output of the down matmul is rounded to the
+    compute dtype and returned as float32, as the reference does.
+    """
+    dt = _torch_dtype(dtype)
+    _require_bf16_compute(dt)
+    xb = x.to(dt).contiguous()
+    T = xb.shape[0]
+    off = _offsets_one_group(T, x.device)
+    wgu = K.pack_gate_up(w_gate.unsqueeze(0).contiguous(), w_up.unsqueeze(0).contiguous())
+    wd = K.pack_down(w_down.unsqueeze(0).contiguous())
+    h = K.grouped_gate_up(xb, off, wgu)
+    return K.grouped_down(h, off, wd).float()
+
+
+def ragged_dispatch(x_flat: torch.Tensor, top_idx: torch.Tensor, weights: torch.Tensor,
+                    w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                    dtype) -> torch.Tensor:
+    """Route each token to its top-k experts and run SwiGLU (``moe.py:37-85``).
+
+    ``x_flat [T,D]`` (compute dtype), ``top_idx [T,K]`` int32, ``weights [T,K]``
+    float32, stacked expert weights ``[N,D,F]``/``[N,F,D]``.  Dropless, stable
+    expert grouping, float32 result ``[T,D]``.
+    """
+    dt = _torch_dtype(dtype)
+    _require_bf16_compute(dt)
+    T, Kk = top_idx.shape
+    N = w_gate.shape[0]
+    plan = K.dispatch_plan(top_idx.to(torch.int32).contiguous(), N, T * Kk)
+    xs = K.permute_rows(x_flat.contiguous(), plan, dt)
+    h = K.grouped_gate_up(xs, plan.offsets, K.pack_gate_up(w_gate, w_up))
+    ys = K.grouped_down(h, plan.offsets, K.pack_down(w_down))
+    return K.combine(ys, plan, weights.float().contiguous(), None, torch.float32)
+
+
+class MoE:
+    """Mixture of Experts with aux-loss-free sigmoid routing (``moe.py:116-294``).
+
+    Reference behaviour by default.  Keyword-only extensions (not in the
+    reference): ``routing="softmax"`` (top-k of softmax, renormalised gates,
+    no bias, no scaling) and ``capacity_factor`` (per-expert capacity
+    ``ceil(CF*T*K/N)`` with token-order priority; ``None`` = dropless).
+    """
+
+    def __init__(self, d_model: int, d_ff: int, n_experts: int, n_active: int,
+                 n_shared_experts: int, router_init_std: float, routed_scaling_factor: float,
+                 dtype, rngs, mesh=None, d_ff_shared: int | None = None, *,
+                 routing: str = "sigmoid", capacity_factor: float | None = None,
+                 device: str | torch.device | None = None):
+        if mesh is not None:
+            size = getattr(getattr(mesh, "devices", None), "size", 1)
+            if size > 1:
+                raise NotImplementedError("one GPU holds every expert; a multi-device mesh is not built")
+        if routing not in ("sigmoid", "softmax"):
+            raise ValueError(f"routing must be 'sigmoid' or 'softmax' (got {routing!r})")
+        dev = torch.device(device) if device is not None else torch.device("cuda")
+        self.mesh = mesh
+        self.expert_axis_name = None
+        self.n_experts = n_experts
+        self.n_active = n_active
+        self.n_shared_experts = n_shared_experts
+        self.routed_scaling_factor = routed_scaling_factor
+        self.dtype = _torch_dtype(dtype)
+        self.routing = routing
+        self.capacity_factor = capacity_factor
+        g = _generator(rngs, dev)
+
+        def normal(shape, std):
+            return torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std
+
+        self.router = Param(normal((d_model, n_experts), router_init_std))
+        self.bias = Param(torch.zeros(n_experts, dtype=torch.float32, device=dev))
+        std = (1.0 / d_model) ** 0.5
+        self.expert_w_gate = Param(normal((n_experts, d_model, d_ff), std))
+        self.expert_w_up = Param(normal((n_experts, d_model, d_ff), std))
+        self.expert_w_down = Param(normal((n_experts, d_ff, d_model), std))
+        dfs = d_ff if d_ff_shared is None else d_ff_shared
+        if n_shared_experts == 1:
+            self.shared_w_gate = Param(normal((d_model, dfs), std))
+            self.shared_w_up = Param(normal((d_model, dfs), std))
+            self.shared_w_down = Param(normal((dfs, d_model), std))
+        else:
+            self.shared_w_gate = Param(normal((n_shared_experts, d_model, dfs), std))
+            self.shared_w_up = Param(normal((n_shared_experts, d_model, dfs), std))
+            self.shared_w_down = Param(normal((n_shared_experts, dfs, d_model), std))
+        self._routed_pack = _PackCache()
+        self._shared_pack = _PackCache()
+
+    # ---- parameters ------------------------------------------------------
+    def named_params(self) -> dict:
+        """Parameter pytree paths -> Param, in reference attribute order."""
+        names = ("router", "bias", "expert_w_gate", "expert_w_up", "expert_w_down",
+                 "shared_w_gate", "shared_w_up", "shared_w_down")
+        return {n: getattr(self, n) for n in names}
+
+    def _packed_routed(self):
+        wg, wu, wd = self.expert_w_gate.value, self.expert_w_up.value, self.expert_w_down.value
+        return self._routed_pack.get((wg, wu, wd), lambda: (K.pack_gate_up(wg, wu), K.pack_down(wd)))
+
+    def _packed_shared(self):
+        wg, wu, wd = self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value
+
+        def build():
+            if self.n_shared_experts == 1:
+                return [(K.pack_gate_up(wg.unsqueeze(0).contiguous(), wu.unsqueeze(0).contiguous()),
+                         K.pack_down(wd.unsqueeze(0).contiguous()))]
+            return [(K.pack_gate_up(wg[i:i + 1].contiguous(), wu[i:i + 1].contiguous()),
+                     K.pack_down(wd[i:i + 1].contiguous())) for i in range(self.n_shared_experts)]
+        return self._shared_pack.get((wg, wu, wd), build)
+
+    # ---- forward -----------------------------------------------------------
+    def _shared_ffn(self, x_flat: torch.Tensor) -> torch.Tensor:
+        """Shared expert(s) (``moe.py:161-168``): bf16 output of one expert, or
+        the float32 mean over ``n_shared_experts``."""
+        if self.n_shared_experts == 0:
+            return 0.0 / self.n_shared_experts  # ZeroDivisionError, as the reference
+        T = x_flat.shape[0]
+        off = _offsets_one_group(T, x_flat.device)
+        outs = []
+        for wgu, wd in self._packed_shared():
+            h = K.grouped_gate_up(x_flat, off, wgu)
+            outs.append(K.grouped_down(h, off, wd))
+        if len(outs) == 1:
+            return outs[0]
+        acc = torch.zeros_like(outs[0], dtype=torch.float32)
+        for o in outs:
+            acc += o.float()
+        return acc / self.n_shared_experts
+
+    def __call__(self, x: torch.Tensor):
+        """``x [B,S,D]`` -> (``out [B,S,D]`` float32, aux dict)."""
+        _require_bf16_compute(self.dtype)
+        if x.dim() != 3:
+            raise ValueError(f"x must be [B, S, d_model] (got {tuple(x.shape)})")
+        B, S, D = x.shape
+        N, Kk = self.n_experts, self.n_active
+        T = B * S
+        x2 = x.reshape(T, D).contiguous()
+        mode = _lib.ROUTE_SIGMOID_BIAS if self.routing == "sigmoid" else _lib.ROUTE_SOFTMAX
+        rsf = self.routed_scaling_factor if self.routing == "sigmoid" else 1.0
+        bias = self.bias.value if self.routing == "sigmoid" else None
+        logits, top_idx, gates = K.router(x2, self.router.value.float().contiguous(),
+                                          bias, Kk, mode, rsf)
+        cap = K.capacity(T, Kk, N, self.capacity_factor)
+        plan = K.dispatch_plan(top_idx, N, cap)
+        xs = K.permute_rows(x2, plan, self.dtype)
+        wgu, wd = self._packed_routed()
+        h = K.grouped_gate_up(xs, plan.offsets, wgu)
+        ys = K.grouped_down(h, plan.offsets, wd)
+        xc = x2 if x2.dtype == self.dtype else x2.to(self.dtype)
+        shared = self._shared_ffn(xc)
+        out = K.combine(ys, plan, gates, shared, torch.float32)
+        losses, counts = K.router_aux(logits, top_idx, B, S)
+        aux = {
+            "router_z_loss": losses[0],
+            "balance_loss": losses[1],
+            "mean_entropy": losses[2],
+            "expert_counts": counts,
+        }
+        return out.reshape(B, S, D), aux

@@ -1,0 +1,173 @@
+/*
+ * hanuman_moe.h -- C ABI of the MI355X (gfx950) MoE-layer forward.
+ *
+ * The reference layer is `MoE.__call__` in model/moe.py:170-294 of
+ * theorionic/hanuman (JAX).  Its stages map onto the entry points below; each
+ * declaration cites the reference lines it replaces.  A jax.ffi handler (or a
+ * ctypes binding) forwards XLA/torch-owned device buffers to these calls.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless noted.  The library never
+ *     allocates device memory: callers pass outputs and workspace.
+ *   - Every call enqueues work on `stream` (a hipStream_t; NULL = the legacy
+ *     default stream) and returns without synchronising.
+ *   - Return value: HMOE_OK (0) or an HMOE_ERR_* code; hmoe_last_error()
+ *     gives a message for the calling thread.  No call aborts the process.
+ *   - T tokens, D d_model, N experts, K top-k, F d_ff, C capacity per expert,
+ *     R = T*K (token, slot) pairs; flat slot index i = t*K + k.
+ *   - Results are deterministic: no atomics decide any output value.
+ */
+#ifndef HANUMAN_MOE_H
+#define HANUMAN_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* hmoe_stream_t; /* hipStream_t */
+
+enum {
+  HMOE_OK = 0,
+  HMOE_ERR_INVALID = 1,     /* bad argument (shape, dtype, null pointer)   */
+  HMOE_ERR_UNSUPPORTED = 2, /* valid but not supported by this build       */
+  HMOE_ERR_HIP = 3,         /* HIP runtime error (launch, attribute)       */
+  HMOE_ERR_WORKSPACE = 4    /* workspace too small                         */
+};
+
+enum { HMOE_F32 = 0, HMOE_BF16 = 1, HMOE_FP8_E4M3 = 2 };
+
+enum {
+  HMOE_ROUTE_SIGMOID_BIAS = 0, /* moe.py:179-192: top-k of sigmoid(l)+bias,
+                                  gates sel/(sum sel + 1e-9) * rsf          */
+  HMOE_ROUTE_SOFTMAX = 1       /* top-k of softmax(l), gates renormalised   */
+};
+
+/* Row tile of the grouped GEMM (a tile's reads past the buffer are clamped to
+ * its last row, so dispatched buffers hold exactly rows_cap rows). */
+#define HMOE_GEMM_TILE_M 256
+
+/* ---- library --------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* hmoe_last_error(void);
+/* ABI version of this header (bumped on incompatible change). */
+int hmoe_abi_version(void);
+
+/* ---- sizes ------------------------------------------------------------ */
+
+/* Capacity per expert: ceil(capacity_factor * T * K / N); a factor <= 0 means
+ * dropless (C = T*K, the reference's behaviour, moe.py:54-65). */
+int64_t hmoe_capacity(int64_t tokens, int top_k, int n_experts, double capacity_factor);
+/* Static bound on kept rows: min(T*K, N*C) (moe.py:59-65 pads to a multiple
+ * of 128 instead; rows past the kept total are never read). */
+int64_t hmoe_rows_cap(int64_t tokens, int top_k, int n_experts, int64_t capacity);
+/* Workspace bytes needed by hmoe_dispatch_plan. */
+size_t hmoe_plan_workspace_bytes(int64_t tokens, int top_k, int n_experts);
+
+/* ---- router: moe.py:175-192 (replaces `x_f @ router`, `sigmoid`, `+bias`,
+ *      `lax.top_k`, `take_along_axis`, the gate normalisation) ------------ */
+
+/* x [T,D] (HMOE_F32 or HMOE_BF16), router_w [D,N] (HMOE_F32 or HMOE_BF16),
+ * bias [N] f32 (may be NULL = zeros; used by HMOE_ROUTE_SIGMOID_BIAS only).
+ * Outputs: logits [T,N] f32 (fp32 rounding of a float64 d-ascending sum),
+ * top_idx [T,K] int32 (descending key, lower index first on ties), gates
+ * [T,K] f32.  N <= 256, K <= min(N, 32). */
+int hmoe_router(const void* x, int x_dtype, const void* router_w, int w_dtype,
+                const float* bias, int64_t tokens, int d_model, int n_experts,
+                int top_k, int mode, float routed_scaling_factor, float* logits,
+                int32_t* top_idx, float* gates, hmoe_stream_t stream);
+
+/* Same selection and gates from precomputed logits [T,N] f32 (moe.py:179-192
+ * applied to given `gate_logits`). */
+int hmoe_router_from_logits(const float* logits, const float* bias, int64_t tokens,
+                            int n_experts, int top_k, int mode,
+                            float routed_scaling_factor, int32_t* top_idx,
+                            float* gates, hmoe_stream_t stream);
+
+/* ---- dispatch plan: moe.py:54-57,80 (replaces `argsort(slot_expert)`,
+ *      `bincount`, `argsort(order)`) plus the capacity drop --------------- */
+
+/* top_idx [T,K] int32 in [0,N).  Outputs:
+ *   counts   [N]        rows routed to each expert before drops (bincount)
+ *   offsets  [N+1]      exclusive scan of min(counts, C): kept-row segments
+ *   slot_pos [T*K]      dispatched row of slot i, or -1 if dropped (= inv)
+ *   perm_src [rows_cap] slot i of dispatched row j (= order), -1 past the end
+ *   keep     [T*K]      1 if slot i is kept (rank within its expert < C)
+ * Stable: within an expert, rows keep ascending i. */
+int hmoe_dispatch_plan(const int32_t* top_idx, int64_t tokens, int top_k,
+                       int n_experts, int64_t capacity, int32_t* counts,
+                       int32_t* offsets, int32_t* slot_pos, int32_t* perm_src,
+                       uint8_t* keep, void* workspace, size_t workspace_bytes,
+                       hmoe_stream_t stream);
+
+/* ---- row permutation: moe.py:56,198 (replaces `x.astype(dtype)` and
+ *      `x_flat[order // K]`) ------------------------------------------------ */
+
+/* xs[slot_pos[t*K+k]] = cast(x[t]) for kept slots; each token row is read
+ * once.  x [T,D] (F32/BF16), xs [rows_cap, D] (F32/BF16). D % 8 == 0. */
+int hmoe_permute_rows(const void* x, int x_dtype, int64_t tokens, int d_model,
+                      int top_k, const int32_t* slot_pos, void* xs, int xs_dtype,
+                      hmoe_stream_t stream);
+
+/* ---- expert weights: moe.py:204-206 (replaces the per-call `.astype(dtype)`
+ *      of the stacked fp32 masters) ---------------------------------------- */
+
+/* Packs expert_w_gate/expert_w_up [N,D,F] (F32/BF16) into the bf16 gate/up
+ * operand [N][2F][D]: packed row p holds column h = (p/64)*32 + p%32 of the
+ * gate (p%64 < 32) or up (p%64 >= 32) weight, D contiguous.  F % 128 == 0. */
+size_t hmoe_packed_gate_up_bytes(int n_experts, int d_model, int d_ff);
+int hmoe_pack_gate_up(const void* w_gate, const void* w_up, int w_dtype,
+                      int n_experts, int d_model, int d_ff, void* packed,
+                      hmoe_stream_t stream);
+/* Packs expert_w_down [N,F,D] into bf16 [N][D][F] (F contiguous). */
+size_t hmoe_packed_down_bytes(int n_experts, int d_ff, int d_model);
+int hmoe_pack_down(const void* w_down, int w_dtype, int n_experts, int d_ff,
+                   int d_model, void* packed, hmoe_stream_t stream);
+
+/* ---- grouped expert GEMMs: moe.py:67-74 (replaces the three
+ *      `jax.lax.ragged_dot` calls and the SwiGLU between them) ------------- */
+
+/* h[r, :] = bf16( silu(xs[r]·Wg[e]) * (xs[r]·Wu[e]) ) for rows r of expert e's
+ * segment [offsets[e], offsets[e+1]).  xs [rows_cap, D] bf16, packed gate/up
+ * from hmoe_pack_gate_up, h [rows_cap, F] bf16.  fp32 accumulation.
+ * D % 256 == 0, F % 128 == 0, N <= 1024. */
+int hmoe_grouped_gate_up(const void* xs, const int32_t* offsets, int n_experts,
+                         int64_t rows_cap, int d_model, int d_ff,
+                         const void* w_gate_up_packed, void* h, hmoe_stream_t stream);
+
+/* ys[r, :] = bf16( h[r]·Wd[e] ) per expert segment.  h [rows_cap, F] bf16,
+ * packed down from hmoe_pack_down, ys [rows_cap, D] bf16. */
+int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
+                      int64_t rows_cap, int d_ff, int d_model,
+                      const void* w_down_packed, void* ys, hmoe_stream_t stream);
+
+/* ---- combine: moe.py:80-85 (replaces `ys[inv]` and the weighted einsum) - */
+
+/* out[t] = sum_k bf16(gates[t,k]) * ys[slot_pos[t*K+k]] (+ residual[t]),
+ * float32 accumulation over k ascending, dropped slots skipped.
+ * ys [rows, D] (BF16/F32); residual [T,D] (F32/BF16) or NULL: the shared
+ * expert's output, added last (moe.py:249-251); out [T,D] (F32/BF16). */
+int hmoe_combine(const void* ys, int ys_dtype, const int32_t* slot_pos,
+                 const float* gates, const void* residual, int residual_dtype,
+                 int64_t tokens, int top_k, int d_model, void* out, int out_dtype,
+                 hmoe_stream_t stream);
+
+/* ---- aux outputs: moe.py:253-292 (replaces logsumexp, the per-sequence
+ *      bincount, the balance loss, the entropy diagnostic) ---------------- */
+
+/* logits [B*S, N] f32 and top_idx [B*S, K] of B sequences of S tokens.
+ * losses[3] = {router_z_loss, balance_loss, mean_entropy}; expert_counts [N]
+ * f32 (integer valued, = counts of hmoe_dispatch_plan).  N <= 256,
+ * B <= 1024.  Scores are the router's sigmoid (moe.py:179). */
+size_t hmoe_aux_workspace_bytes(int batch, int seq, int n_experts);
+int hmoe_router_aux(const float* logits, const int32_t* top_idx, int batch, int seq,
+                    int n_experts, int top_k, float* losses, float* expert_counts,
+                    void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HANUMAN_MOE_H */

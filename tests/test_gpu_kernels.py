@@ -1,0 +1,297 @@
+"""Per-kernel parity of the HIP path against the oracle (needs an MI355X).
+
+Integer outputs (top-k indices, counts, offsets, permutation, drop mask) and
+every float32 value the contract fixes bit for bit (router logits, gates,
+combine sums) are compared exactly; the grouped GEMM against float64 on the
+same bf16 operands with a stated tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from hanuman_amd import _lib
+from hanuman_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_f32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def dev_bf16(a, dev):
+    return dev_f32(a, dev).to(torch.bfloat16)
+
+
+def host(t):
+    if t.dtype == torch.bfloat16:
+        return t.float().cpu().numpy()
+    return t.cpu().numpy()
+
+
+def assert_bits_equal(got, ref, what):
+    got = np.ascontiguousarray(got)
+    ref = np.ascontiguousarray(ref)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    if got.dtype == np.float32:
+        bad = got.view(np.uint32) != ref.view(np.uint32)
+    else:
+        bad = got != ref
+    n = int(bad.sum())
+    assert n == 0, f"{what}: {n} of {bad.size} elements differ; first at {np.argwhere(bad)[:5].tolist()}"
+
+
+# ------------------------------------------------------------------- router --
+
+ROUTER_CASES = [
+    # T, D, N, K, x_dtype, w_dtype, mode, rsf, bias
+    (2048, 256, 8, 2, "f32", "f32", "softmax", 1.0, False),
+    (1024, 2048, 64, 8, "bf16", "f32", "softmax", 1.0, False),
+    (777, 2048, 128, 8, "bf16", "f32", "softmax", 1.0, False),
+    (300, 512, 200, 6, "bf16", "f32", "sigmoid", 2.5, True),
+    (256, 4096, 32, 4, "bf16", "bf16", "softmax", 1.0, False),
+    (129, 1536, 80, 8, "bf16", "f32", "sigmoid", 2.5, True),
+]
+
+
+@pytest.mark.parametrize("case", ROUTER_CASES, ids=lambda c: f"T{c[0]}_D{c[1]}_N{c[2]}_K{c[3]}_{c[6]}")
+def test_router_bit_exact(gpu, case):
+    T, D, N, Kk, xd, wd, mode, rsf, with_bias = case
+    print(f"router case {case}", flush=True)
+    rng = np.random.default_rng(T + D + N)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    if xd == "bf16":
+        x = O.bf16_round(x)
+    w = (0.02 * rng.standard_normal((D, N))).astype(np.float32)
+    if wd == "bf16":
+        w = O.bf16_round(w)
+    bias = (0.05 * rng.standard_normal(N)).astype(np.float32) if with_bias else None
+    logits_ref = O.router_logits(x, w)
+    if mode == "softmax":
+        idx_ref, g_ref = O.route_softmax(logits_ref, Kk)
+    else:
+        idx_ref, g_ref, _ = O.route_sigmoid(logits_ref, bias, Kk, rsf)
+    xt = dev_bf16(x, gpu) if xd == "bf16" else dev_f32(x, gpu)
+    wt = dev_bf16(w, gpu) if wd == "bf16" else dev_f32(w, gpu)
+    bt = dev_f32(bias, gpu) if bias is not None else None
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    logits, idx, g = K.router(xt, wt, bt, Kk, m, rsf)
+    torch.cuda.synchronize()
+    assert_bits_equal(host(logits), logits_ref, "logits")
+    assert_bits_equal(host(idx), idx_ref, "top_idx")
+    assert_bits_equal(host(g), g_ref, "gates")
+
+
+def test_router_from_logits_ties_and_signed_zero(gpu):
+    rng = np.random.default_rng(21)
+    T, N, Kk = 512, 64, 8
+    logits = rng.integers(-3, 4, size=(T, N)).astype(np.float32)   # many exact ties
+    logits[0] = 0.0
+    logits[0, 10:20] = -0.0
+    logits[1] = 1.0
+    for mode in (_lib.ROUTE_SOFTMAX, _lib.ROUTE_SIGMOID_BIAS):
+        bias = np.zeros(N, np.float32) if mode == _lib.ROUTE_SIGMOID_BIAS else None
+        if mode == _lib.ROUTE_SOFTMAX:
+            idx_ref, g_ref = O.route_softmax(logits, Kk)
+        else:
+            idx_ref, g_ref, _ = O.route_sigmoid(logits, bias, Kk, 2.5)
+        idx, g = K.router_from_logits(dev_f32(logits, gpu),
+                                      dev_f32(bias, gpu) if bias is not None else None, Kk, mode, 2.5)
+        torch.cuda.synchronize()
+        assert_bits_equal(host(idx), idx_ref, f"top_idx mode {mode}")
+        assert_bits_equal(host(g), g_ref, f"gates mode {mode}")
+    assert host(idx)[1].tolist() == list(range(Kk))      # all equal -> lowest indices
+
+
+def test_router_from_logits_dispatch_workload_full_size(gpu):
+    rng = np.random.default_rng(0)
+    T, N, Kk = 32768, 64, 8
+    logits = rng.standard_normal((T, N), dtype=np.float32)
+    idx_ref, g_ref = O.route_softmax(logits, Kk)
+    idx, g = K.router_from_logits(dev_f32(logits, gpu), None, Kk, _lib.ROUTE_SOFTMAX)
+    torch.cuda.synchronize()
+    assert_bits_equal(host(idx), idx_ref, "top_idx")
+    assert_bits_equal(host(g), g_ref, "gates")
+
+
+# -------------------------------------------------------------------- plan --
+
+def _skewed_top_idx(rng, T, K, N):
+    logits = rng.standard_normal((T, N), dtype=np.float32)
+    ranks = rng.permutation(N) + 1
+    logits += (3.0 * ranks.astype(np.float64) ** -1.1).astype(np.float32)
+    return O.topk_desc(logits, K)
+
+
+PLAN_CASES = [
+    # name, T, K, N, capacity factor (None = dropless)
+    ("dispatch_full", 32768, 8, 64, 1.0),
+    ("skewed_full", 65536, 8, 128, 1.25),
+    ("dropless", 4096, 8, 64, None),
+    ("tiny", 3, 2, 5, None),
+    ("cap1", 1000, 4, 16, 0.001),
+    ("one_expert", 700, 1, 1, 0.5),
+    ("ragged_blocks", 4097, 3, 1000, 1.0),
+]
+
+
+@pytest.mark.parametrize("case", PLAN_CASES, ids=lambda c: c[0])
+def test_dispatch_plan_bit_exact(gpu, case):
+    name, T, Kk, N, cf = case
+    print(f"plan case {case}", flush=True)
+    rng = np.random.default_rng(T * 7 + N)
+    if name == "skewed_full":
+        top = _skewed_top_idx(rng, T, Kk, N)
+    else:
+        top = np.stack([rng.permutation(N)[:Kk] if N >= Kk else rng.integers(0, N, Kk)
+                        for _ in range(T)]).astype(np.int32) if T <= 5000 else \
+            O.topk_desc(rng.standard_normal((T, N), dtype=np.float32), Kk)
+    C = O.capacity_of(T, Kk, N, cf)
+    ref = O.dispatch_plan(top, N, C)
+    cap = K.capacity(T, Kk, N, cf)
+    assert cap == C
+    plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, cap)
+    torch.cuda.synchronize()
+    assert plan.rows_cap == O.rows_cap_of(T, Kk, N, C)
+    for k in ("counts", "offsets", "slot_pos", "perm_src", "keep"):
+        assert_bits_equal(host(getattr(plan, k)), ref[k], k)
+
+
+def test_dispatch_plan_is_deterministic(gpu):
+    rng = np.random.default_rng(5)
+    top = torch.from_numpy(O.topk_desc(rng.standard_normal((16384, 64), dtype=np.float32), 8)).to(gpu)
+    a = K.dispatch_plan(top, 64, 2560)
+    b = K.dispatch_plan(top, 64, 2560)
+    torch.cuda.synchronize()
+    for k in ("counts", "offsets", "slot_pos", "perm_src", "keep"):
+        assert torch.equal(getattr(a, k), getattr(b, k)), k
+
+
+# ------------------------------------------------------------- permutation --
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_permute_rows_bit_exact(gpu, xdt):
+    rng = np.random.default_rng(30)
+    T, D, N, Kk = 3000, 2048, 64, 8
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    if xdt == "bf16":
+        x = O.bf16_round(x)
+    top = O.topk_desc(rng.standard_normal((T, N), dtype=np.float32), Kk)
+    C = O.capacity_of(T, Kk, N, 1.0)
+    ref = O.dispatch_plan(top, N, C)
+    xs_ref = O.permute_rows(O.bf16_round(x), ref["perm_src"], Kk)
+    xt = dev_bf16(x, gpu) if xdt == "bf16" else dev_f32(x, gpu)
+    plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, C)
+    xs = K.permute_rows(xt, plan, torch.bfloat16)
+    torch.cuda.synchronize()
+    total = int(ref["offsets"][-1])
+    assert_bits_equal(host(xs)[:total], xs_ref[:total], "xs")
+
+
+# ----------------------------------------------------------------- combine --
+
+@pytest.mark.parametrize("residual", [None, "bf16", "f32"])
+@pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
+def test_combine_bit_exact(gpu, residual, out_dtype):
+    rng = np.random.default_rng(40)
+    T, D, N, Kk = 2000, 1024, 32, 4
+    top = O.topk_desc(rng.standard_normal((T, N), dtype=np.float32), Kk)
+    C = O.capacity_of(T, Kk, N, 1.0)
+    ref = O.dispatch_plan(top, N, C)
+    rows = int(ref["offsets"][-1])
+    ys = O.bf16_round(rng.standard_normal((O.rows_cap_of(T, Kk, N, C), D)).astype(np.float32))
+    g = rng.random((T, Kk)).astype(np.float32)
+    res = None
+    if residual == "bf16":
+        res = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    elif residual == "f32":
+        res = rng.standard_normal((T, D)).astype(np.float32)
+    out_ref = O.combine(ys[:max(rows, 1)], ref["slot_pos"], g, T, Kk, residual=res)
+    plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, C)
+    rt = None if res is None else (dev_bf16(res, gpu) if residual == "bf16" else dev_f32(res, gpu))
+    out = K.combine(dev_bf16(ys, gpu), plan, dev_f32(g, gpu), rt,
+                    torch.float32 if out_dtype == "f32" else torch.bfloat16)
+    torch.cuda.synchronize()
+    if out_dtype == "bf16":
+        out_ref = O.bf16_round(out_ref)
+    assert_bits_equal(host(out), out_ref, "combine")
+
+
+# ------------------------------------------------------------- pack + GEMM --
+
+def test_pack_layouts(gpu):
+    rng = np.random.default_rng(50)
+    N, D, F = 3, 256, 384
+    wg, wu = rng.standard_normal((2, N, D, F)).astype(np.float32)
+    wd = rng.standard_normal((N, F, D)).astype(np.float32)
+    pgu = host(K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu)))
+    pd = host(K.pack_down(dev_f32(wd, gpu)))
+    torch.cuda.synchronize()
+    p = np.arange(2 * F)
+    col = (p // 64) * 32 + p % 32
+    is_up = (p % 64) >= 32
+    exp_gu = np.where(is_up[None, :, None], np.transpose(wu, (0, 2, 1))[:, col],
+                      np.transpose(wg, (0, 2, 1))[:, col])
+    assert_bits_equal(pgu, O.bf16_round(exp_gu), "packed gate/up")
+    assert_bits_equal(pd, O.bf16_round(np.transpose(wd, (0, 2, 1))), "packed down")
+
+
+GEMM_CASES = [
+    # name, D, F, segment sizes
+    ("ragged", 256, 128, [0, 1, 255, 256, 257, 600, 0, 31]),
+    ("wide", 2048, 1024, [300, 2048, 513]),
+    ("skinny_tail", 512, 768, [1, 1, 1, 700]),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: c[0])
+def test_grouped_gemm(gpu, case):
+    name, D, F, sizes = case
+    print(f"gemm case {case}", flush=True)
+    rng = np.random.default_rng(60 + D)
+    N = len(sizes)
+    offsets = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(offsets[-1])
+    xs = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+    off_t = torch.from_numpy(offsets).to(gpu)
+    h = K.grouped_gate_up(dev_bf16(xs, gpu), off_t, K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu)))
+    h_host = host(h)
+    ys = K.grouped_down(h, off_t, K.pack_down(dev_f32(wd, gpu)))
+    ys_host = host(ys)
+    torch.cuda.synchronize()
+    wgb, wub, wdb = (O.bf16_round(w).astype(np.float64) for w in (wg, wu, wd))
+    for e in range(N):
+        a, b = offsets[e], offsets[e + 1]
+        if b == a:
+            continue
+        x64 = xs[a:b].astype(np.float64)
+        g = x64 @ wgb[e]
+        u = x64 @ wub[e]
+        h_ref = g / (1 + np.exp(-g)) * u
+        err_h = np.abs(h_host[a:b] - h_ref)
+        assert np.all(err_h <= 8e-3 * np.abs(h_ref) + 1e-3 * np.abs(h_ref).max()), \
+            f"h expert {e}: max err {err_h.max()}"
+        y_ref = h_host[a:b].astype(np.float64) @ wdb[e]
+        err_y = np.abs(ys_host[a:b] - y_ref)
+        assert np.all(err_y <= 8e-3 * np.abs(y_ref) + 1e-3 * np.abs(y_ref).max()), \
+            f"ys expert {e}: max err {err_y.max()}"
+
+
+# --------------------------------------------------------------------- aux --
+
+def test_router_aux(gpu):
+    rng = np.random.default_rng(70)
+    B, S, N, Kk = 3, 200, 40, 6
+    logits = (2 * rng.standard_normal((B * S, N))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    idx, _, scores = O.route_sigmoid(logits, bias, Kk, 2.5)
+    ref = O.aux_losses(logits, scores, idx, B, S, N)
+    losses, counts = K.router_aux(dev_f32(logits, gpu), torch.from_numpy(idx).to(gpu), B, S)
+    torch.cuda.synchronize()
+    got = host(losses)
+    assert np.allclose(got, [ref["router_z_loss"], ref["balance_loss"], ref["mean_entropy"]],
+                       rtol=2e-5, atol=0)
+    assert_bits_equal(host(counts), ref["expert_counts"], "expert_counts")

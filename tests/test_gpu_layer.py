@@ -1,0 +1,169 @@
+"""Whole-layer parity of the HIP path against the oracle (needs an MI355X).
+
+Routing, plan and drop mask must be bit-exact; the layer output must be within
+2e-2 normwise relative error of the oracle's fp32 result (float64 arithmetic
+on the fp32 master weights), the bf16 tolerance of the measured workloads.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from hanuman_amd import workloads as W
+from hanuman_amd.layer import DeviceLayer
+from hanuman_amd.moe import MoE
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+def host(t):
+    return t.float().cpu().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+
+def check_routing_and_plan(res, ref_idx, ref_gates, ref_plan, ref_logits=None):
+    if ref_logits is not None:
+        assert np.array_equal(host(res["logits"]).view(np.uint32), ref_logits.view(np.uint32))
+    assert np.array_equal(host(res["top_idx"]), ref_idx), "top_idx"
+    assert np.array_equal(host(res["gates"]).view(np.uint32), ref_gates.view(np.uint32)), "gates"
+    plan = res["plan"]
+    for k in ("counts", "offsets", "slot_pos", "perm_src", "keep"):
+        assert np.array_equal(host(getattr(plan, k)), ref_plan[k]), k
+
+
+def oracle_routing(inp):
+    wl = inp.wl
+    logits = inp.logits if wl.router_from_logits else O.router_logits(inp.x, inp.router)
+    idx, gates = O.route_softmax(logits, wl.top_k)
+    plan = O.dispatch_plan(idx, wl.n_experts, wl.capacity)
+    return logits, idx, gates, plan
+
+
+@pytest.mark.parametrize("name,tokens", [("tiny_fp32", 2048), ("dispatch_identity", 4096),
+                                         ("full_bf16", 2048), ("skewed_bf16", 4096)])
+def test_workload_reduced_tokens(gpu, name, tokens):
+    wl = W.WORKLOADS[name].scaled(tokens)
+    print(f"layer {name} T={wl.tokens}", flush=True)
+    inp = W.make_inputs(wl, seed=0)
+    ref = O.moe_forward(inp.x, {"router": inp.router, "expert_w_gate": inp.w_gate,
+                                "expert_w_up": inp.w_up, "expert_w_down": inp.w_down},
+                        top_k=wl.top_k, routing="softmax", capacity_factor=wl.capacity_factor,
+                        expert=wl.expert, dtype="bf16", precision="fp32",
+                        logits=inp.logits if wl.router_from_logits else None)
+    layer = DeviceLayer(inp, gpu)
+    res = layer.forward()
+    torch.cuda.synchronize()
+    check_routing_and_plan(res, ref["top_idx"], ref["gates"], ref["plan"],
+                           None if wl.router_from_logits else ref["logits"])
+    out = host(res["out"])
+    if wl.expert == "identity":
+        assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), "identity combine"
+    else:
+        err = O.normwise_rel_err(out, ref["out"])
+        print(f"{name}: normwise rel err {err:.3e}", flush=True)
+        assert err < BF16_TOL
+
+
+def sampled_token_ref(inp, idx, gates, plan, tokens):
+    """fp32 (float64 arithmetic) output of selected tokens from the oracle's
+    routing and plan: y[t] = sum_k keep * bf16(g) * expert_e(x[t])."""
+    K = inp.wl.top_k
+    keep = plan["keep"].reshape(-1, K)[tokens]
+    sel = idx[tokens]
+    g16 = O.bf16_round(gates[tokens]).astype(np.float64)
+    x = O.bf16_round(inp.x[tokens]).astype(np.float64)
+    out = np.zeros((len(tokens), inp.x.shape[1]))
+    for e in np.unique(sel):
+        for k in range(K):
+            rows = np.nonzero((sel[:, k] == e) & (keep[:, k] > 0))[0]
+            if rows.size == 0:
+                continue
+            g = x[rows] @ inp.w_gate[e].astype(np.float64)
+            u = x[rows] @ inp.w_up[e].astype(np.float64)
+            y = (g / (1 + np.exp(-g)) * u) @ inp.w_down[e].astype(np.float64)
+            out[rows] += g16[rows, k:k + 1] * y
+    return out
+
+
+@pytest.mark.parametrize("name", ["full_bf16", "skewed_bf16"])
+def test_workload_full_size(gpu, name):
+    wl = W.WORKLOADS[name]
+    print(f"layer {name} full size T={wl.tokens}", flush=True)
+    inp = W.make_inputs(wl, seed=0)
+    logits, idx, gates, plan = oracle_routing(inp)
+    layer = DeviceLayer(inp, gpu)
+    res = layer.forward()
+    torch.cuda.synchronize()
+    check_routing_and_plan(res, idx, gates, plan, None if wl.router_from_logits else logits)
+    dropped = 1.0 - plan["keep"].mean()
+    print(f"{name}: dropped fraction {dropped:.4f}, counts min/max "
+          f"{plan['counts'].min()}/{plan['counts'].max()}", flush=True)
+    rng = np.random.default_rng(1)
+    tokens = np.sort(rng.choice(wl.tokens, 128, replace=False))
+    ref = sampled_token_ref(inp, idx, gates, plan, tokens)
+    got = host(res["out"])[tokens]
+    err = O.normwise_rel_err(got, ref)
+    print(f"{name}: sampled-token normwise rel err {err:.3e}", flush=True)
+    assert err < BF16_TOL
+    # size-independent properties: every kept row of xs is its token's row
+    xs = res["xs"]
+    j = torch.from_numpy(np.nonzero(plan["perm_src"] >= 0)[0][::997]).to(gpu)
+    src_tok = torch.from_numpy(plan["perm_src"]).to(gpu)[j] // wl.top_k
+    assert torch.equal(xs[j], layer.x[src_tok].to(torch.bfloat16))
+
+
+def test_dispatch_identity_full_size(gpu):
+    wl = W.WORKLOADS["dispatch_identity"]
+    inp = W.make_inputs(wl, seed=0)
+    logits, idx, gates, plan = oracle_routing(inp)
+    res = DeviceLayer(inp, gpu).forward()
+    torch.cuda.synchronize()
+    check_routing_and_plan(res, idx, gates, plan)
+    ref = O.combine_identity(inp.x, plan["slot_pos"], gates, wl.tokens, wl.top_k)
+    assert np.array_equal(host(res["out"]).view(np.uint32), ref.view(np.uint32))
+    assert 0.0 < 1.0 - plan["keep"].mean() < 0.02
+
+
+def _params_np(m: MoE) -> dict:
+    return {k: p.value.float().cpu().numpy() for k, p in m.named_params().items()}
+
+
+@pytest.mark.parametrize("n_shared", [1, 2])
+def test_moe_module_reference_mode(gpu, n_shared):
+    B, S, D, F, N, Kk = 2, 96, 256, 128, 8, 2
+    m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.bfloat16, rngs=0, device=gpu)
+    m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))
+    x = torch.randn(B, S, D, generator=torch.Generator(device=gpu).manual_seed(3), device=gpu)
+    x = x.to(torch.bfloat16)
+    out, aux = m(x)
+    torch.cuda.synchronize()
+    p = _params_np(m)
+    xn = x.float().cpu().numpy().reshape(B * S, D)
+    ref = O.moe_forward(xn, p, top_k=Kk, routing="sigmoid", routed_scaling_factor=2.5,
+                        n_shared=n_shared, dtype="bf16", precision="fp32", batch_shape=(B, S))
+    assert out.dtype == torch.float32 and tuple(out.shape) == (B, S, D)
+    err = O.normwise_rel_err(host(out).reshape(B * S, D), ref["out"])
+    print(f"MoE reference mode n_shared={n_shared}: normwise rel err {err:.3e}", flush=True)
+    assert err < BF16_TOL
+    a = ref["aux"]
+    assert np.allclose([float(aux["router_z_loss"]), float(aux["balance_loss"]),
+                        float(aux["mean_entropy"])],
+                       [a["router_z_loss"], a["balance_loss"], a["mean_entropy"]], rtol=2e-5)
+    assert np.array_equal(host(aux["expert_counts"]), a["expert_counts"])
+
+
+def test_moe_module_capacity_softmax(gpu):
+    B, S, D, F, N, Kk = 1, 512, 512, 256, 16, 4
+    m = MoE(D, F, N, Kk, 1, 0.5, 1.0, "bfloat16", rngs=7, device=gpu, routing="softmax",
+            capacity_factor=0.5)
+    x = torch.randn(B, S, D, generator=torch.Generator(device=gpu).manual_seed(4), device=gpu)
+    out, aux = m(x.to(torch.bfloat16))
+    torch.cuda.synchronize()
+    p = _params_np(m)
+    xn = x.to(torch.bfloat16).float().cpu().numpy().reshape(B * S, D)
+    ref = O.moe_forward(xn, p, top_k=Kk, routing="softmax", capacity_factor=0.5, n_shared=1,
+                        dtype="bf16", precision="fp32")
+    assert (ref["plan"]["keep"] == 0).any()
+    err = O.normwise_rel_err(host(out).reshape(B * S, D), ref["out"])
+    assert err < BF16_TOL

@@ -1,0 +1,76 @@
+"""Host-side logic that needs no GPU: workload definitions, input generation,
+and the drop-in module's constructor contract (parameter names and shapes of
+``model/moe.py:126-159``)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from hanuman_amd import workloads as W
+from hanuman_amd.moe import MoE, Param
+
+
+def test_workload_capacities():
+    caps = {n: (w.capacity, w.rows_cap) for n, w in W.WORKLOADS.items()}
+    assert caps["tiny_fp32"] == (640, 4096)
+    assert caps["dispatch_identity"] == (4096, 262144)
+    assert caps["full_bf16"] == (2560, 131072)
+    assert caps["skewed_bf16"] == (5120, 524288)
+    assert caps["fp8_experts"] == (1280, 32768)
+    for w in W.WORKLOADS.values():
+        assert w.capacity == O.capacity_of(w.tokens, w.top_k, w.n_experts, w.capacity_factor)
+
+
+def test_inputs_are_seeded_and_bf16_rounded():
+    wl = W.WORKLOADS["full_bf16"].scaled(64)
+    a = W.make_inputs(wl, seed=0)
+    b = W.make_inputs(wl, seed=0)
+    c = W.make_inputs(wl, seed=1)
+    assert np.array_equal(a.x, b.x) and np.array_equal(a.w_down, b.w_down)
+    assert not np.array_equal(a.x, c.x)
+    assert np.array_equal(a.x, O.bf16_round(a.x))
+    assert a.router.shape == (2048, 64) and a.w_gate.shape == (64, 2048, 1024)
+    assert abs(float(a.w_gate.std()) - 0.02) < 1e-3
+
+
+def test_bf16_rounding_helper_matches_oracle():
+    x = np.random.default_rng(0).standard_normal(100_000).astype(np.float32) * 1e3
+    assert np.array_equal(W.bf16_round_np(x), O.bf16_round(x))
+
+
+def test_zipf_bias_skews_load():
+    wl = W.WORKLOADS["skewed_bf16"].scaled(4096)
+    inp = W.make_inputs(wl, seed=0, with_weights=False)
+    assert inp.bias.max() == pytest.approx(3.0) and inp.bias.min() > 0
+    idx = O.topk_desc(inp.logits, wl.top_k)
+    counts = np.bincount(idx.reshape(-1), minlength=wl.n_experts)
+    assert counts.max() > 4 * counts.mean()
+    plan = O.dispatch_plan(idx, wl.n_experts, wl.capacity)
+    assert 0.05 < 1 - plan["keep"].mean() < 0.5      # real drops
+
+
+def test_moe_constructor_contract():
+    m = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu")
+    shapes = {k: tuple(p.value.shape) for k, p in m.named_params().items()}
+    assert shapes == {"router": (64, 8), "bias": (8,), "expert_w_gate": (8, 64, 32),
+                      "expert_w_up": (8, 64, 32), "expert_w_down": (8, 32, 64),
+                      "shared_w_gate": (64, 32), "shared_w_up": (64, 32),
+                      "shared_w_down": (32, 64)}
+    assert all(isinstance(p, Param) for p in m.named_params().values())
+    assert m.bias.value.abs().sum() == 0
+    assert abs(float(m.router.value.std()) - 0.01) < 3e-3
+    m2 = MoE(64, 32, 8, 2, 3, 0.01, 2.5, torch.bfloat16, rngs=0, device="cpu", d_ff_shared=16)
+    assert tuple(m2.shared_w_gate.value.shape) == (3, 64, 16)
+    assert tuple(m2.shared_w_down.value.shape) == (3, 16, 64)
+
+
+def test_moe_rejects_what_is_not_built():
+    with pytest.raises(NotImplementedError):
+        MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu",
+            mesh=type("M", (), {"devices": np.zeros(8)})())
+    m = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "float32", rngs=0, device="cpu")
+    with pytest.raises(NotImplementedError):
+        m(torch.zeros(1, 4, 64))
+    m = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu")
+    with pytest.raises(ValueError, match="GPU"):   # no CPU path: kernels need device tensors
+        m(torch.zeros(1, 4, 64, dtype=torch.bfloat16))

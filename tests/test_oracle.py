@@ -1,0 +1,299 @@
+"""Pins the CPU oracle (oracle/moe_oracle.py) without running the reference.
+
+The reference (JAX/Flax) cannot run in this image and holds no golden vectors
+for the MoE path, so each oracle function is checked against something that
+fixes it independently: a library routine (numpy argsort/bincount/matmul,
+torch dtype conversions), exact rational arithmetic, brute force on tiny
+inputs, or a closed form the mathematics forces.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+# ------------------------------------------------------------------ dtypes --
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(1)
+    a = np.concatenate([
+        (rng.standard_normal(200_000) * 10.0 ** rng.integers(-30, 30, 200_000)).astype(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.3895314e38, -3.3895314e38, 1e-45, 2**-126],
+                 np.float32)])
+    ours = O.bf16_bits(a)
+    ref = torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32)))[0]
+
+
+def test_e4m3_matches_torch_after_clamp():
+    rng = np.random.default_rng(2)
+    a = np.concatenate([
+        (rng.standard_normal(300_000) * 2.0 ** rng.integers(-12, 12, 300_000)).astype(np.float32),
+        np.array([0.0, -0.0, 448, 449, 464, 465, 480, 1e6, -1e6, 2**-9, 2**-10, 3 * 2**-10,
+                  -2**-10, 2**-6, 2**-7 * 1.0625, 1e-30], np.float32)])
+    ours = O.e4m3_encode(a)
+    ref = torch.from_numpy(np.clip(a, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, ref)
+
+
+def test_e4m3_decode_roundtrip_and_grid():
+    codes = np.arange(256, dtype=np.uint8)
+    v = O.e4m3_decode(codes)
+    finite = ~np.isnan(v)
+    assert finite.sum() == 254                       # 0x7F and 0xFF are NaN
+    assert np.array_equal(O.e4m3_encode(v[finite]), codes[finite])
+    assert v[0x7E] == 448.0 and v[0x01] == 2.0 ** -9  # max normal, min subnormal
+    torch_v = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(v[finite], torch_v[finite])
+
+
+# ------------------------------------------------------- deterministic exp --
+
+def test_exp_det_accuracy():
+    x = np.linspace(-87.0, 88.5, 3_000_001, dtype=np.float32)
+    y = O.exp_det(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    assert np.max(np.abs(y / ref - 1.0)) < 3e-7
+
+
+def test_exp_det_special_values():
+    x = np.array([0.0, -0.0, 88.6, 1e30, -87.5, -1e30, np.nan, 1.0], np.float32)
+    y = O.exp_det(x)
+    assert y[0] == 1.0 and y[1] == 1.0
+    assert np.isinf(y[2]) and np.isinf(y[3])
+    assert y[4] == 0.0 and y[5] == 0.0
+    assert np.isnan(y[6])
+    assert abs(float(y[7]) - math.e) < 3e-7 * math.e
+
+
+def test_sigmoid_det_against_float64():
+    x = np.linspace(-40, 40, 400_001, dtype=np.float32)
+    s = O.sigmoid_det(x).astype(np.float64)
+    ref = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(s - ref) / ref) < 6e-7
+    assert O.sigmoid_det(np.array([100.0, -100.0], np.float32)).tolist() == [1.0, 0.0]
+
+
+# ------------------------------------------------------------------ router --
+
+def test_total_order_key():
+    vals = np.array([-np.inf, -3.0, -1e-30, -0.0, 0.0, 1e-45, 2.0, np.inf], np.float32)
+    k = O.total_order_key(vals)
+    assert np.all(np.diff(k) > 0)                    # strictly increasing, -0 < +0
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(10_000).astype(np.float32)
+    assert np.array_equal(np.argsort(O.total_order_key(a), kind="stable"),
+                          np.argsort(a, kind="stable"))
+
+
+def test_router_logits_is_correctly_rounded_dot():
+    """Tiny case: the float64 d-ascending sum, rounded once, equals the float32
+    rounding of the exact rational dot product."""
+    rng = np.random.default_rng(4)
+    x = O.bf16_round(rng.standard_normal((6, 16)).astype(np.float32))
+    w = (0.02 * rng.standard_normal((16, 5))).astype(np.float32)
+    got = O.router_logits(x, w)
+    for t in range(6):
+        for n in range(5):
+            exact = sum(Fraction(float(x[t, d])) * Fraction(float(w[d, n])) for d in range(16))
+            assert got[t, n] == np.float32(float(exact))   # float(Fraction) rounds once
+
+
+def test_router_logits_bruteforce_and_blas():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((7, 33)).astype(np.float32)
+    w = rng.standard_normal((33, 9)).astype(np.float32)
+    got = O.router_logits(x, w, token_block=3)
+    loop = np.empty_like(got)
+    for t in range(7):
+        for n in range(9):
+            acc = 0.0
+            for d in range(33):
+                acc += float(x[t, d]) * float(w[d, n])
+            loop[t, n] = np.float32(acc)
+    assert np.array_equal(got, loop)
+    blas = (x.astype(np.float64) @ w.astype(np.float64)).astype(np.float32)
+    assert np.max(np.abs(got - blas)) <= np.max(np.abs(blas)) * 2e-7
+
+
+def test_topk_matches_argsort_and_breaks_ties_low_index():
+    rng = np.random.default_rng(6)
+    key = rng.standard_normal((500, 64)).astype(np.float32)
+    idx = O.topk_desc(key, 8)
+    ref = np.argsort(-key, axis=1, kind="stable")[:, :8]
+    assert np.array_equal(idx, ref)
+    tied = np.zeros((2, 8), np.float32)
+    tied[0, [1, 5, 6]] = 1.0
+    tied[1, :] = 0.5
+    got = O.topk_desc(tied, 4)
+    assert got[0].tolist() == [1, 5, 6, 0]
+    assert got[1].tolist() == [0, 1, 2, 3]
+    signed_zero = np.array([[-0.0, 0.0, -0.0, 0.0]], np.float32)
+    assert O.topk_desc(signed_zero, 4)[0].tolist() == [1, 3, 0, 2]
+
+
+def test_route_softmax_gates_are_renormalised_softmax():
+    rng = np.random.default_rng(7)
+    logits = rng.standard_normal((300, 64)).astype(np.float32)
+    idx, g = O.route_softmax(logits, 8)
+    l64 = logits.astype(np.float64)
+    p = np.exp(l64 - l64.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    sel = np.take_along_axis(p, idx, 1)
+    assert np.allclose(g, sel / sel.sum(1, keepdims=True), rtol=2e-6, atol=0)
+    assert np.all(np.diff(np.take_along_axis(logits, idx, 1), axis=1) <= 0)
+
+
+def test_route_sigmoid_matches_reference_formula():
+    rng = np.random.default_rng(8)
+    logits = (rng.standard_normal((300, 16)) * 3).astype(np.float32)
+    bias = (rng.standard_normal(16) * 0.1).astype(np.float32)
+    idx, g, scores = O.route_sigmoid(logits, bias, 4, 2.5)
+    s64 = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    assert np.allclose(scores, s64, rtol=1e-6, atol=0)
+    key = scores + bias
+    assert np.array_equal(idx, np.argsort(-key, axis=1, kind="stable")[:, :4])
+    sel = np.take_along_axis(s64, idx, 1)
+    assert np.allclose(g, sel / (sel.sum(1, keepdims=True) + 1e-9) * 2.5, rtol=2e-6)
+
+
+# ----------------------------------------------------------- dispatch plan --
+
+@pytest.mark.parametrize("T,K,N,C", [(1, 1, 1, 1), (5, 2, 3, 2), (16, 4, 8, 3), (33, 3, 5, 100),
+                                     (64, 8, 64, 1), (40, 2, 4, 20)])
+def test_plan_matches_bruteforce(T, K, N, C):
+    rng = np.random.default_rng(T * 131 + N)
+    top = rng.integers(0, N, size=(T, K)).astype(np.int32)
+    a = O.dispatch_plan(top, N, C)
+    b = O.dispatch_plan_bruteforce(top, N, C)
+    for k in ("counts", "kept", "offsets", "slot_pos", "perm_src", "keep"):
+        assert np.array_equal(a[k], b[k]), k
+
+
+def test_plan_dropless_equals_stable_argsort_and_bincount():
+    rng = np.random.default_rng(9)
+    top = rng.integers(0, 64, size=(2048, 8)).astype(np.int32)
+    R = top.size
+    p = O.dispatch_plan(top, 64, R)
+    assert np.array_equal(p["perm_src"], np.argsort(top.reshape(-1), kind="stable"))
+    assert np.array_equal(p["counts"], np.bincount(top.reshape(-1), minlength=64))
+    assert np.array_equal(p["slot_pos"], np.argsort(p["perm_src"], kind="stable"))
+    assert p["keep"].all()
+
+
+def test_plan_capacity_invariants():
+    rng = np.random.default_rng(10)
+    N, K, T = 16, 4, 1000
+    # heavy skew: expert 0 gets far more than its capacity
+    top = np.where(rng.random((T, K)) < 0.5, 0, rng.integers(0, N, (T, K))).astype(np.int32)
+    C = O.capacity_of(T, K, N, 1.0)
+    p = O.dispatch_plan(top, N, C)
+    e = top.reshape(-1)
+    assert p["counts"].sum() == T * K
+    assert np.array_equal(p["kept"], np.minimum(p["counts"], C))
+    assert p["keep"].sum() == np.minimum(p["counts"], C).sum()
+    kept_idx = np.nonzero(p["keep"])[0]
+    total = p["offsets"][-1]
+    assert sorted(p["slot_pos"][kept_idx].tolist()) == list(range(total))  # bijection on kept
+    assert np.all(p["perm_src"][total:] == -1)
+    assert np.all(p["perm_src"][p["slot_pos"][kept_idx]] == kept_idx)
+    for ex in range(N):                                  # first C slots of each expert win
+        slots = np.nonzero(e == ex)[0]
+        assert np.array_equal(np.nonzero(p["keep"][slots])[0], np.arange(min(len(slots), C)))
+        seg = p["perm_src"][p["offsets"][ex]:p["offsets"][ex + 1]]
+        assert np.all(np.diff(seg) > 0)                  # stable: ascending slot index
+        assert np.all(e[seg] == ex)
+
+
+def test_capacity_formula():
+    assert O.capacity_of(16384, 8, 64, 1.25) == 2560
+    assert O.capacity_of(32768, 8, 64, 1.0) == 4096
+    assert O.capacity_of(65536, 8, 128, 1.25) == 5120
+    assert O.capacity_of(8192, 4, 32, 1.25) == 1280
+    assert O.capacity_of(2048, 2, 8, 1.25) == 640
+    assert O.capacity_of(10, 3, 7, 1.0) == 5             # ceil(30/7)
+    assert O.capacity_of(10, 3, 7, None) == 30
+
+
+def test_permute_rows():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((20, 8)).astype(np.float32)
+    top = rng.integers(0, 4, (20, 3)).astype(np.int32)
+    p = O.dispatch_plan(top, 4, 6)
+    xs = O.permute_rows(x, p["perm_src"], 3)
+    for j, i in enumerate(p["perm_src"]):
+        if i >= 0:
+            assert np.array_equal(xs[j], x[i // 3])
+        else:
+            assert not xs[j].any()
+
+
+# ---------------------------------------------------------- expert + combine --
+
+def test_expert_ffn_is_per_expert_matmul():
+    rng = np.random.default_rng(12)
+    N, D, F = 4, 16, 8
+    wg, wu = rng.standard_normal((2, N, D, F)).astype(np.float32)
+    wd = rng.standard_normal((N, F, D)).astype(np.float32)
+    offsets = np.array([0, 3, 3, 10, 12])               # expert 1 is empty
+    xs = rng.standard_normal((14, D)).astype(np.float32)
+    ys = O.expert_ffn(xs, offsets, wg, wu, wd, "fp32")
+    for e in range(N):
+        for r in range(offsets[e], offsets[e + 1]):
+            g = xs[r].astype(np.float64) @ wg[e]
+            u = xs[r].astype(np.float64) @ wu[e]
+            h = g / (1 + np.exp(-g)) * u
+            assert np.allclose(ys[r], h @ wd[e], rtol=1e-5, atol=1e-5)
+    assert not ys[12:].any()
+    yb = O.expert_ffn(xs, offsets, wg, wu, wd, "bf16")
+    assert O.normwise_rel_err(yb[:12], ys[:12]) < 2e-2
+
+
+def test_combine_identity_expert_closed_form():
+    rng = np.random.default_rng(13)
+    T, K, N, D = 64, 4, 8, 16
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    top = rng.integers(0, N, (T, K)).astype(np.int32)
+    g = rng.random((T, K)).astype(np.float32)
+    p = O.dispatch_plan(top, N, 20)                     # some drops
+    xs = O.permute_rows(x, p["perm_src"], K)
+    y = O.combine(xs, p["slot_pos"], g, T, K)
+    keep = p["keep"].reshape(T, K).astype(np.float64)
+    gb = O.bf16_round(g).astype(np.float64)
+    ref = x.astype(np.float64) * (keep * gb).sum(1, keepdims=True)
+    assert np.allclose(y, ref, rtol=1e-6, atol=1e-7)
+    assert (p["keep"] == 0).any()
+
+
+def test_whole_layer_with_identical_experts():
+    """All experts equal => routed output = (sum_k bf16 gate_k) * expert(x)."""
+    rng = np.random.default_rng(14)
+    T, D, N, K, F = 32, 16, 6, 3, 8
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    wg1, wu1 = (0.3 * rng.standard_normal((2, D, F))).astype(np.float32)
+    wd1 = (0.3 * rng.standard_normal((F, D))).astype(np.float32)
+    params = {"router": (0.5 * rng.standard_normal((D, N))).astype(np.float32),
+              "bias": np.zeros(N, np.float32),
+              "expert_w_gate": np.repeat(wg1[None], N, 0), "expert_w_up": np.repeat(wu1[None], N, 0),
+              "expert_w_down": np.repeat(wd1[None], N, 0)}
+    r = O.moe_forward(x, params, top_k=K, routing="sigmoid", routed_scaling_factor=2.5)
+    one = O.expert_ffn(x, np.array([0, T]), wg1[None], wu1[None], wd1[None], "fp32")
+    gsum = O.bf16_round(r["gates"]).astype(np.float64).sum(1, keepdims=True)
+    assert np.allclose(r["out"], one * gsum, rtol=1e-5, atol=1e-6)
+
+
+def test_aux_closed_forms():
+    B, S, N, K = 2, 8, 4, 2
+    logits = np.zeros((B * S, N), np.float32)          # uniform router
+    scores = O.sigmoid_det(logits)
+    top = np.tile(np.array([[0, 1], [2, 3]], np.int32), (B * S // 2, 1))
+    aux = O.aux_losses(logits, scores, top, B, S, N)
+    assert math.isclose(aux["router_z_loss"], math.log(N) ** 2, rel_tol=1e-12)
+    assert math.isclose(aux["balance_loss"], 1.0, rel_tol=1e-6)   # perfect balance
+    assert math.isclose(aux["mean_entropy"], math.log(N), rel_tol=1e-6)
+    assert aux["expert_counts"].tolist() == [B * S // 2] * N
