@@ -8,22 +8,28 @@
 // With SWIGLU the packed columns alternate 32 gate / 32 up columns of the same
 // h columns and the epilogue writes h = bf16(silu(gate) * up).
 //
-// Tiling: one workgroup (4 waves) computes a 256 x 256 output tile; wave
-// (wm, wn) owns a 128 x 128 quarter as 4 x 4 blocks of
-// v_mfma_f32_32x32x16_bf16.  K advances 64 at a time through two LDS stages
-// (rows padded to 72 bf16 = 144 bytes, so the 16-byte fragment reads of eight
-// consecutive lanes hit all 32 banks once).  Global loads for the next stage
-// are issued before the current stage's MFMAs.  The MFMA takes the weight
-// fragment as its first operand, so an accumulator lane holds one token row
-// and four consecutive output columns per group, stored as one 8-byte write.
+// Persistent kernel: one workgroup (4 waves) per CU loops over 256 x 256
+// output tiles.  Tiles are numbered expert by expert (ceil(rows_e / 256)
+// m-tiles each, n fastest); every workgroup computes the numbering from
+// `offsets`, so the launch never depends on the routing.  The tile range is
+// split evenly over the 8 XCDs (workgroup i runs on XCD i % 8) and the
+// workgroups of an XCD stride through their range together, so at any moment
+// an XCD works on a few consecutive m-tiles of one expert and shares their A
+// rows and B columns in its L2.
 //
-// Scheduling: blocks enumerate (m-tile, n-tile) with n fastest; m-tiles are
-// numbered expert by expert (ceil(rows_e / 256) each, computed in-kernel from
-// `offsets`).  The launch covers the static bound ceil(rows_cap/256) + N
-// m-tiles; blocks past the real count return at once.  A rows are read
-// through clamped pointers, so buffers need exactly rows_cap rows.  Consecutive logical
-// tiles are placed on the same XCD (workgroups are dealt round-robin over the
-// 8 XCDs), so tiles sharing an A row block or a B column block share an L2.
+// Main loop (per 64-wide K step): the next step's A and B tiles (2 x 32 KB)
+// go straight from global memory into the other LDS stage with
+// global_load_lds_dwordx4 (no register staging), while the current stage feeds
+// 4 x 16 v_mfma_f32_32x32x16_bf16 per wave (each wave owns a 128 x 128
+// quarter).  An LDS row holds 64 bf16 as eight 16-byte chunks; chunk c of row
+// r is stored at position c ^ (r & 7), so the eight lanes that read one MFMA
+// fragment row-group hit eight different bank groups.  Fragments are
+// double-buffered in registers and the instruction order is fenced: the next
+// sub-step's LDS reads and DMA issues go out before the current sub-step's 16
+// MFMAs.  The next tile's first stage is prefetched during the current tile's
+// last K step, so the pipeline does not drain between tiles.
+#include <atomic>
+
 #include "hmoe_common.h"
 
 namespace hmoe {
@@ -32,22 +38,87 @@ namespace {
 constexpr int kBM = HMOE_GEMM_TILE_M;
 constexpr int kBN = 256;
 constexpr int kBK = 64;
-constexpr int kPitch = kBK + 8;
 constexpr int kThreads = 256;
-constexpr int kStageElems = kBM * kPitch;
+constexpr int kStageBytes = 65536;  // A 32 KB | B 32 KB
 constexpr int kMaxExperts = 1024;
 constexpr int kNumXcd = 8;
 
 static_assert(kBM == 256, "tile loaders assume 256-row tiles");
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+// Exclusive scan of per-expert m-tile counts into tstart[0..n_experts];
+// returns the total.  Every thread takes four experts.
+__device__ __forceinline__ int scan_tiles(const int32_t* __restrict__ offsets, int n_experts,
+                                          int32_t* tstart, int32_t* scan_tmp) {
+  const int tid = threadIdx.x;
+  int local[4];
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * 4 + j;
+    int tiles = 0;
+    if (e < n_experts) tiles = (offsets[e + 1] - offsets[e] + kBM - 1) / kBM;
+    local[j] = tiles;
+    sum += tiles;
+  }
+  scan_tmp[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kThreads; off <<= 1) {
+    const int v = tid >= off ? scan_tmp[tid - off] : 0;
+    __syncthreads();
+    scan_tmp[tid] += v;
+    __syncthreads();
+  }
+  int run = scan_tmp[tid] - sum;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * 4 + j;
+    if (e < n_experts) tstart[e] = run;
+    run += local[j];
+  }
+  if (tid == kThreads - 1) tstart[n_experts] = scan_tmp[kThreads - 1];
+  __syncthreads();
+  return tstart[n_experts];
+}
+
+// Expert, first row, segment end and first column of logical tile t.
+__device__ __forceinline__ void decode_tile(int t, int n_tiles_n, const int32_t* tstart,
+                                            const int32_t* __restrict__ offsets, int n_experts,
+                                            int& e, int64_t& row0, int64_t& row_end, int& n0) {
+  const int m_tile = t / n_tiles_n;
+  const int n_tile = t - m_tile * n_tiles_n;
+  int lo = 0, hi = n_experts;  // largest e with tstart[e] <= m_tile (it has >= 1 tile)
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (tstart[mid] <= m_tile) lo = mid; else hi = mid;
+  }
+  e = lo;
+  row0 = offsets[e] + static_cast<int64_t>(m_tile - tstart[e]) * kBM;
+  row_end = offsets[e + 1];
+  n0 = n_tile * kBN;
+}
 
 template <bool SWIGLU>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
     uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kStageElems];
+  // The two stages live in dynamic LDS.  With a static array the compiler
+  // cannot tell the stage being loaded from the stage being read and waits
+  // for every DMA load before the next LDS read; the stage protocol below
+  // (DMA into stage cur^1, read stage cur, vmcnt(0) + barrier at the end of
+  // each K step) already orders them.
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int32_t tstart[kMaxExperts + 1];
   __shared__ int32_t scan_tmp[kThreads];
 
@@ -55,185 +126,239 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  // ---- tile schedule: m-tiles per expert, exclusive scan ----------------
-  {
-    int local[4];
-    int sum = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = tid * 4 + j;
-      int tiles = 0;
-      if (e < n_experts) {
-        const int rows = offsets[e + 1] - offsets[e];
-        tiles = (rows + kBM - 1) / kBM;
-      }
-      local[j] = tiles;
-      sum += tiles;
-    }
-    scan_tmp[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < kThreads; off <<= 1) {
-      const int v = tid >= off ? scan_tmp[tid - off] : 0;
-      __syncthreads();
-      scan_tmp[tid] += v;
-      __syncthreads();
-    }
-    int run = scan_tmp[tid] - sum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = tid * 4 + j;
-      if (e < n_experts) tstart[e] = run;
-      run += local[j];
-    }
-    if (tid == kThreads - 1) tstart[n_experts] = scan_tmp[kThreads - 1];
-    __syncthreads();
-  }
-
-  const int grid = gridDim.x;
-  const int pid = blockIdx.x;
-  const int logical = (pid % kNumXcd) * (grid / kNumXcd) + pid / kNumXcd;
-  const int m_tile = logical / n_tiles_n;
-  const int n_tile = logical % n_tiles_n;
-  if (m_tile >= tstart[n_experts]) return;  // uniform per workgroup
-  int lo = 0, hi = n_experts;  // largest e with tstart[e] <= m_tile
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (tstart[mid] <= m_tile) lo = mid; else hi = mid;
-  }
-  const int e = lo;
-  const int64_t row0 = offsets[e] + static_cast<int64_t>(m_tile - tstart[e]) * kBM;
-  const int64_t row_end = offsets[e + 1];
-  const int n0 = n_tile * kBN;
-
-  const uint16_t* b_base = B + (static_cast<int64_t>(e) * ncols + n0) * kdim;
-
-  // ---- global -> register staging (8 x 16 B of A and of B per thread) ----
-  // A rows past the buffer (the last tile of the last segment) are clamped
-  // to its last row; their results are never stored.
-  const int ld_row = tid >> 3;
-  const int ld_col = (tid & 7) * 8;
-  const uint16_t* a_ptr[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int64_t r = row0 + ld_row + 32 * i;
-    r = r < a_rows ? r : a_rows - 1;
-    a_ptr[i] = A + r * kdim + ld_col;
-  }
-  u32x4 ra[8], rb[8];
-  auto load_stage = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = ld_row + 32 * i;
-      ra[i] = *reinterpret_cast<const u32x4*>(a_ptr[i] + k0);
-      rb[i] = *reinterpret_cast<const u32x4*>(b_base + static_cast<int64_t>(r) * kdim + k0 + ld_col);
-    }
-  };
-  auto store_stage = [&](int st) {
-    uint16_t* sa = smem[st][0];
-    uint16_t* sb = smem[st][1];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = ld_row + 32 * i;
-      *reinterpret_cast<u32x4*>(sa + r * kPitch + ld_col) = ra[i];
-      *reinterpret_cast<u32x4*>(sb + r * kPitch + ld_col) = rb[i];
-    }
-  };
-
-  const int wm = wave >> 1, wn = wave & 1;
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 8;
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
+  const int total =
+      __builtin_amdgcn_readfirstlane(scan_tiles(offsets, n_experts, tstart, scan_tmp) * n_tiles_n);
+  const int xcd = blockIdx.x % kNumXcd;
+  const int per_xcd = gridDim.x / kNumXcd;
+  const int slot = blockIdx.x / kNumXcd;
+  const int lo = static_cast<int>((static_cast<int64_t>(total) * xcd) / kNumXcd);
+  const int hi = static_cast<int>((static_cast<int64_t>(total) * (xcd + 1)) / kNumXcd);
+  const int first = lo + slot;
+  if (first >= hi) return;  // uniform per workgroup
   const int ktiles = kdim / kBK;
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) load_stage((kt + 1) * kBK);
-    const uint16_t* sa = smem[cur][0] + (wm * 128 + frag_row) * kPitch + frag_k;
-    const uint16_t* sb = smem[cur][1] + (wn * 128 + frag_row) * kPitch + frag_k;
+
+  // ---- global -> LDS loads ------------------------------------------------
+  // Round i (0..7) of a stage: this thread fills 16-byte slot i*256 + tid,
+  // i.e. row i*32 + tid/8 at position tid&7, which holds chunk
+  // (tid&7) ^ (row&7) = (tid&7) ^ ((tid>>3)&7).  One wave instruction writes
+  // 1 KB of contiguous LDS.
+  const int ld_r = tid >> 3;
+  const int ld_c = (tid & 7) ^ (ld_r & 7);
+  const uint32_t b_off0 = static_cast<uint32_t>(ld_r * kdim + ld_c * 8) * 2u;
+  uint32_t a_off[8];
+  const uint16_t* a_tile = A;
+  const uint16_t* b_tile = B;
+  auto set_load_tile = [&](int t) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    e = __builtin_amdgcn_readfirstlane(e);
+    n0 = __builtin_amdgcn_readfirstlane(n0);
+    const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
+    a_tile = A + static_cast<int64_t>(r0) * kdim;
+    b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * kdim;
+    // Rows past the buffer (the last tile of the last segment) are clamped to
+    // its last row; their results are never stored.
+    const int64_t lim = a_rows - 1 - r0;
 #pragma unroll
-    for (int k16 = 0; k16 < kBK / 16; ++k16) {
-      bf16x8 af[4], bfr[4];
+    for (int i = 0; i < 8; ++i) {
+      int rr = i * 32 + ld_r;
+      rr = rr < lim ? rr : static_cast<int>(lim);
+      a_off[i] = static_cast<uint32_t>(rr * kdim + ld_c * 8) * 2u;
+    }
+  };
+  // Part p (0..3) issues rounds 2p and 2p+1 of A and of B for K offset k0.
+  auto issue_loads = [&](int stage, int k0, int part) {
+    uint8_t* base = smem + stage * kStageBytes;
+    const uint8_t* ab = reinterpret_cast<const uint8_t*>(a_tile + k0);
+    const uint8_t* bb = reinterpret_cast<const uint8_t*>(b_tile + k0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        af[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kPitch + k16 * 16);
-        bfr[i] = *reinterpret_cast<const bf16x8*>(sb + i * 32 * kPitch + k16 * 16);
-      }
+    for (int q = 0; q < 2; ++q) {
+      const int i = part * 2 + q;
+      __builtin_amdgcn_global_load_lds(ab + a_off[i], (lds_ptr_t)(base + i * 4096 + wave * 1024),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(bb + b_off0 + static_cast<uint32_t>(i * 32 * kdim * 2),
+                                       (lds_ptr_t)(base + 32768 + i * 4096 + wave * 1024), 16, 0,
+                                       0);
+    }
+  };
+
+  // ---- MFMA fragments -------------------------------------------------------
+  // v_mfma_f32_32x32x16_bf16 operand: lane L holds row L&31, K chunk
+  // (2s + L/32) of sub-step s.  Fragment i of the wave's 128 rows is 32 rows
+  // (4096 bytes) further down.  The weight fragment is the first operand, so
+  // an accumulator lane holds one token row and groups of four consecutive
+  // output columns.
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31;
+  const int fhalf = lane >> 5;
+  int fa_addr[4], fb_addr[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int cpos = ((2 * s + fhalf) ^ (frow & 7)) * 16;
+    fa_addr[s] = (wm * 128 + frow) * 128 + cpos;
+    fb_addr[s] = 32768 + (wn * 128 + frow) * 128 + cpos;
+  }
+  bf16x8 fa[2][4], fb[2][4];
+  auto read_frags = [&](int buf, int stage, int s) {
+    const uint8_t* base = smem + stage * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[buf][i] = *reinterpret_cast<const bf16x8*>(base + fa_addr[s] + i * 4096);
+      fb[buf][i] = *reinterpret_cast<const bf16x8*>(base + fb_addr[s] + i * 4096);
+    }
+  };
+  f32x16 acc[4][4];
+
+  // One K step on stage `cur`: loads for the next step into stage cur^1 (when
+  // `load`), fragment double-buffering, 64 MFMAs, then a barrier (which also
+  // waits for this thread's DMA loads).
+  int cur = 0;
+  auto kstep = [&](bool load, int ld_k0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (load) issue_loads(cur ^ 1, ld_k0, s);
+      if (s < 3) read_frags((s + 1) & 1, cur, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s & 1][j], fa[s & 1][i], acc[i][j],
+                                                              0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < ktiles) store_stage(cur ^ 1);
     __syncthreads();
-  }
+  };
 
-  // ---- epilogue ----------------------------------------------------------
-  // acc[i][j] lane L, element r: token row wm*128 + i*32 + (L & 31);
-  // column wn*128 + j*32 + (r/4)*8 + (L>>5)*4 + (r&3).
+  set_load_tile(first);
+#pragma unroll
+  for (int part = 0; part < 4; ++part) issue_loads(0, 0, part);
+  __syncthreads();
+  read_frags(0, 0, 0);
+
   const int col_lane = (lane >> 5) * 4;
+  for (int t = first; t < hi; t += per_xcd) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + wm * 128 + i * 32 + frag_row;
-    if (row >= row_end) continue;
-    uint16_t* crow = C + row * ldc;
-    if (SWIGLU) {
-      const int hbase = (n0 + wn * 128) / 2;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float h[4];
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int kt = 0; kt + 1 < ktiles; ++kt) {
+      kstep(true, (kt + 1) * kBK);
+      read_frags(0, cur ^ 1, 0);
+      cur ^= 1;
+    }
+    const bool next = t + per_xcd < hi;
+    if (next) set_load_tile(t + per_xcd);
+    kstep(next, 0);
+
+    // ---- epilogue: acc[i][j] lane L, element r = token row
+    // wm*128 + i*32 + (L&31), column wn*128 + j*32 + (r/4)*8 + (L/32)*4 + r%4.
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float gv = acc[i][2 * p][g * 4 + q];
-            const float uv = acc[i][2 * p + 1][g * 4 + q];
-            h[q] = silu_f32(gv) * uv;
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + wm * 128 + i * 32 + frow;
+      if (row < row_end) {
+        uint16_t* crow = C + row * ldc;
+        if (SWIGLU) {
+          const int hbase = (n0 + wn * 128) / 2;
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float h[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                h[q] = silu_f32(acc[i][2 * p][g * 4 + q]) * acc[i][2 * p + 1][g * 4 + q];
+              uint2 pk;
+              pk.x = pack_bf16x2_rne(h[0], h[1]);
+              pk.y = pack_bf16x2_rne(h[2], h[3]);
+              *reinterpret_cast<uint2*>(crow + hbase + p * 32 + g * 8 + col_lane) = pk;
+            }
           }
-          uint2 pk;
-          pk.x = pack_bf16x2(h[0], h[1]);
-          pk.y = pack_bf16x2(h[2], h[3]);
-          *reinterpret_cast<uint2*>(crow + hbase + p * 32 + g * 8 + col_lane) = pk;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              uint2 pk;
+              pk.x = pack_bf16x2_rne(acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1]);
+              pk.y = pack_bf16x2_rne(acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]);
+              *reinterpret_cast<uint2*>(crow + n0 + wn * 128 + j * 32 + g * 8 + col_lane) = pk;
+            }
+          }
         }
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          uint2 pk;
-          pk.x = pack_bf16x2(acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1]);
-          pk.y = pack_bf16x2(acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]);
-          *reinterpret_cast<uint2*>(crow + n0 + wn * 128 + j * 32 + g * 8 + col_lane) = pk;
-        }
-      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (next) read_frags(0, cur ^ 1, 0);
+    cur ^= 1;
+  }
+}
+
+// Workgroups per launch: one per CU, a multiple of the XCD count.
+int persistent_grid(hipStream_t s, int* grid, int* dev_out) {
+  int dev = 0;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess) {
+    if (hipGetDevice(&dev) != hipSuccess) {
+      set_error("grouped GEMM: cannot query the current device");
+      return HMOE_ERR_HIP;
     }
   }
+  static std::atomic<int> cached[64];
+  int cus = dev >= 0 && dev < 64 ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (cus == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+      set_error("grouped GEMM: cannot query the CU count of device %d", dev);
+      return HMOE_ERR_HIP;
+    }
+    if (dev >= 0 && dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
+  }
+  int g = (cus / kNumXcd) * kNumXcd;
+  *grid = g > 0 ? g : kNumXcd;
+  *dev_out = dev;
+  return HMOE_OK;
+}
+
+// Allows 2 * kStageBytes of dynamic LDS for both kernel variants, once per device.
+int allow_dynamic_lds(int dev) {
+  static std::atomic<bool> done[64];
+  if (dev >= 0 && dev < 64 && done[dev].load(std::memory_order_acquire)) return HMOE_OK;
+  const int bytes = 2 * kStageBytes;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<true>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess ||
+      hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<false>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+    set_error("grouped GEMM: cannot allow %d bytes of dynamic LDS on device %d", bytes, dev);
+    return HMOE_ERR_HIP;
+  }
+  if (dev >= 0 && dev < 64) done[dev].store(true, std::memory_order_release);
+  return HMOE_OK;
 }
 
 int launch_grouped(bool swiglu, const void* A, const void* B, const int32_t* offsets,
                    int n_experts, int64_t rows_cap, int kdim, int ncols, void* C, int64_t ldc,
                    hipStream_t s, const char* what) {
   const int n_tiles_n = ncols / kBN;
-  const int64_t m_tiles = ceil_div(rows_cap, kBM) + n_experts;
-  int64_t blocks = m_tiles * n_tiles_n;
-  blocks = ceil_div(blocks, kNumXcd) * kNumXcd;
-  HMOE_REQUIRE(blocks < (int64_t(1) << 31), "%s: too many tiles", what);
+  const int64_t max_tiles = (ceil_div(rows_cap, kBM) + n_experts) * n_tiles_n;
+  HMOE_REQUIRE(max_tiles < (int64_t(1) << 31), "%s: too many tiles", what);
+  HMOE_REQUIRE(rows_cap < (int64_t(1) << 31), "%s: rows_cap must fit in int32", what);
+  int dev = 0;
+  int grid = 0;
+  if (int rc = persistent_grid(s, &grid, &dev)) return rc;
+  if (int rc = allow_dynamic_lds(dev)) return rc;
+  const size_t lds = 2 * kStageBytes;
   if (swiglu)
-    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(grid), dim3(kThreads), lds, s,
                        static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), offsets,
                        n_experts, rows_cap, kdim, ncols, static_cast<uint16_t*>(C), ldc, n_tiles_n);
   else
-    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(grid), dim3(kThreads), lds, s,
                        static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), offsets,
                        n_experts, rows_cap, kdim, ncols, static_cast<uint16_t*>(C), ldc, n_tiles_n);
   return check_launch(what);
