@@ -1,22 +1,15 @@
 // Router: fp32 logits, top-k selection and gate weights (model/moe.py:175-192).
 //
-// One workgroup of 4 waves handles 32 tokens; each wave owns 8 tokens and a
-// lane owns experts lane, lane+64, ... (EPL per lane).  Logits accumulate in
-// float64 with d ascending: the products of bf16/fp32 activations and
-// fp32/bf16 weights are exact in float64, so the fused multiply-add gives the
-// same bits as the oracle's multiply-then-add, and the single rounding to
-// float32 at the end makes the logits reproducible bit for bit.  Top-k is K
-// rounds of a wave-wide max over a packed (totalOrder key, ~expert) 64-bit
-// value, so equal keys resolve to the lower expert index.
+// Logits are float32 roundings of float64 sums taken in ascending d from +0.0
+// (see router_kernel for how the float64 matrix cores keep that order).
+// Top-k is K rounds of a wave-wide max over a packed (totalOrder key,
+// ~expert) 64-bit value, so equal keys resolve to the lower expert index.
 #include "hmoe_common.h"
 
 namespace hmoe {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kTokPerWave = 8;
-constexpr int kTokPerBlock = kWaves * kTokPerWave;
-constexpr int kDChunk = 32;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
@@ -95,79 +88,144 @@ __device__ __forceinline__ void select_and_gate(const float (&logit)[EPL], const
 }
 
 template <typename XT>
-__device__ __forceinline__ double load_as_f64(const XT* p, int64_t i);
+__device__ __forceinline__ float load_as_f32(const XT* p, int64_t i);
 template <>
-__device__ __forceinline__ double load_as_f64<float>(const float* p, int64_t i) {
-  return static_cast<double>(p[i]);
+__device__ __forceinline__ float load_as_f32<float>(const float* p, int64_t i) {
+  return p[i];
 }
 template <>
-__device__ __forceinline__ double load_as_f64<uint16_t>(const uint16_t* p, int64_t i) {
-  return static_cast<double>(bf16_bits_to_f32(p[i]));
+__device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p, int64_t i) {
+  return bf16_bits_to_f32(p[i]);
 }
 
-template <int EPL, typename XT, typename WT>
+// Logits on the float64 matrix cores.  v_mfma_f64_16x16x4f64 computes
+// D = C + A[:,0]B[0,:] + ... + A[:,3]B[3,:] with the additions done one after
+// another in k order, each rounded to float64 (C first); the products of
+// bf16/fp32 activations and fp32/bf16 weights are exact in float64.  Walking d
+// upwards four at a time from C = +0.0 therefore reproduces the sequential
+// d-ascending float64 sum bit for bit.  Operand layout: A[i][k] in lane
+// i + 16k, B[k][j] in lane j + 16k; D[i][j] in lane j + 16*(i%4), register i/4.
+//
+// A workgroup of 4 waves takes 64 tokens; each wave 16 tokens against all
+// experts (NT tiles of 16 experts, zero-padded past n_experts).  x and W are
+// staged in LDS as float32, 32 d at a time, double-buffered through registers
+// (the next chunk's global loads are issued before the current chunk's
+// MFMAs).  The float32-rounded logits go through LDS to the wave-per-token
+// selection.
+constexpr int kRTokBlk = 64;
+constexpr int kRTokWave = 16;
+constexpr int kRDc = 32;
+constexpr int kRXPitch = kRDc + 1;
+
+template <int NT>
+struct RouterLds {
+  static constexpr int kNP = 16 * NT;
+  static constexpr int kWPitch = kNP + 8;
+  float x[2][kRTokBlk][kRXPitch];
+  float w[2][kRDc][kWPitch];
+};
+
+template <int NT, typename XT, typename WT>
 __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, const WT* __restrict__ w,
                                                      const float* __restrict__ bias, int64_t tokens,
                                                      int d_model, int n_experts, int top_k, int mode,
                                                      float rsf, float* __restrict__ logits,
                                                      int32_t* __restrict__ top_idx,
                                                      float* __restrict__ gates) {
-  __shared__ double xs_lds[kTokPerBlock][kDChunk + 1];
-  __shared__ double w_lds[kDChunk][64 * EPL];
+  constexpr int kNP = RouterLds<NT>::kNP;
+  constexpr int kEPL = (kNP + 63) / 64;
+  constexpr int kXPer = kRTokBlk * kRDc / 256;        // x elements per thread per chunk (8)
+  constexpr int kWPer = (kRDc * kNP + 255) / 256;     // w elements per thread per chunk
+  __shared__ RouterLds<NT> lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTokPerBlock;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRTokBlk;
 
-  double acc[kTokPerWave][EPL];
+  // Staging assignment: x element (tt, dd) = (tid / 4, (tid % 4) * 8 + q).
+  const int xs_tt = tid >> 2;
+  const int xs_dd = (tid & 3) * 8;
+  const int64_t xs_row = (t0 + xs_tt < tokens ? t0 + xs_tt : tokens - 1) * static_cast<int64_t>(d_model);
+  float xr[kXPer];
+  float wr[kWPer];
+  auto fetch = [&](int d0) {
 #pragma unroll
-  for (int t = 0; t < kTokPerWave; ++t)
+    for (int q = 0; q < kXPer; ++q) {
+      const int d = d0 + xs_dd + q;
+      xr[q] = d < d_model ? load_as_f32(x, xs_row + d) : 0.0f;
+    }
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) acc[t][j] = 0.0;
+    for (int q = 0; q < kWPer; ++q) {
+      const int idx = q * 256 + tid;
+      const int dd = idx / kNP, e = idx % kNP;
+      const int d = d0 + dd;
+      wr[q] = (idx < kRDc * kNP && e < n_experts && d < d_model)
+                  ? load_as_f32(w, static_cast<int64_t>(d) * n_experts + e)
+                  : 0.0f;
+    }
+  };
+  auto park = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < kXPer; ++q) lds.x[buf][xs_tt][xs_dd + q] = xr[q];
+#pragma unroll
+    for (int q = 0; q < kWPer; ++q) {
+      const int idx = q * 256 + tid;
+      if (idx < kRDc * kNP) lds.w[buf][idx / kNP][idx % kNP] = wr[q];
+    }
+  };
 
-  for (int d0 = 0; d0 < d_model; d0 += kDChunk) {
-    __syncthreads();
-    for (int i = tid; i < kTokPerBlock * kDChunk; i += 256) {
-      const int tt = i / kDChunk, dd = i % kDChunk;
-      const int64_t t = t0 + tt;
-      const int d = d0 + dd;
-      xs_lds[tt][dd] = (t < tokens && d < d_model) ? load_as_f64(x, t * d_model + d) : 0.0;
-    }
-    for (int i = tid; i < kDChunk * 64 * EPL; i += 256) {
-      const int dd = i / (64 * EPL), e = i % (64 * EPL);
-      const int d = d0 + dd;
-      w_lds[dd][e] = (e < n_experts && d < d_model)
-                         ? load_as_f64(w, static_cast<int64_t>(d) * n_experts + e)
-                         : 0.0;
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int dd = 0; dd < kDChunk; ++dd) {
-      double wv[EPL];
+  f64x4 acc[NT];
 #pragma unroll
-      for (int j = 0; j < EPL; ++j) wv[j] = w_lds[dd][lane + 64 * j];
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int t = 0; t < kTokPerWave; ++t) {
-        const double xv = xs_lds[wave * kTokPerWave + t][dd];
+    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0;
+
+  const int a_row = wave * kRTokWave + (lane & 15);
+  const int k_of_lane = lane >> 4;
+  const int nchunks = (d_model + kRDc - 1) / kRDc;
+  fetch(0);
+  park(0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nchunks) fetch((c + 1) * kRDc);
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) acc[t][j] = __builtin_fma(xv, wv[j], acc[t][j]);
+    for (int s = 0; s < kRDc / 4; ++s) {
+      const double a = static_cast<double>(lds.x[buf][a_row][4 * s + k_of_lane]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const double b = static_cast<double>(lds.w[buf][4 * s + k_of_lane][t * 16 + (lane & 15)]);
+        acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
       }
     }
+    if (c + 1 < nchunks) park(buf ^ 1);
+    __syncthreads();
   }
 
-#pragma unroll 1
-  for (int t = 0; t < kTokPerWave; ++t) {
-    const int64_t tok = t0 + wave * kTokPerWave + t;
-    if (tok >= tokens) break;
-    float l[EPL];
+  // Logits (float32) of this wave's 16 tokens into LDS, row = token, col = expert.
+  float* lg = &lds.w[0][0][0];  // kRTokBlk x kNP floats fit in the two W stages
+  static_assert(sizeof(float) * kRTokBlk * kNP <= sizeof(lds.w), "logit staging does not fit");
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      l[j] = static_cast<float>(acc[t][j]);
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      lg[(wave * kRTokWave + (lane >> 4) + 4 * r) * kNP + t * 16 + (lane & 15)] =
+          static_cast<float>(acc[t][r]);
+  __syncthreads();
+
+#pragma unroll 1
+  for (int i = 0; i < kRTokWave; ++i) {
+    const int64_t tok = t0 + wave * kRTokWave + i;
+    if (tok >= tokens) break;
+    float l[kEPL];
+#pragma unroll
+    for (int j = 0; j < kEPL; ++j) {
       const int e = lane + 64 * j;
+      l[j] = e < kNP ? lg[(wave * kRTokWave + i) * kNP + e] : 0.0f;
       if (e < n_experts) logits[tok * n_experts + e] = l[j];
     }
-    select_and_gate<EPL>(l, bias, n_experts, top_k, mode, rsf, top_idx + tok * top_k,
-                         gates + tok * top_k);
+    select_and_gate<kEPL>(l, bias, n_experts, top_k, mode, rsf, top_idx + tok * top_k,
+                          gates + tok * top_k);
   }
 }
 
@@ -191,28 +249,28 @@ __global__ __launch_bounds__(256) void select_kernel(const float* __restrict__ l
                        gates + tok * top_k);
 }
 
-template <int EPL, typename XT, typename WT>
+template <int NT, typename XT, typename WT>
 void launch_router(const void* x, const void* w, const float* bias, int64_t tokens, int d_model,
                    int n_experts, int top_k, int mode, float rsf, float* logits, int32_t* top_idx,
                    float* gates, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, kTokPerBlock)));
-  hipLaunchKernelGGL((router_kernel<EPL, XT, WT>), grid, dim3(256), 0, stream,
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, kRTokBlk)));
+  hipLaunchKernelGGL((router_kernel<NT, XT, WT>), grid, dim3(256), 0, stream,
                      static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
                      n_experts, top_k, mode, rsf, logits, top_idx, gates);
 }
 
-template <int EPL>
+template <int NT>
 void dispatch_router(int x_dtype, int w_dtype, const void* x, const void* w, const float* bias,
                      int64_t tokens, int d_model, int n_experts, int top_k, int mode, float rsf,
                      float* logits, int32_t* top_idx, float* gates, hipStream_t s) {
   if (x_dtype == HMOE_BF16 && w_dtype == HMOE_F32)
-    launch_router<EPL, uint16_t, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, uint16_t, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   else if (x_dtype == HMOE_F32 && w_dtype == HMOE_F32)
-    launch_router<EPL, float, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, float, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   else if (x_dtype == HMOE_BF16 && w_dtype == HMOE_BF16)
-    launch_router<EPL, uint16_t, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, uint16_t, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   else
-    launch_router<EPL, float, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, float, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
 }
 
 int validate_routing(int64_t tokens, int n_experts, int top_k, int mode) {
@@ -242,12 +300,17 @@ extern "C" int hmoe_router(const void* x, int x_dtype, const void* router_w, int
   if (tokens == 0) return HMOE_OK;
   HMOE_REQUIRE(x && router_w && logits && top_idx && gates, "router: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (n_experts <= 64)
-    dispatch_router<1>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, routed_scaling_factor, logits, top_idx, gates, s);
+  const float rsf = routed_scaling_factor;
+  if (n_experts <= 16)
+    dispatch_router<1>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+  else if (n_experts <= 32)
+    dispatch_router<2>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+  else if (n_experts <= 64)
+    dispatch_router<4>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   else if (n_experts <= 128)
-    dispatch_router<2>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, routed_scaling_factor, logits, top_idx, gates, s);
+    dispatch_router<8>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   else
-    dispatch_router<4>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, routed_scaling_factor, logits, top_idx, gates, s);
+    dispatch_router<16>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   return check_launch("hmoe_router");
 }
 
