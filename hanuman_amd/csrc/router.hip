@@ -87,14 +87,36 @@ __device__ __forceinline__ void select_and_gate(const float (&logit)[EPL], const
   }
 }
 
+// Eight consecutive activations as raw bits (one or two 16-byte loads; the
+// address must be 16-byte aligned), widened to float32 later.
 template <typename XT>
-__device__ __forceinline__ float load_as_f32(const XT* p, int64_t i);
+struct X8;
 template <>
-__device__ __forceinline__ float load_as_f32<float>(const float* p, int64_t i) {
+struct X8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
+};
+template <>
+struct X8<uint16_t> {
+  u32x4 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ float get(int i) const {
+    const uint32_t u = v[i >> 1];
+    return __uint_as_float((i & 1) ? (u & 0xffff0000u) : (u << 16));
+  }
+};
+template <typename WT>
+__device__ __forceinline__ float load_w_f32(const WT* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_w_f32<float>(const float* p, int64_t i) {
   return p[i];
 }
 template <>
-__device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p, int64_t i) {
+__device__ __forceinline__ float load_w_f32<uint16_t>(const uint16_t* p, int64_t i) {
   return bf16_bits_to_f32(p[i]);
 }
 
@@ -142,35 +164,41 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   const int wave = tid >> 6;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRTokBlk;
 
-  // Staging assignment: x element (tt, dd) = (tid / 4, (tid % 4) * 8 + q).
+  // Staging assignment: x elements (tt, dd..dd+7) = (tid / 4, (tid % 4) * 8).
+  // d_model is a multiple of 8, so a group of 8 is wholly inside or outside
+  // the row.  Every load is unconditional from an in-range address (clamped
+  // token row, d or expert 0) and masked afterwards, so the loads of a chunk
+  // stay in flight together until they are parked in LDS.
+  static_assert(kXPer == 8, "x staging assumes eight activations per thread");
   const int xs_tt = tid >> 2;
   const int xs_dd = (tid & 3) * 8;
   const int64_t xs_row = (t0 + xs_tt < tokens ? t0 + xs_tt : tokens - 1) * static_cast<int64_t>(d_model);
-  float xr[kXPer];
+  X8<XT> xr;
   float wr[kWPer];
-  auto fetch = [&](int d0) {
-#pragma unroll
-    for (int q = 0; q < kXPer; ++q) {
-      const int d = d0 + xs_dd + q;
-      xr[q] = d < d_model ? load_as_f32(x, xs_row + d) : 0.0f;
-    }
-#pragma unroll
-    for (int q = 0; q < kWPer; ++q) {
-      const int idx = q * 256 + tid;
-      const int dd = idx / kNP, e = idx % kNP;
-      const int d = d0 + dd;
-      wr[q] = (idx < kRDc * kNP && e < n_experts && d < d_model)
-                  ? load_as_f32(w, static_cast<int64_t>(d) * n_experts + e)
-                  : 0.0f;
-    }
+  auto w_ok = [&](int q, int d0) {
+    const int idx = q * 256 + tid;
+    return idx < kRDc * kNP && idx % kNP < n_experts && d0 + idx / kNP < d_model;
   };
-  auto park = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < kXPer; ++q) lds.x[buf][xs_tt][xs_dd + q] = xr[q];
+  auto fetch = [&](int d0) {
+    const int dx = d0 + xs_dd;
+    xr.load(x + xs_row + (dx < d_model ? dx : 0));
 #pragma unroll
     for (int q = 0; q < kWPer; ++q) {
       const int idx = q * 256 + tid;
-      if (idx < kRDc * kNP) lds.w[buf][idx / kNP][idx % kNP] = wr[q];
+      const int64_t off = static_cast<int64_t>(d0 + idx / kNP) * n_experts + idx % kNP;
+      wr[q] = load_w_f32(w, w_ok(q, d0) ? off : 0);
+    }
+    // Keep the loads ahead of the MFMAs; the masking happens in park().
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto park = [&](int buf, int d0) {
+    const bool x_ok = d0 + xs_dd < d_model;
+#pragma unroll
+    for (int q = 0; q < kXPer; ++q) lds.x[buf][xs_tt][xs_dd + q] = x_ok ? xr.get(q) : 0.0f;
+#pragma unroll
+    for (int q = 0; q < kWPer; ++q) {
+      const int idx = q * 256 + tid;
+      if (idx < kRDc * kNP) lds.w[buf][idx / kNP][idx % kNP] = w_ok(q, d0) ? wr[q] : 0.0f;
     }
   };
 
@@ -184,7 +212,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   const int k_of_lane = lane >> 4;
   const int nchunks = (d_model + kRDc - 1) / kRDc;
   fetch(0);
-  park(0);
+  park(0, 0);
   __syncthreads();
   for (int c = 0; c < nchunks; ++c) {
     const int buf = c & 1;
@@ -198,7 +226,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
         acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
       }
     }
-    if (c + 1 < nchunks) park(buf ^ 1);
+    if (c + 1 < nchunks) park(buf ^ 1, (c + 1) * kRDc);
     __syncthreads();
   }
 
@@ -294,7 +322,8 @@ extern "C" int hmoe_router(const void* x, int x_dtype, const void* router_w, int
                            int32_t* top_idx, float* gates, hmoe_stream_t stream) {
   using namespace hmoe;
   if (int rc = validate_routing(tokens, n_experts, top_k, mode)) return rc;
-  HMOE_REQUIRE(d_model >= 1, "router: d_model must be >= 1 (got %d)", d_model);
+  HMOE_REQUIRE(d_model >= 8 && d_model % 8 == 0,
+               "router: d_model must be a positive multiple of 8 (got %d)", d_model);
   HMOE_REQUIRE(x_dtype == HMOE_F32 || x_dtype == HMOE_BF16, "router: x dtype must be F32 or BF16");
   HMOE_REQUIRE(w_dtype == HMOE_F32 || w_dtype == HMOE_BF16, "router: weight dtype must be F32 or BF16");
   if (tokens == 0) return HMOE_OK;
