@@ -34,26 +34,37 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+FP64_PEAK_TFLOPS = 78.6       # MI355X dense fp64 MFMA
+
+
 def algorithmic(wl, kept_rows: int) -> dict:
-    """Per-launch algorithmic work of each stage (bytes or FLOP)."""
+    """Per-launch algorithmic work of each stage: (bound, amount, peak)."""
     T, D, N, K, F = wl.tokens, wl.d_model, wl.n_experts, wl.top_k, wl.d_ff
     R = T * K
-    ex = 2  # bf16 activations
+    fp8 = wl.expert_dtype == "fp8"
+    ex = 1 if fp8 else 2  # dispatched activation bytes
     x_in = 4 if wl.x_dtype == "f32" else 2
     out_b = 4 if wl.out_dtype == "f32" else 2
+    w_b = 2 if wl.router_w_dtype == "bf16" else 4
+    mfma_peak = FP8_PEAK_TFLOPS if fp8 else BF16_PEAK_TFLOPS
     w = {}
     if wl.router_from_logits:
-        w["router"] = ("hbm", T * N * 4 + T * K * 8)
+        w["router"] = ("hbm", T * N * 4 + T * K * 8, HBM_PEAK_GBS)
     else:
-        w["router"] = ("hbm", T * D * x_in + D * N * 4 + T * N * 4 + T * K * 8)
-    w["plan"] = ("hbm", 2 * R * 4 + R * 4 + R * 4 + R + N * 8)
-    # dispatch: read every token once, write the kept rows, read the slot map
-    w["permute"] = ("hbm", T * D * x_in + kept_rows * D * ex + R * 4)
+        # float64 matrix-core dot products (the bit-exact logit recipe)
+        w["router"] = ("fp64", 2 * T * D * N, FP64_PEAK_TFLOPS)
+    w["plan"] = ("hbm", 2 * R * 4 + R * 4 + R * 4 + R + N * 8, HBM_PEAK_GBS)
+    # dispatch: read every token once, write the kept rows (+ scales), read the slot map
+    w["permute"] = ("hbm", T * D * x_in + kept_rows * (D * ex + (4 if fp8 else 0)) + R * 4,
+                    HBM_PEAK_GBS)
     if wl.expert == "swiglu":
-        w["gate_up"] = ("mfma", 2 * 2 * kept_rows * D * F)
-        w["down"] = ("mfma", 2 * kept_rows * F * D)
-    # combine: read kept rows, write tokens, read slot map and gates
-    w["combine"] = ("hbm", kept_rows * D * ex + T * D * out_b + R * 8)
+        w["gate_up"] = ("mfma", 2 * 2 * kept_rows * D * F, mfma_peak)
+        if fp8:
+            # h (bf16) read once, codes and row scales written
+            w["quant_h"] = ("hbm", kept_rows * F * 2 + kept_rows * F + kept_rows * 4, HBM_PEAK_GBS)
+        w["down"] = ("mfma", 2 * kept_rows * F * D, mfma_peak)
+    # combine: read kept rows (bf16), write tokens, read slot map and gates
+    w["combine"] = ("hbm", kept_rows * D * 2 + T * D * out_b + R * 8, HBM_PEAK_GBS)
     return w
 
 
@@ -81,10 +92,12 @@ def cpu_baseline(wl_name: str, sample_tokens: int, seed: int) -> dict:
                                capture_output=True, text=True, timeout=10).stdout.split(":")[-1].strip()
     except Exception:  # noqa: BLE001 -- informational only
         model = "unknown"
+    note = (" (float32 experts: the e4m3 expert path has no CPU-native form)"
+            if wl.expert_dtype == "fp8" else "")
     return {"value": round(wl.tokens / t, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": (f"{wl.tokens} tokens of the {wl_name} layer (same shape, seed {seed}), "
-                       f"NumPy float32 restatement of model/moe.py with OpenBLAS, median of 3 "
-                       f"after 1 warm-up, {cores} threads, CPU {model}")}
+                       f"NumPy float32 restatement of model/moe.py with OpenBLAS{note}, median "
+                       f"of 3 after 1 warm-up, {cores} threads, CPU {model}")}
 
 
 def main():
@@ -120,36 +133,47 @@ def main():
     del inp
     torch.cuda.synchronize()
 
-    stages = ["router", "plan", "permute"] + (["gate_up", "down"] if wl.expert == "swiglu" else []) + ["combine"]
+    fp8 = wl.expert_dtype == "fp8"
+    stages = ["router", "plan", "permute"]
+    if wl.expert == "swiglu":
+        stages += ["gate_up", "quant_h", "down"] if fp8 else ["gate_up", "down"]
+    stages += ["combine"]
 
     def step(ev=None):
         """One layer forward; with ``ev`` records an event after each stage."""
         import hanuman_amd.kernels as K
-        if ev is not None:
-            ev[0].record()
+        marks = iter(ev) if ev is not None else None
+
+        def mark():
+            if marks is not None:
+                next(marks).record()
+
+        mark()
         logits, top_idx, gates = layer.route()
-        if ev is not None:
-            ev[1].record()
+        mark()
         plan = K.dispatch_plan(top_idx, wl.n_experts, layer.capacity, layer.workspace)
-        if ev is not None:
-            ev[2].record()
-        xs = K.permute_rows(layer.x, plan, torch.bfloat16)
-        if ev is not None:
-            ev[3].record()
-        i = 4
-        if wl.expert == "swiglu":
-            h = K.grouped_gate_up(xs, plan.offsets, layer.w_gate_up)
-            if ev is not None:
-                ev[i].record()
-            ys = K.grouped_down(h, plan.offsets, layer.w_down)
-            if ev is not None:
-                ev[i + 1].record()
-            i += 2
+        mark()
+        if fp8:
+            xs_q, xs_s = K.permute_rows_fp8(layer.x, plan)
+            mark()
+            h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, layer.w_gate_up, layer.w_gate_up_scale)
+            mark()
+            h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
+            mark()
+            ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, layer.w_down, layer.w_down_scale)
+            mark()
         else:
-            ys = xs
+            xs = K.permute_rows(layer.x, plan, torch.bfloat16)
+            mark()
+            if wl.expert == "swiglu":
+                h = K.grouped_gate_up(xs, plan.offsets, layer.w_gate_up)
+                mark()
+                ys = K.grouped_down(h, plan.offsets, layer.w_down)
+                mark()
+            else:
+                ys = xs
         out = K.combine(ys, plan, gates, None, layer.out_dtype)
-        if ev is not None:
-            ev[i].record()
+        mark()
         return plan, out
 
     for _ in range(args.warmup):
@@ -176,24 +200,26 @@ def main():
     work = algorithmic(wl, kept)
     kernels = {}
     for st in stages:
-        kind, amount = work[st]
+        kind, amount, peak = work[st]
         t = stage_ms[st] / 1e3
         if kind == "hbm":
             ach = amount / t / 1e9
             kernels[st] = {"ms": round(stage_ms[st], 4), "bound": "hbm", "achieved": round(ach, 1),
-                           "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "bytes": amount}
+                           "unit": "GB/s", "peak": peak, "frac": round(ach / peak, 4), "bytes": amount}
         else:
             ach = amount / t / 1e12
-            kernels[st] = {"ms": round(stage_ms[st], 4), "bound": "mfma", "achieved": round(ach, 1),
-                           "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "flop": amount}
+            kernels[st] = {"ms": round(stage_ms[st], 4), "bound": kind, "achieved": round(ach, 1),
+                           "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4),
+                           "flop": amount}
     tokens_per_s = wl.tokens / (ms_per_step / 1e3)
     if wl.expert == "swiglu":
         flop = work["gate_up"][1] + work["down"][1]
+        peak = work["gate_up"][2]
         t_gemm = (stage_ms["gate_up"] + stage_ms["down"]) / 1e3
         ach = flop / t_gemm / 1e12
         roofline = {"kernel": "grouped_gemm_kernel (gate/up + down)", "bound": "mfma",
-                    "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                    "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
+                    "frac": round(ach / peak, 4), "traffic": None,
                     "flop_per_launch": flop, "ms": round(t_gemm * 1e3, 4)}
     else:
         b = work["permute"][1] + work["combine"][1]
@@ -225,7 +251,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8-e4m3" if fp8 else "bf16",
         "data": "synthetic (seeded normal inputs and weights, fixed draw order)",
         "config": {"workload": name, "tokens": wl.tokens, "d_model": wl.d_model,
                    "n_experts": wl.n_experts, "top_k": wl.top_k, "d_ff": wl.d_ff,

@@ -233,8 +233,137 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const TI* __restrict_
   }
 }
 
+// ------------------------------------------------------- e4m3 quantisation --
+// Per-row rule: amax = max |v| over the row, codes e4m3(clamp(v * (448/amax),
+// +-448)) rounded to nearest even by v_cvt_pk_fp8_f32, dequantisation scale
+// amax/448 (both divisions correctly rounded); an all-zero row gets scale 1.
+constexpr float kE4m3Max = 448.0f;
+
+template <typename TI>
+__device__ __forceinline__ void wave_row_scales(const TI* __restrict__ row, int chunks, float& s,
+                                                float& inv) {
+  const int lane = threadIdx.x & 63;
+  float amax = 0.0f;
+  for (int c = lane; c < chunks; c += 64) {
+    Chunk8<TI> v;
+    v.load(row + static_cast<int64_t>(c) * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v.get(i)));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  s = amax > 0.0f ? amax / kE4m3Max : 1.0f;
+  inv = amax > 0.0f ? kE4m3Max / amax : 1.0f;
+}
+
+template <typename TI>
+__device__ __forceinline__ uint2 quant8_e4m3(const Chunk8<TI>& v, float inv) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v.get(i) * inv, -kE4m3Max), kE4m3Max);
+  uint2 out;
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  out.x = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w, true));
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+  out.y = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], w, true));
+  return out;
+}
+
+// One wave per token: quantise the row once and write it to every kept slot.
+template <typename TI>
+__global__ __launch_bounds__(256) void permute_rows_fp8_kernel(
+    const TI* __restrict__ x, int64_t tokens, int d_model, int top_k,
+    const int32_t* __restrict__ slot_pos, uint8_t* __restrict__ xs_q, float* __restrict__ xs_scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  const int32_t my_pos = lane < top_k ? slot_pos[t * top_k + lane] : -1;
+  const int chunks = d_model / 8;
+  const TI* src = x + t * d_model;
+  float s, inv;
+  wave_row_scales(src, chunks, s, inv);
+  if (lane < top_k && my_pos >= 0) xs_scale[my_pos] = s;
+  // Wave-uniform loop: every lane takes part in the slot broadcasts.
+  for (int c0 = 0; c0 < chunks; c0 += 64) {
+    const int c = c0 + lane;
+    const bool ok = c < chunks;
+    Chunk8<TI> v;
+    v.load(src + static_cast<int64_t>(ok ? c : 0) * 8);
+    const uint2 q = quant8_e4m3(v, inv);
+    for (int k = 0; k < top_k; ++k) {
+      const int32_t pos = __shfl(my_pos, k, 64);
+      if (pos >= 0 && ok)
+        *reinterpret_cast<uint2*>(xs_q + static_cast<int64_t>(pos) * d_model + c * 8) = q;
+    }
+  }
+}
+
+// One wave per row of a bf16 matrix; rows at or past offsets[n_experts] (when
+// given) are skipped.
+__global__ __launch_bounds__(256) void quantize_rows_fp8_kernel(
+    const uint16_t* __restrict__ a, int64_t rows, int cols, const int32_t* __restrict__ offsets,
+    int n_experts, uint8_t* __restrict__ q, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  if (offsets != nullptr && r >= offsets[n_experts]) return;
+  const int chunks = cols / 8;
+  const uint16_t* src = a + r * cols;
+  float s, inv;
+  wave_row_scales(src, chunks, s, inv);
+  if (lane == 0) scale[r] = s;
+  for (int c = lane; c < chunks; c += 64) {
+    Chunk8<uint16_t> v;
+    v.load(src + static_cast<int64_t>(c) * 8);
+    *reinterpret_cast<uint2*>(q + r * cols + c * 8) = quant8_e4m3(v, inv);
+  }
+}
+
 }  // namespace
 }  // namespace hmoe
+
+extern "C" int hmoe_permute_rows_fp8(const void* x, int x_dtype, int64_t tokens, int d_model,
+                                     int top_k, const int32_t* slot_pos, uint8_t* xs_q,
+                                     float* xs_scale, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(tokens >= 0 && top_k >= 1 && top_k <= 64,
+               "permute_rows_fp8: need tokens >= 0 and 1 <= top_k <= 64");
+  HMOE_REQUIRE(d_model >= 8 && d_model % 8 == 0,
+               "permute_rows_fp8: d_model must be a multiple of 8 (got %d)", d_model);
+  HMOE_REQUIRE(x_dtype == HMOE_F32 || x_dtype == HMOE_BF16,
+               "permute_rows_fp8: x dtype must be F32 or BF16");
+  if (tokens == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && slot_pos && xs_q && xs_scale, "permute_rows_fp8: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4)));
+  if (x_dtype == HMOE_BF16)
+    hipLaunchKernelGGL(permute_rows_fp8_kernel<uint16_t>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), tokens, d_model, top_k, slot_pos, xs_q,
+                       xs_scale);
+  else
+    hipLaunchKernelGGL(permute_rows_fp8_kernel<float>, grid, dim3(256), 0, s,
+                       static_cast<const float*>(x), tokens, d_model, top_k, slot_pos, xs_q,
+                       xs_scale);
+  return check_launch("hmoe_permute_rows_fp8");
+}
+
+extern "C" int hmoe_quantize_rows_fp8(const void* a, int64_t rows, int cols,
+                                      const int32_t* offsets, int n_experts, uint8_t* q,
+                                      float* scale, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(rows >= 0, "quantize_rows_fp8: rows must be >= 0");
+  HMOE_REQUIRE(cols >= 8 && cols % 8 == 0,
+               "quantize_rows_fp8: cols must be a multiple of 8 (got %d)", cols);
+  HMOE_REQUIRE(offsets == nullptr || n_experts >= 1,
+               "quantize_rows_fp8: n_experts must be >= 1 with offsets");
+  if (rows == 0) return HMOE_OK;
+  HMOE_REQUIRE(a && q && scale, "quantize_rows_fp8: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(quantize_rows_fp8_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))),
+                     dim3(256), 0, s, static_cast<const uint16_t*>(a), rows, cols, offsets,
+                     n_experts, q, scale);
+  return check_launch("hmoe_quantize_rows_fp8");
+}
 
 extern "C" size_t hmoe_plan_workspace_bytes(int64_t tokens, int top_k, int n_experts) {
   if (tokens <= 0 || top_k <= 0 || n_experts <= 0) return 0;

@@ -108,11 +108,60 @@ __device__ __forceinline__ void decode_tile(int t, int n_tiles_n, const int32_t*
   n0 = n_tile * kBN;
 }
 
-template <bool SWIGLU>
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// Element-type traits: bf16 (32x32x16 MFMA, 64 elements = 128 bytes per LDS
+// row per K step, 4 sub-steps) or OCP e4m3 (32x32x64 MFMA at unit block
+// scales, 128 elements per K step, 2 sub-steps).  Either way a K step moves
+// 128 bytes of every A and B row, so the LDS layout and the DMA are the same.
+template <bool FP8>
+struct GemmElem;
+template <>
+struct GemmElem<false> {
+  static constexpr int kBytes = 2;
+  static constexpr int kSub = 4;
+  typedef bf16x8 frag_t;
+  // Lane L, sub-step s: row L&31, 16-byte chunk 2s + L/32.
+  __device__ static frag_t read(const uint8_t* base, int row_byte, int row, int s, int half) {
+    return *reinterpret_cast<const bf16x8*>(base + row_byte + (((2 * s + half) ^ (row & 7)) * 16));
+  }
+  __device__ static f32x16 mfma(const frag_t& b, const frag_t& a, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
+  }
+};
+template <>
+struct GemmElem<true> {
+  static constexpr int kBytes = 1;
+  static constexpr int kSub = 2;
+  typedef i32x8 frag_t;
+  // Lane L, sub-step s: row L&31, 32 bytes = chunks 4s + 2(L/32) and the next.
+  __device__ static frag_t read(const uint8_t* base, int row_byte, int row, int s, int half) {
+    const int c0 = 4 * s + 2 * half;
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(base + row_byte + ((c0 ^ (row & 7)) * 16));
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(base + row_byte + (((c0 + 1) ^ (row & 7)) * 16));
+    frag_t f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[i] = static_cast<int>(lo[i]);
+      f[4 + i] = static_cast<int>(hi[i]);
+    }
+    return f;
+  }
+  __device__ static f32x16 mfma(const frag_t& b, const frag_t& a, const f32x16& c) {
+    // Format 0 = e4m3 for both operands; E8M0 block scales 127 = 1.0.
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+
+// With FP8, a_scale [a_rows] and b_scale [n_experts * ncols] dequantise the
+// float32 accumulators in the epilogue (before the SwiGLU).
+template <bool SWIGLU, bool FP8>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+    const float* __restrict__ a_scale, const float* __restrict__ b_scale,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
     uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n) {
+  typedef GemmElem<FP8> E;
   // The two stages live in dynamic LDS.  With a static array the compiler
   // cannot tell the stage being loaded from the stage being read and waits
   // for every DMA load before the next LDS read; the stage protocol below
@@ -135,7 +184,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
   const int hi = static_cast<int>((static_cast<int64_t>(total) * (xcd + 1)) / kNumXcd);
   const int first = lo + slot;
   if (first >= hi) return;  // uniform per workgroup
-  const int ktiles = kdim / kBK;
+  const int row_bytes = kdim * E::kBytes;
+  const int ksteps = row_bytes / 128;
 
   // ---- global -> LDS loads ------------------------------------------------
   // Round i (0..7) of a stage: this thread fills 16-byte slot i*256 + tid,
@@ -144,10 +194,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
   // 1 KB of contiguous LDS.
   const int ld_r = tid >> 3;
   const int ld_c = (tid & 7) ^ (ld_r & 7);
-  const uint32_t b_off0 = static_cast<uint32_t>(ld_r * kdim + ld_c * 8) * 2u;
+  const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
   uint32_t a_off[8];
-  const uint16_t* a_tile = A;
-  const uint16_t* b_tile = B;
+  const uint8_t* a_tile = A;
+  const uint8_t* b_tile = B;
   auto set_load_tile = [&](int t) {
     int e, n0;
     int64_t row0, row_end;
@@ -155,8 +205,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
-    a_tile = A + static_cast<int64_t>(r0) * kdim;
-    b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * kdim;
+    a_tile = A + static_cast<int64_t>(r0) * row_bytes;
+    b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes;
     // Rows past the buffer (the last tile of the last segment) are clamped to
     // its last row; their results are never stored.
     const int64_t lim = a_rows - 1 - r0;
@@ -164,68 +214,67 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     for (int i = 0; i < 8; ++i) {
       int rr = i * 32 + ld_r;
       rr = rr < lim ? rr : static_cast<int>(lim);
-      a_off[i] = static_cast<uint32_t>(rr * kdim + ld_c * 8) * 2u;
+      a_off[i] = static_cast<uint32_t>(rr * row_bytes + ld_c * 16);
     }
   };
-  // Part p (0..3) issues rounds 2p and 2p+1 of A and of B for K offset k0.
-  auto issue_loads = [&](int stage, int k0, int part) {
+  // Part p (0..3) issues rounds 2p and 2p+1 of A and of B for K step kb.
+  auto issue_loads = [&](int stage, int kb, int part) {
     uint8_t* base = smem + stage * kStageBytes;
-    const uint8_t* ab = reinterpret_cast<const uint8_t*>(a_tile + k0);
-    const uint8_t* bb = reinterpret_cast<const uint8_t*>(b_tile + k0);
+    const uint8_t* ab = a_tile + kb * 128;
+    const uint8_t* bb = b_tile + kb * 128;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int i = part * 2 + q;
       __builtin_amdgcn_global_load_lds(ab + a_off[i], (lds_ptr_t)(base + i * 4096 + wave * 1024),
                                        16, 0, 0);
-      __builtin_amdgcn_global_load_lds(bb + b_off0 + static_cast<uint32_t>(i * 32 * kdim * 2),
+      __builtin_amdgcn_global_load_lds(bb + b_off0 + static_cast<uint32_t>(i * 32 * row_bytes),
                                        (lds_ptr_t)(base + 32768 + i * 4096 + wave * 1024), 16, 0,
                                        0);
     }
   };
 
   // ---- MFMA fragments -------------------------------------------------------
-  // v_mfma_f32_32x32x16_bf16 operand: lane L holds row L&31, K chunk
-  // (2s + L/32) of sub-step s.  Fragment i of the wave's 128 rows is 32 rows
-  // (4096 bytes) further down.  The weight fragment is the first operand, so
-  // an accumulator lane holds one token row and groups of four consecutive
-  // output columns.
+  // The weight fragment is the first MFMA operand, so an accumulator lane
+  // holds one token row and groups of four consecutive output columns.
+  // Fragment i of the wave's 128 rows is 32 rows (4096 bytes) further down.
   const int wm = wave >> 1, wn = wave & 1;
   const int frow = lane & 31;
   const int fhalf = lane >> 5;
-  int fa_addr[4], fb_addr[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int cpos = ((2 * s + fhalf) ^ (frow & 7)) * 16;
-    fa_addr[s] = (wm * 128 + frow) * 128 + cpos;
-    fb_addr[s] = 32768 + (wn * 128 + frow) * 128 + cpos;
-  }
-  bf16x8 fa[2][4], fb[2][4];
+  const int fa_row = wm * 128 + frow;
+  const int fb_row = wn * 128 + frow;
+  typename E::frag_t fa[2][4], fb[2][4];
   auto read_frags = [&](int buf, int stage, int s) {
     const uint8_t* base = smem + stage * kStageBytes;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fa[buf][i] = *reinterpret_cast<const bf16x8*>(base + fa_addr[s] + i * 4096);
-      fb[buf][i] = *reinterpret_cast<const bf16x8*>(base + fb_addr[s] + i * 4096);
+      fa[buf][i] = E::read(base, (fa_row + 32 * i) * 128, fa_row, s, fhalf);
+      fb[buf][i] = E::read(base + 32768, (fb_row + 32 * i) * 128, fb_row, s, fhalf);
     }
   };
   f32x16 acc[4][4];
 
   // One K step on stage `cur`: loads for the next step into stage cur^1 (when
-  // `load`), fragment double-buffering, 64 MFMAs, then a barrier (which also
+  // `load`; the four load parts are spread over the sub-steps), fragment
+  // double-buffering, 64 (bf16) or 32 (fp8) MFMAs, then a barrier (which also
   // waits for this thread's DMA loads).
   int cur = 0;
-  auto kstep = [&](bool load, int ld_k0) {
+  auto kstep = [&](bool load, int ld_kb) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (load) issue_loads(cur ^ 1, ld_k0, s);
-      if (s < 3) read_frags((s + 1) & 1, cur, s + 1);
+    for (int s = 0; s < E::kSub; ++s) {
+      if (load) {
+        if (E::kSub == 4) {
+          issue_loads(cur ^ 1, ld_kb, s);
+        } else {
+          issue_loads(cur ^ 1, ld_kb, 2 * s);
+          issue_loads(cur ^ 1, ld_kb, 2 * s + 1);
+        }
+      }
+      if (s + 1 < E::kSub) read_frags((s + 1) & 1, cur, s + 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s & 1][j], fa[s & 1][i], acc[i][j],
-                                                              0, 0, 0);
+        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
@@ -245,8 +294,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    for (int kt = 0; kt + 1 < ktiles; ++kt) {
-      kstep(true, (kt + 1) * kBK);
+    for (int kb = 0; kb + 1 < ksteps; ++kb) {
+      kstep(true, kb + 1);
       read_frags(0, cur ^ 1, 0);
       cur ^= 1;
     }
@@ -264,6 +313,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
       const int64_t row = row0 + wm * 128 + i * 32 + frow;
       if (row < row_end) {
         uint16_t* crow = C + row * ldc;
+        const float sa = FP8 ? a_scale[row] : 1.0f;
+        const float* sb = FP8 ? b_scale + static_cast<int64_t>(e) * ncols + n0 + wn * 128 + col_lane : nullptr;
         if (SWIGLU) {
           const int hbase = (n0 + wn * 128) / 2;
 #pragma unroll
@@ -272,8 +323,15 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
             for (int g = 0; g < 4; ++g) {
               float h[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q)
-                h[q] = silu_f32(acc[i][2 * p][g * 4 + q]) * acc[i][2 * p + 1][g * 4 + q];
+              for (int q = 0; q < 4; ++q) {
+                float gv = acc[i][2 * p][g * 4 + q];
+                float uv = acc[i][2 * p + 1][g * 4 + q];
+                if (FP8) {
+                  gv = gv * sa * sb[(2 * p) * 32 + g * 8 + q];
+                  uv = uv * sa * sb[(2 * p + 1) * 32 + g * 8 + q];
+                }
+                h[q] = silu_f32(gv) * uv;
+              }
               uint2 pk;
               pk.x = pack_bf16x2_rne(h[0], h[1]);
               pk.y = pack_bf16x2_rne(h[2], h[3]);
@@ -285,9 +343,15 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
           for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
+              float v[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                v[q] = acc[i][j][g * 4 + q];
+                if (FP8) v[q] = v[q] * sa * sb[j * 32 + g * 8 + q];
+              }
               uint2 pk;
-              pk.x = pack_bf16x2_rne(acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1]);
-              pk.y = pack_bf16x2_rne(acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]);
+              pk.x = pack_bf16x2_rne(v[0], v[1]);
+              pk.y = pack_bf16x2_rne(v[2], v[3]);
               *reinterpret_cast<uint2*>(crow + n0 + wn * 128 + j * 32 + g * 8 + col_lane) = pk;
             }
           }
@@ -325,15 +389,19 @@ int persistent_grid(hipStream_t s, int* grid, int* dev_out) {
   return HMOE_OK;
 }
 
-// Allows 2 * kStageBytes of dynamic LDS for both kernel variants, once per device.
+template <bool SWIGLU, bool FP8>
+bool set_lds_limit(int bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<SWIGLU, FP8>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+}
+
+// Allows 2 * kStageBytes of dynamic LDS for every kernel variant, once per device.
 int allow_dynamic_lds(int dev) {
   static std::atomic<bool> done[64];
   if (dev >= 0 && dev < 64 && done[dev].load(std::memory_order_acquire)) return HMOE_OK;
   const int bytes = 2 * kStageBytes;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<true>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess ||
-      hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<false>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+  if (!set_lds_limit<true, false>(bytes) || !set_lds_limit<false, false>(bytes) ||
+      !set_lds_limit<true, true>(bytes) || !set_lds_limit<false, true>(bytes)) {
     set_error("grouped GEMM: cannot allow %d bytes of dynamic LDS on device %d", bytes, dev);
     return HMOE_ERR_HIP;
   }
@@ -341,26 +409,31 @@ int allow_dynamic_lds(int dev) {
   return HMOE_OK;
 }
 
-int launch_grouped(bool swiglu, const void* A, const void* B, const int32_t* offsets,
-                   int n_experts, int64_t rows_cap, int kdim, int ncols, void* C, int64_t ldc,
-                   hipStream_t s, const char* what) {
+int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const float* a_scale,
+                   const float* b_scale, const int32_t* offsets, int n_experts, int64_t rows_cap,
+                   int kdim, int ncols, void* C, int64_t ldc, hipStream_t s, const char* what) {
   const int n_tiles_n = ncols / kBN;
   const int64_t max_tiles = (ceil_div(rows_cap, kBM) + n_experts) * n_tiles_n;
   HMOE_REQUIRE(max_tiles < (int64_t(1) << 31), "%s: too many tiles", what);
   HMOE_REQUIRE(rows_cap < (int64_t(1) << 31), "%s: rows_cap must fit in int32", what);
+  HMOE_REQUIRE(static_cast<int64_t>(kBM) * kdim * (fp8 ? 1 : 2) < (int64_t(1) << 31),
+               "%s: reduction dimension too large", what);
   int dev = 0;
   int grid = 0;
   if (int rc = persistent_grid(s, &grid, &dev)) return rc;
   if (int rc = allow_dynamic_lds(dev)) return rc;
   const size_t lds = 2 * kStageBytes;
-  if (swiglu)
-    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(grid), dim3(kThreads), lds, s,
-                       static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), offsets,
-                       n_experts, rows_cap, kdim, ncols, static_cast<uint16_t*>(C), ldc, n_tiles_n);
-  else
-    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(grid), dim3(kThreads), lds, s,
-                       static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), offsets,
-                       n_experts, rows_cap, kdim, ncols, static_cast<uint16_t*>(C), ldc, n_tiles_n);
+  const uint8_t* a = static_cast<const uint8_t*>(A);
+  const uint8_t* b = static_cast<const uint8_t*>(B);
+  uint16_t* c = static_cast<uint16_t*>(C);
+#define HMOE_LAUNCH_GEMM(SW, F8)                                                                  \
+  hipLaunchKernelGGL((grouped_gemm_kernel<SW, F8>), dim3(grid), dim3(kThreads), lds, s, a, b,   \
+                     a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n)
+  if (swiglu && !fp8) HMOE_LAUNCH_GEMM(true, false);
+  else if (!swiglu && !fp8) HMOE_LAUNCH_GEMM(false, false);
+  else if (swiglu && fp8) HMOE_LAUNCH_GEMM(true, true);
+  else HMOE_LAUNCH_GEMM(false, true);
+#undef HMOE_LAUNCH_GEMM
   return check_launch(what);
 }
 
@@ -380,8 +453,9 @@ extern "C" int hmoe_grouped_gate_up(const void* xs, const int32_t* offsets, int 
                     "grouped_gate_up: d_ff must be a multiple of %d (got %d)", kBN / 2, d_ff);
   if (rows_cap == 0) return HMOE_OK;
   HMOE_REQUIRE(xs && offsets && w_gate_up_packed && h, "grouped_gate_up: null pointer argument");
-  return launch_grouped(true, xs, w_gate_up_packed, offsets, n_experts, rows_cap, d_model, 2 * d_ff,
-                        h, d_ff, static_cast<hipStream_t>(stream), "hmoe_grouped_gate_up");
+  return launch_grouped(true, false, xs, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up");
 }
 
 extern "C" int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
@@ -397,6 +471,47 @@ extern "C" int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_ex
                     "grouped_down: d_model must be a multiple of %d (got %d)", kBN, d_model);
   if (rows_cap == 0) return HMOE_OK;
   HMOE_REQUIRE(h && offsets && w_down_packed && ys, "grouped_down: null pointer argument");
-  return launch_grouped(false, h, w_down_packed, offsets, n_experts, rows_cap, d_ff, d_model, ys,
-                        d_model, static_cast<hipStream_t>(stream), "hmoe_grouped_down");
+  return launch_grouped(false, false, h, w_down_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_ff, d_model, ys, d_model, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_down");
+}
+
+extern "C" int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_scale,
+                                        const int32_t* offsets, int n_experts, int64_t rows_cap,
+                                        int d_model, int d_ff, const uint8_t* w_packed,
+                                        const float* w_scales, void* h, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_fp8: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "grouped_gate_up_fp8: rows_cap must be >= 0");
+  HMOE_REQUIRE_CODE(d_model % 128 == 0 && d_model >= 128, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_fp8: d_model must be a multiple of 128 (got %d)", d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_fp8: d_ff must be a multiple of %d (got %d)", kBN / 2, d_ff);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(xs_q && xs_scale && offsets && w_packed && w_scales && h,
+               "grouped_gate_up_fp8: null pointer argument");
+  return launch_grouped(true, true, xs_q, w_packed, xs_scale, w_scales, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_fp8");
+}
+
+extern "C" int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale,
+                                     const int32_t* offsets, int n_experts, int64_t rows_cap,
+                                     int d_ff, int d_model, const uint8_t* w_packed,
+                                     const float* w_scales, void* ys, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_down_fp8: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "grouped_down_fp8: rows_cap must be >= 0");
+  HMOE_REQUIRE_CODE(d_ff % 128 == 0 && d_ff >= 128, HMOE_ERR_UNSUPPORTED,
+                    "grouped_down_fp8: d_ff must be a multiple of 128 (got %d)", d_ff);
+  HMOE_REQUIRE_CODE(d_model % kBN == 0 && d_model > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_down_fp8: d_model must be a multiple of %d (got %d)", kBN, d_model);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(h_q && h_scale && offsets && w_packed && w_scales && ys,
+               "grouped_down_fp8: null pointer argument");
+  return launch_grouped(false, true, h_q, w_packed, h_scale, w_scales, offsets, n_experts,
+                        rows_cap, d_ff, d_model, ys, d_model, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_down_fp8");
 }

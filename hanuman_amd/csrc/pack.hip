@@ -63,8 +63,158 @@ __global__ __launch_bounds__(256) void pack_transpose_kernel(const TW* __restric
   }
 }
 
+// ----------------------------------------------------------- e4m3 packing --
+// Per-output-channel e4m3 codes (same rule as the activations: codes
+// e4m3(clamp(w * (448/amax), +-448)), scale amax/448, amax over the reduction
+// dimension of the column).  Three passes: column amax into `scales` (packed
+// order), the transpose-quantise, then amax -> amax/448 in place.
+
+// amax over rows_r of column c of src[e] (rows_r x cols_c), written to
+// out[e * out_stride + packed_row(c)].  Block (64, 4): 64 columns, 4 row groups.
+template <typename TW, bool GATE_UP>
+__global__ __launch_bounds__(256) void colmax_kernel(const TW* __restrict__ src, int rows_r,
+                                                     int cols_c, int up_half, float* __restrict__ out,
+                                                     int out_stride) {
+  __shared__ float part[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int e = blockIdx.y;
+  const int c = blockIdx.x * 64 + tx;
+  float m = 0.0f;
+  if (c < cols_c) {
+    const TW* col = src + static_cast<int64_t>(e) * rows_r * cols_c + c;
+    for (int r = ty; r < rows_r; r += 4) m = fmaxf(m, fabsf(load_w(col, static_cast<int64_t>(r) * cols_c)));
+  }
+  part[ty][tx] = m;
+  __syncthreads();
+  if (ty == 0 && c < cols_c) {
+    m = fmaxf(fmaxf(part[0][tx], part[1][tx]), fmaxf(part[2][tx], part[3][tx]));
+    // Packed row of column c: gate/up interleave 32 columns of each per 64 rows.
+    const int p = GATE_UP ? (c >> 5) * 64 + up_half * 32 + (c & 31) : c;
+    out[static_cast<int64_t>(e) * out_stride + p] = m;
+  }
+}
+
+__device__ __forceinline__ uint8_t e4m3_code(float v) {
+  v = fminf(fmaxf(v, -448.0f), 448.0f);
+  return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xff);
+}
+
+// Transposes 64x64 tiles of src[e][r][c] into e4m3 dst[e][p][r] like
+// pack_transpose_kernel, scaling each packed row p by 448/amax[e][p].
+template <typename TW, bool GATE_UP>
+__global__ __launch_bounds__(256) void pack_fp8_kernel(const TW* __restrict__ src0,
+                                                       const TW* __restrict__ src1, int rows_r,
+                                                       int cols_c, const float* __restrict__ amax,
+                                                       uint8_t* __restrict__ dst) {
+  __shared__ float tile[64][65];
+  const int e = blockIdx.z;
+  const int r0 = blockIdx.y * 64;
+  const int p0 = blockIdx.x * 64;
+  const int dst_rows = GATE_UP ? 2 * cols_c : cols_c;
+  const int64_t src_stride_e = static_cast<int64_t>(rows_r) * cols_c;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int rr = ty; rr < 64; rr += 4) {
+    const int r = r0 + rr;
+    const int p = p0 + tx;
+    float v = 0.0f;
+    if (r < rows_r && p < dst_rows) {
+      const TW* s = src0;
+      int col = p;
+      if (GATE_UP) {
+        s = ((p & 63) < 32) ? src0 : src1;
+        col = (p >> 6) * 32 + (p & 31);
+      }
+      v = load_w(s, e * src_stride_e + static_cast<int64_t>(r) * cols_c + col);
+    }
+    tile[rr][tx] = v;
+  }
+  __syncthreads();
+  for (int pp = ty; pp < 64; pp += 4) {
+    const int p = p0 + pp;
+    const int r = r0 + tx;
+    if (p < dst_rows && r < rows_r) {
+      const float m = amax[static_cast<int64_t>(e) * dst_rows + p];
+      const float inv = m > 0.0f ? 448.0f / m : 1.0f;
+      dst[(static_cast<int64_t>(e) * dst_rows + p) * rows_r + r] = e4m3_code(tile[tx][pp] * inv);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void amax_to_scale_kernel(float* __restrict__ v, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) v[i] = v[i] > 0.0f ? v[i] / 448.0f : 1.0f;
+}
+
 }  // namespace
 }  // namespace hmoe
+
+extern "C" size_t hmoe_packed_fp8_gate_up_bytes(int n_experts, int d_model, int d_ff) {
+  if (n_experts <= 0 || d_model <= 0 || d_ff <= 0) return 0;
+  return static_cast<size_t>(n_experts) * 2 * d_ff * d_model;
+}
+
+extern "C" size_t hmoe_packed_fp8_down_bytes(int n_experts, int d_ff, int d_model) {
+  if (n_experts <= 0 || d_model <= 0 || d_ff <= 0) return 0;
+  return static_cast<size_t>(n_experts) * d_ff * d_model;
+}
+
+extern "C" int hmoe_pack_fp8_gate_up(const void* w_gate, const void* w_up, int w_dtype,
+                                     int n_experts, int d_model, int d_ff, uint8_t* packed,
+                                     float* scales, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && d_model >= 1 && d_ff >= 1, "pack_fp8_gate_up: sizes must be >= 1");
+  HMOE_REQUIRE(d_ff % 32 == 0, "pack_fp8_gate_up: d_ff must be a multiple of 32 (got %d)", d_ff);
+  HMOE_REQUIRE(w_dtype == HMOE_F32 || w_dtype == HMOE_BF16,
+               "pack_fp8_gate_up: dtype must be F32 or BF16");
+  HMOE_REQUIRE(w_gate && w_up && packed && scales, "pack_fp8_gate_up: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 cgrid(static_cast<unsigned>(ceil_div(d_ff, 64)), static_cast<unsigned>(n_experts));
+  const dim3 tgrid(static_cast<unsigned>(ceil_div(2 * d_ff, 64)),
+                   static_cast<unsigned>(ceil_div(d_model, 64)), static_cast<unsigned>(n_experts));
+  if (w_dtype == HMOE_F32) {
+    const float* g = static_cast<const float*>(w_gate);
+    const float* u = static_cast<const float*>(w_up);
+    hipLaunchKernelGGL((colmax_kernel<float, true>), cgrid, dim3(256), 0, s, g, d_model, d_ff, 0, scales, 2 * d_ff);
+    hipLaunchKernelGGL((colmax_kernel<float, true>), cgrid, dim3(256), 0, s, u, d_model, d_ff, 1, scales, 2 * d_ff);
+    hipLaunchKernelGGL((pack_fp8_kernel<float, true>), tgrid, dim3(256), 0, s, g, u, d_model, d_ff, scales, packed);
+  } else {
+    const uint16_t* g = static_cast<const uint16_t*>(w_gate);
+    const uint16_t* u = static_cast<const uint16_t*>(w_up);
+    hipLaunchKernelGGL((colmax_kernel<uint16_t, true>), cgrid, dim3(256), 0, s, g, d_model, d_ff, 0, scales, 2 * d_ff);
+    hipLaunchKernelGGL((colmax_kernel<uint16_t, true>), cgrid, dim3(256), 0, s, u, d_model, d_ff, 1, scales, 2 * d_ff);
+    hipLaunchKernelGGL((pack_fp8_kernel<uint16_t, true>), tgrid, dim3(256), 0, s, g, u, d_model, d_ff, scales, packed);
+  }
+  const int64_t n = static_cast<int64_t>(n_experts) * 2 * d_ff;
+  hipLaunchKernelGGL(amax_to_scale_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
+                     scales, n);
+  return check_launch("hmoe_pack_fp8_gate_up");
+}
+
+extern "C" int hmoe_pack_fp8_down(const void* w_down, int w_dtype, int n_experts, int d_ff,
+                                  int d_model, uint8_t* packed, float* scales,
+                                  hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && d_model >= 1 && d_ff >= 1, "pack_fp8_down: sizes must be >= 1");
+  HMOE_REQUIRE(w_dtype == HMOE_F32 || w_dtype == HMOE_BF16, "pack_fp8_down: dtype must be F32 or BF16");
+  HMOE_REQUIRE(w_down && packed && scales, "pack_fp8_down: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 cgrid(static_cast<unsigned>(ceil_div(d_model, 64)), static_cast<unsigned>(n_experts));
+  const dim3 tgrid(static_cast<unsigned>(ceil_div(d_model, 64)), static_cast<unsigned>(ceil_div(d_ff, 64)),
+                   static_cast<unsigned>(n_experts));
+  if (w_dtype == HMOE_F32) {
+    const float* w = static_cast<const float*>(w_down);
+    hipLaunchKernelGGL((colmax_kernel<float, false>), cgrid, dim3(256), 0, s, w, d_ff, d_model, 0, scales, d_model);
+    hipLaunchKernelGGL((pack_fp8_kernel<float, false>), tgrid, dim3(256), 0, s, w, static_cast<const float*>(nullptr), d_ff, d_model, scales, packed);
+  } else {
+    const uint16_t* w = static_cast<const uint16_t*>(w_down);
+    hipLaunchKernelGGL((colmax_kernel<uint16_t, false>), cgrid, dim3(256), 0, s, w, d_ff, d_model, 0, scales, d_model);
+    hipLaunchKernelGGL((pack_fp8_kernel<uint16_t, false>), tgrid, dim3(256), 0, s, w, static_cast<const uint16_t*>(nullptr), d_ff, d_model, scales, packed);
+  }
+  const int64_t n = static_cast<int64_t>(n_experts) * d_model;
+  hipLaunchKernelGGL(amax_to_scale_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
+                     scales, n);
+  return check_launch("hmoe_pack_fp8_down");
+}
 
 extern "C" size_t hmoe_packed_gate_up_bytes(int n_experts, int d_model, int d_ff) {
   if (n_experts <= 0 || d_model <= 0 || d_ff <= 0) return 0;

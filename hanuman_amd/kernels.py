@@ -151,6 +151,38 @@ def permute_rows(x: torch.Tensor, plan: Plan, out_dtype: torch.dtype = torch.bfl
     return xs
 
 
+def permute_rows_fp8(x: torch.Tensor, plan: Plan):
+    """Dispatched e4m3 rows and their per-token scales (fp8 workload rule):
+    ``(xs_q uint8 [rows_cap, D], xs_scale f32 [rows_cap])``."""
+    _check(x, "x", 2)
+    T, D = x.shape
+    if plan.slot_pos.numel() != T * plan.top_k:
+        raise ValueError("plan does not match x's token count")
+    xs_q = torch.empty((plan.rows_cap, D), dtype=torch.uint8, device=x.device)
+    xs_s = torch.empty(plan.rows_cap, dtype=torch.float32, device=x.device)
+    call("hmoe_permute_rows_fp8", _ptr(x), _dtype_code(x), T, D, plan.top_k, _ptr(plan.slot_pos),
+         _ptr(xs_q), _ptr(xs_s), _stream())
+    return xs_q, xs_s
+
+
+def quantize_rows_fp8(a: torch.Tensor, offsets: torch.Tensor | None = None):
+    """Per-row e4m3 codes and scales of a bf16 matrix ``[rows, cols]``; rows at
+    or past ``offsets[-1]`` are skipped (left as allocated) when offsets are given."""
+    _check(a, "a", 2)
+    if a.dtype != torch.bfloat16:
+        raise TypeError("quantize_rows_fp8 takes a bf16 matrix")
+    rows, cols = a.shape
+    q = torch.empty((rows, cols), dtype=torch.uint8, device=a.device)
+    sc = torch.ones(rows, dtype=torch.float32, device=a.device)
+    n = 0
+    if offsets is not None:
+        _check(offsets, "offsets", 1)
+        n = offsets.numel() - 1
+    call("hmoe_quantize_rows_fp8", _ptr(a), rows, cols, _ptr(offsets), n, _ptr(q), _ptr(sc),
+         _stream())
+    return q, sc
+
+
 # ---------------------------------------------------------------- weights --
 
 def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
@@ -173,6 +205,31 @@ def pack_down(w_down: torch.Tensor) -> torch.Tensor:
     out = torch.empty((N, D, F), dtype=torch.bfloat16, device=w_down.device)
     call("hmoe_pack_down", _ptr(w_down), _dtype_code(w_down), N, F, D, _ptr(out), _stream())
     return out
+
+
+def pack_fp8_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor):
+    """e4m3 gate/up operand [N, 2F, D] (uint8) and its scales [N, 2F]."""
+    _check(w_gate, "w_gate", 3)
+    _check(w_up, "w_up", 3)
+    if w_gate.shape != w_up.shape or w_gate.dtype != w_up.dtype:
+        raise ValueError("w_gate and w_up must have the same shape and dtype")
+    N, D, F = w_gate.shape
+    out = torch.empty((N, 2 * F, D), dtype=torch.uint8, device=w_gate.device)
+    sc = torch.empty((N, 2 * F), dtype=torch.float32, device=w_gate.device)
+    call("hmoe_pack_fp8_gate_up", _ptr(w_gate), _ptr(w_up), _dtype_code(w_gate), N, D, F,
+         _ptr(out), _ptr(sc), _stream())
+    return out, sc
+
+
+def pack_fp8_down(w_down: torch.Tensor):
+    """e4m3 down operand [N, D, F] (uint8) and its scales [N, D]."""
+    _check(w_down, "w_down", 3)
+    N, F, D = w_down.shape
+    out = torch.empty((N, D, F), dtype=torch.uint8, device=w_down.device)
+    sc = torch.empty((N, D), dtype=torch.float32, device=w_down.device)
+    call("hmoe_pack_fp8_down", _ptr(w_down), _dtype_code(w_down), N, F, D, _ptr(out), _ptr(sc),
+         _stream())
+    return out, sc
 
 
 # ------------------------------------------------------------ grouped GEMM --
@@ -210,6 +267,40 @@ def grouped_down(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor,
     ys = torch.empty((h.shape[0], D), dtype=torch.bfloat16, device=h.device)
     call("hmoe_grouped_down", _ptr(h), _ptr(offsets), N, R, F, D, _ptr(w_down), _ptr(ys),
          _stream())
+    return ys
+
+
+def grouped_gate_up_fp8(xs_q: torch.Tensor, xs_scale: torch.Tensor, offsets: torch.Tensor,
+                        w_packed: torch.Tensor, w_scales: torch.Tensor) -> torch.Tensor:
+    """bf16 ``h`` of the fp8 gate/up GEMM (dequantised, SwiGLU applied)."""
+    for t, n in ((xs_q, "xs_q"), (xs_scale, "xs_scale"), (offsets, "offsets"),
+                 (w_packed, "w_packed"), (w_scales, "w_scales")):
+        _check(t, n)
+    N, F2, D = w_packed.shape
+    if (xs_q.dtype != torch.uint8 or w_packed.dtype != torch.uint8 or xs_q.shape[1] != D
+            or xs_scale.numel() != xs_q.shape[0] or tuple(w_scales.shape) != (N, F2)
+            or offsets.numel() != N + 1 or offsets.dtype != torch.int32):
+        raise ValueError("grouped_gate_up_fp8: inconsistent shapes or dtypes")
+    h = torch.empty((xs_q.shape[0], F2 // 2), dtype=torch.bfloat16, device=xs_q.device)
+    call("hmoe_grouped_gate_up_fp8", _ptr(xs_q), _ptr(xs_scale), _ptr(offsets), N, xs_q.shape[0],
+         D, F2 // 2, _ptr(w_packed), _ptr(w_scales), _ptr(h), _stream())
+    return h
+
+
+def grouped_down_fp8(h_q: torch.Tensor, h_scale: torch.Tensor, offsets: torch.Tensor,
+                     w_packed: torch.Tensor, w_scales: torch.Tensor) -> torch.Tensor:
+    """bf16 ``ys`` of the fp8 down GEMM (dequantised)."""
+    for t, n in ((h_q, "h_q"), (h_scale, "h_scale"), (offsets, "offsets"),
+                 (w_packed, "w_packed"), (w_scales, "w_scales")):
+        _check(t, n)
+    N, D, F = w_packed.shape
+    if (h_q.dtype != torch.uint8 or w_packed.dtype != torch.uint8 or h_q.shape[1] != F
+            or h_scale.numel() != h_q.shape[0] or tuple(w_scales.shape) != (N, D)
+            or offsets.numel() != N + 1 or offsets.dtype != torch.int32):
+        raise ValueError("grouped_down_fp8: inconsistent shapes or dtypes")
+    ys = torch.empty((h_q.shape[0], D), dtype=torch.bfloat16, device=h_q.device)
+    call("hmoe_grouped_down_fp8", _ptr(h_q), _ptr(h_scale), _ptr(offsets), N, h_q.shape[0], F, D,
+         _ptr(w_packed), _ptr(w_scales), _ptr(ys), _stream())
     return ys
 
 

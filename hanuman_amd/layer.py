@@ -19,9 +19,10 @@ _TORCH_DT = {"bf16": torch.bfloat16, "f32": torch.float32}
 class DeviceLayer:
     def __init__(self, inp: Inputs, device: str | torch.device = "cuda"):
         wl: Workload = inp.wl
-        if wl.expert_dtype != "bf16":
-            raise NotImplementedError(f"{wl.name}: expert dtype {wl.expert_dtype} is not built yet")
+        if wl.expert_dtype not in ("bf16", "fp8"):
+            raise NotImplementedError(f"{wl.name}: expert dtype {wl.expert_dtype} is not built")
         self.wl = wl
+        self.fp8 = wl.expert_dtype == "fp8"
         dev = torch.device(device)
         self.device = dev
         self.x = torch.from_numpy(inp.x).to(dev, _TORCH_DT[wl.x_dtype]).contiguous()
@@ -35,13 +36,21 @@ class DeviceLayer:
         self.capacity = wl.capacity
         self.w_gate_up = None
         self.w_down = None
+        self.w_gate_up_scale = None
+        self.w_down_scale = None
         if wl.expert == "swiglu":
             wg = torch.from_numpy(inp.w_gate).to(dev)
             wu = torch.from_numpy(inp.w_up).to(dev)
-            self.w_gate_up = K.pack_gate_up(wg, wu)
+            if self.fp8:
+                self.w_gate_up, self.w_gate_up_scale = K.pack_fp8_gate_up(wg, wu)
+            else:
+                self.w_gate_up = K.pack_gate_up(wg, wu)
             del wg, wu
             wd = torch.from_numpy(inp.w_down).to(dev)
-            self.w_down = K.pack_down(wd)
+            if self.fp8:
+                self.w_down, self.w_down_scale = K.pack_fp8_down(wd)
+            else:
+                self.w_down = K.pack_down(wd)
             del wd
         ws = int(_lib.lib().hmoe_plan_workspace_bytes(wl.tokens, wl.top_k, wl.n_experts))
         self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
@@ -55,17 +64,30 @@ class DeviceLayer:
             return self.logits_in, top_idx, gates
         return K.router(self.x, self.router_w, None, wl.top_k, self.mode)
 
+    def experts_fp8(self, plan):
+        """e4m3 dispatch and expert GEMMs: (xs_q, xs_scale, h, h_q, h_scale, ys)."""
+        xs_q, xs_s = K.permute_rows_fp8(self.x, plan)
+        h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, self.w_gate_up, self.w_gate_up_scale)
+        h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
+        ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, self.w_down, self.w_down_scale)
+        return xs_q, xs_s, h, h_q, h_s, ys
+
     def forward(self) -> dict:
         wl = self.wl
         logits, top_idx, gates = self.route()
         plan = K.dispatch_plan(top_idx, wl.n_experts, self.capacity, self.workspace)
-        xs = K.permute_rows(self.x, plan, torch.bfloat16)
+        extra = {}
         h = None
-        if wl.expert == "identity":
-            ys = xs
+        if self.fp8:
+            xs, xs_s, h, h_q, h_s, ys = self.experts_fp8(plan)
+            extra = {"xs_scale": xs_s, "h_q": h_q, "h_scale": h_s}
         else:
-            h = K.grouped_gate_up(xs, plan.offsets, self.w_gate_up)
-            ys = K.grouped_down(h, plan.offsets, self.w_down)
+            xs = K.permute_rows(self.x, plan, torch.bfloat16)
+            if wl.expert == "identity":
+                ys = xs
+            else:
+                h = K.grouped_gate_up(xs, plan.offsets, self.w_gate_up)
+                ys = K.grouped_down(h, plan.offsets, self.w_down)
         out = K.combine(ys, plan, gates, None, self.out_dtype)
         return {"logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan, "xs": xs,
-                "h": h, "ys": ys, "out": out}
+                "h": h, "ys": ys, "out": out, **extra}

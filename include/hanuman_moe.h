@@ -74,7 +74,7 @@ size_t hmoe_plan_workspace_bytes(int64_t tokens, int top_k, int n_experts);
  * bias [N] f32 (may be NULL = zeros; used by HMOE_ROUTE_SIGMOID_BIAS only).
  * Outputs: logits [T,N] f32 (fp32 rounding of a float64 d-ascending sum),
  * top_idx [T,K] int32 (descending key, lower index first on ties), gates
- * [T,K] f32.  N <= 256, K <= min(N, 32). */
+ * [T,K] f32.  N <= 256, K <= min(N, 32), D % 8 == 0. */
 int hmoe_router(const void* x, int x_dtype, const void* router_w, int w_dtype,
                 const float* bias, int64_t tokens, int d_model, int n_experts,
                 int top_k, int mode, float routed_scaling_factor, float* logits,
@@ -112,6 +112,24 @@ int hmoe_permute_rows(const void* x, int x_dtype, int64_t tokens, int d_model,
                       int top_k, const int32_t* slot_pos, void* xs, int xs_dtype,
                       hmoe_stream_t stream);
 
+/* ---- fp8 dispatch (workload rule, no reference code): the row permutation
+ *      above with per-token e4m3 quantisation fused in ---------------------- */
+
+/* xs_q[slot_pos[t*K+k]] = e4m3 codes of x[t] for kept slots, xs_scale[...] =
+ * that token's scale.  Per row: amax = max|x|, codes
+ * e4m3(clamp(x * (448/amax), +-448)) (round to nearest even), scale amax/448;
+ * an all-zero row gets scale 1.  x [T,D] (F32/BF16), xs_q [rows_cap, D]
+ * uint8, xs_scale [rows_cap] f32.  D % 8 == 0. */
+int hmoe_permute_rows_fp8(const void* x, int x_dtype, int64_t tokens, int d_model,
+                          int top_k, const int32_t* slot_pos, uint8_t* xs_q,
+                          float* xs_scale, hmoe_stream_t stream);
+
+/* Same per-row rule for a bf16 matrix a [rows, cols] (the SwiGLU output h
+ * before the fp8 down GEMM).  With offsets != NULL, rows at or past
+ * offsets[n_experts] are left untouched.  cols % 8 == 0. */
+int hmoe_quantize_rows_fp8(const void* a, int64_t rows, int cols, const int32_t* offsets,
+                           int n_experts, uint8_t* q, float* scale, hmoe_stream_t stream);
+
 /* ---- expert weights: moe.py:204-206 (replaces the per-call `.astype(dtype)`
  *      of the stacked fp32 masters) ---------------------------------------- */
 
@@ -126,6 +144,18 @@ int hmoe_pack_gate_up(const void* w_gate, const void* w_up, int w_dtype,
 size_t hmoe_packed_down_bytes(int n_experts, int d_ff, int d_model);
 int hmoe_pack_down(const void* w_down, int w_dtype, int n_experts, int d_ff,
                    int d_model, void* packed, hmoe_stream_t stream);
+
+/* e4m3 versions of the two packed operands (same layouts, one byte per
+ * weight) with per-output-channel scales in packed-row order: gate/up scales
+ * [N][2F], down scales [N][D].  Rule as hmoe_permute_rows_fp8, amax over the
+ * reduction dimension of each output column. */
+size_t hmoe_packed_fp8_gate_up_bytes(int n_experts, int d_model, int d_ff);
+int hmoe_pack_fp8_gate_up(const void* w_gate, const void* w_up, int w_dtype, int n_experts,
+                          int d_model, int d_ff, uint8_t* packed, float* scales,
+                          hmoe_stream_t stream);
+size_t hmoe_packed_fp8_down_bytes(int n_experts, int d_ff, int d_model);
+int hmoe_pack_fp8_down(const void* w_down, int w_dtype, int n_experts, int d_ff, int d_model,
+                       uint8_t* packed, float* scales, hmoe_stream_t stream);
 
 /* ---- grouped expert GEMMs: moe.py:67-74 (replaces the three
  *      `jax.lax.ragged_dot` calls and the SwiGLU between them) ------------- */
@@ -143,6 +173,20 @@ int hmoe_grouped_gate_up(const void* xs, const int32_t* offsets, int n_experts,
 int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
                       int64_t rows_cap, int d_ff, int d_model,
                       const void* w_down_packed, void* ys, hmoe_stream_t stream);
+
+/* fp8 expert GEMMs (workload rule): e4m3 operands on the CDNA4 32x32x64
+ * fp8 MFMA with float32 accumulation; the accumulators are dequantised with
+ * the row scale times the column scale, then (gate/up) the SwiGLU is applied.
+ * h and ys are bf16.  gate/up: D % 128 == 0, F % 128 == 0; down: F % 128 == 0,
+ * D % 256 == 0. */
+int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_scale, const int32_t* offsets,
+                             int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                             const uint8_t* w_packed, const float* w_scales, void* h,
+                             hmoe_stream_t stream);
+int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale, const int32_t* offsets,
+                          int n_experts, int64_t rows_cap, int d_ff, int d_model,
+                          const uint8_t* w_packed, const float* w_scales, void* ys,
+                          hmoe_stream_t stream);
 
 /* ---- combine: moe.py:80-85 (replaces `ys[inv]` and the weighted einsum) - */
 

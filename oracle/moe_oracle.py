@@ -47,7 +47,7 @@ __all__ = [
     "capacity_of", "rows_cap_of", "dispatch_plan", "dispatch_plan_bruteforce",
     "permute_rows", "silu", "expert_ffn", "combine", "combine_identity", "aux_losses",
     "shared_expert", "moe_forward", "quantize_rows_e4m3", "quantize_cols_e4m3",
-    "normwise_rel_err",
+    "expert_ffn_fp8", "quantize_expert_weights", "dequantized_weights", "normwise_rel_err",
 ]
 
 
@@ -411,24 +411,77 @@ def expert_ffn(xs, offsets, wg, wu, wd, precision: str = "fp32") -> np.ndarray:
     return ys
 
 
+def _e4m3_scales(amax):
+    """Dequantisation scale ``amax/448`` and quantisation multiplier
+    ``448/amax`` (both correctly rounded float32 divisions); an all-zero group
+    gets 1 and 1."""
+    amax = np.asarray(amax, dtype=F32)
+    pos = amax > 0
+    safe = np.where(pos, amax, F32(1.0)).astype(F32)
+    s = np.where(pos, (safe / F32(448.0)).astype(F32), F32(1.0)).astype(F32)
+    inv = np.where(pos, (F32(448.0) / safe).astype(F32), F32(1.0)).astype(F32)
+    return s, inv
+
+
 def quantize_rows_e4m3(a):
-    """Per-row e4m3 quantisation: ``s = amax/448`` (1 for an all-zero row),
-    ``q = e4m3(a / s)``.  Returns (codes uint8, scales float32)."""
+    """Per-row e4m3 quantisation (the fp8 workload rule for activations):
+    ``amax`` = max |a| over the row, ``q = e4m3(clamp(a * (448/amax), +-448))``
+    (one float32 multiply, round-to-nearest-even, saturating), dequantisation
+    scale ``s = amax/448``.  Returns (codes uint8, scales float32)."""
     a = np.asarray(a, dtype=F32)
     amax = np.max(np.abs(a), axis=-1)
-    s = np.where(amax > 0, (amax / F32(448.0)).astype(F32), F32(1.0)).astype(F32)
-    q = e4m3_encode((a / s[..., None]).astype(F32))
+    s, inv = _e4m3_scales(amax)
+    q = e4m3_encode((a * inv[..., None]).astype(F32))
     return q, s
 
 
 def quantize_cols_e4m3(w):
     """Per-output-channel e4m3 quantisation of ``w [..., K, Ncols]``: one scale
-    per column (max over K).  Returns (codes uint8, scales float32 [..., Ncols])."""
+    per column (max over K), same rule as :func:`quantize_rows_e4m3`.
+    Returns (codes uint8, scales float32 [..., Ncols])."""
     w = np.asarray(w, dtype=F32)
     amax = np.max(np.abs(w), axis=-2)
-    s = np.where(amax > 0, (amax / F32(448.0)).astype(F32), F32(1.0)).astype(F32)
-    q = e4m3_encode((w / s[..., None, :]).astype(F32))
+    s, inv = _e4m3_scales(amax)
+    q = e4m3_encode((w * inv[..., None, :]).astype(F32))
     return q, s
+
+
+def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s):
+    """Grouped SwiGLU on e4m3 operands (the fp8 workload's expert rule).
+
+    ``xs_q [R, D]`` codes with per-row scales ``xs_s``; ``wg_q/wu_q [N, D, F]``
+    codes with per-column scales ``[N, F]``; ``wd_q [N, F, D]`` with ``[N, D]``.
+    ``g = (x.wg) * sx * sg``, ``u`` likewise, ``h = bf16(silu(g) * u)``; h is
+    re-quantised per row (:func:`quantize_rows_e4m3`) and
+    ``ys = bf16((hq.wd) * sh * sd)``.  Dot products of decoded codes in
+    float64.  Returns (ys float32 of bf16 values, h, hq, hs)."""
+    offsets = np.asarray(offsets, dtype=np.int64)
+    N = len(offsets) - 1
+    R = xs_q.shape[0]
+    F = wg_q.shape[2]
+    D = wd_q.shape[2]
+    h = np.zeros((R, F), F32)
+    for e in range(N):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if b <= a:
+            continue
+        x = e4m3_decode(xs_q[a:b]).astype(F64) * np.asarray(xs_s[a:b], F64)[:, None]
+        g = (x @ e4m3_decode(wg_q[e]).astype(F64)) * np.asarray(wg_s[e], F64)[None, :]
+        u = (x @ e4m3_decode(wu_q[e]).astype(F64)) * np.asarray(wu_s[e], F64)[None, :]
+        h[a:b] = bf16_round((silu(g) * u).astype(F32))
+    total = int(offsets[-1])
+    hq = np.zeros((R, F), np.uint8)
+    hs = np.ones(R, F32)
+    hq[:total], hs[:total] = quantize_rows_e4m3(h[:total])
+    ys = np.zeros((R, D), F32)
+    for e in range(N):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if b <= a:
+            continue
+        hh = e4m3_decode(hq[a:b]).astype(F64) * hs[a:b].astype(F64)[:, None]
+        y = (hh @ e4m3_decode(wd_q[e]).astype(F64)) * np.asarray(wd_s[e], F64)[None, :]
+        ys[a:b] = bf16_round(y.astype(F32))
+    return ys, h, hq, hs
 
 
 # --------------------------------------------------------------------------
@@ -532,6 +585,26 @@ def aux_losses(logits, scores, top_idx, B: int, S: int, N: int) -> dict:
     }
 
 
+def quantize_expert_weights(params: dict) -> dict:
+    """Per-output-channel e4m3 codes and scales of the stacked expert weights
+    (``expert_w_gate/up [N,D,F]``: scale per F column; ``expert_w_down
+    [N,F,D]``: scale per D column)."""
+    wg_q, wg_s = quantize_cols_e4m3(params["expert_w_gate"])
+    wu_q, wu_s = quantize_cols_e4m3(params["expert_w_up"])
+    wd_q, wd_s = quantize_cols_e4m3(params["expert_w_down"])
+    return {"wg_q": wg_q, "wg_s": wg_s, "wu_q": wu_q, "wu_s": wu_s, "wd_q": wd_q, "wd_s": wd_s}
+
+
+def dequantized_weights(wq: dict) -> dict:
+    """float32 expert weights that the e4m3 codes and scales represent (the
+    weights of the fp8 workload's float32 tolerance reference)."""
+    return {
+        "expert_w_gate": (e4m3_decode(wq["wg_q"]) * wq["wg_s"][:, None, :]).astype(F32),
+        "expert_w_up": (e4m3_decode(wq["wu_q"]) * wq["wu_s"][:, None, :]).astype(F32),
+        "expert_w_down": (e4m3_decode(wq["wd_q"]) * wq["wd_s"][:, None, :]).astype(F32),
+    }
+
+
 # --------------------------------------------------------------------------
 # full layer
 # --------------------------------------------------------------------------
@@ -548,7 +621,7 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
                 routed_scaling_factor: float = 2.5, capacity_factor=None,
                 expert: str = "swiglu", n_shared: int = 0, dtype: str = "bf16",
                 precision: str = "fp32", logits=None, fast_router: bool = False,
-                batch_shape=None) -> dict:
+                batch_shape=None, out_dtype: str = "f32") -> dict:
     """Whole-layer forward (``MoE.__call__``, ``moe.py:170-294``).
 
     ``x`` [T,D] float32 values (bf16-representable when ``dtype="bf16"``).
@@ -556,6 +629,9 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
     ``expert_w_down [N,F,D]`` and, when ``n_shared > 0``, ``shared_w_*``.
     ``routing``: ``"sigmoid"`` (reference) or ``"softmax"`` (workload).
     ``logits``: precomputed router logits (identity-expert workload).
+    ``expert``: ``"swiglu"``, ``"identity"`` or ``"swiglu_fp8"`` (e4m3 operands,
+    :func:`expert_ffn_fp8`; quantised weights from ``params["fp8"]`` or
+    :func:`quantize_expert_weights`).  ``out_dtype="bf16"`` rounds the output.
     Returns a dict with every intermediate the kernels produce.
     """
     x = np.asarray(x, dtype=F32)
@@ -575,10 +651,25 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
     C = capacity_of(T, K, N, capacity_factor)
     plan = dispatch_plan(top_idx, N, C)
     x_c = bf16_round(x) if dtype == "bf16" else x
-    xs = permute_rows(x_c, plan["perm_src"], K)
-    if expert == "identity":
+    extra = {}
+    if expert == "swiglu_fp8":
+        xq, xsc = quantize_rows_e4m3(x_c)
+        perm = plan["perm_src"]
+        valid = perm >= 0
+        xs_q = np.zeros((perm.size, D), np.uint8)
+        xs_q[valid] = xq[perm[valid] // K]
+        xs_s = np.ones(perm.size, F32)
+        xs_s[valid] = xsc[perm[valid] // K]
+        wq = params["fp8"] if "fp8" in params else quantize_expert_weights(params)
+        ys, h, hq, hs = expert_ffn_fp8(xs_q, xs_s, plan["offsets"], wq["wg_q"], wq["wg_s"],
+                                       wq["wu_q"], wq["wu_s"], wq["wd_q"], wq["wd_s"])
+        xs = xs_q
+        extra = {"x_q": xq, "x_s": xsc, "xs_s": xs_s, "h": h, "hq": hq, "hs": hs, "fp8": wq}
+    elif expert == "identity":
+        xs = permute_rows(x_c, plan["perm_src"], K)
         ys = xs
     elif expert == "swiglu":
+        xs = permute_rows(x_c, plan["perm_src"], K)
         ys = expert_ffn(xs, plan["offsets"], params["expert_w_gate"], params["expert_w_up"],
                         params["expert_w_down"], precision=precision)
     else:
@@ -588,8 +679,10 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
         residual = shared_expert(x_c, params["shared_w_gate"], params["shared_w_up"],
                                  params["shared_w_down"], n_shared, precision=precision)
     out = combine(ys, plan["slot_pos"], gates, T, K, residual=residual)
+    if out_dtype == "bf16":
+        out = bf16_round(out)
     res = {"logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan,
-           "capacity": C, "xs": xs, "ys": ys, "out": out, "scores": scores}
+           "capacity": C, "xs": xs, "ys": ys, "out": out, "scores": scores, **extra}
     if routing == "sigmoid" and batch_shape is not None:
         Bb, Ss = batch_shape
         res["aux"] = aux_losses(logits, scores, top_idx, Bb, Ss, N)

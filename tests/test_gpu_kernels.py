@@ -295,3 +295,115 @@ def test_router_aux(gpu):
     assert np.allclose(got, [ref["router_z_loss"], ref["balance_loss"], ref["mean_entropy"]],
                        rtol=2e-5, atol=0)
     assert_bits_equal(host(counts), ref["expert_counts"], "expert_counts")
+
+
+# ------------------------------------------------------------------- fp8 --
+
+@pytest.mark.parametrize("D,xdt", [(4096, "bf16"), (256, "bf16"), (8, "f32"), (1032, "f32")])
+def test_permute_rows_fp8_bit_exact(gpu, D, xdt):
+    print(f"permute fp8 D={D} {xdt}", flush=True)
+    rng = np.random.default_rng(90 + D)
+    T, N, Kk = 700, 32, 4
+    x = (rng.standard_normal((T, D)) * np.exp(rng.uniform(-8, 4, (T, 1)))).astype(np.float32)
+    x[5] = 0.0
+    x[6, : min(D, 4)] = [-0.0, 1e-30, -1e-30, 0.0][: min(D, 4)]
+    if xdt == "bf16":
+        x = O.bf16_round(x)
+    top = O.topk_desc(rng.standard_normal((T, N), dtype=np.float32), Kk)
+    C = O.capacity_of(T, Kk, N, 1.0)
+    ref = O.dispatch_plan(top, N, C)
+    xq, xsc = O.quantize_rows_e4m3(x)
+    total = int(ref["offsets"][-1])
+    src = ref["perm_src"][:total] // Kk
+    xt = dev_bf16(x, gpu) if xdt == "bf16" else dev_f32(x, gpu)
+    plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, C)
+    xs_q, xs_s = K.permute_rows_fp8(xt, plan)
+    torch.cuda.synchronize()
+    assert_bits_equal(xs_q.cpu().numpy()[:total], xq[src], "xs_q")
+    assert_bits_equal(xs_s.cpu().numpy()[:total], xsc[src], "xs_scale")
+
+
+def test_quantize_rows_fp8_bit_exact_and_skips_past_offsets(gpu):
+    rng = np.random.default_rng(91)
+    R, F = 300, 2048
+    h = O.bf16_round((rng.standard_normal((R, F)) * np.exp(rng.uniform(-20, 6, (R, 1)))).astype(np.float32))
+    h[7] = 0.0
+    q_ref, s_ref = O.quantize_rows_e4m3(h)
+    q, s = K.quantize_rows_fp8(dev_bf16(h, gpu))
+    torch.cuda.synchronize()
+    assert_bits_equal(q.cpu().numpy(), q_ref, "codes")
+    assert_bits_equal(s.cpu().numpy(), s_ref, "scales")
+    offsets = torch.tensor([0, 100, 250], dtype=torch.int32, device=gpu)
+    q2, s2 = K.quantize_rows_fp8(dev_bf16(h, gpu), offsets)
+    torch.cuda.synchronize()
+    assert_bits_equal(q2.cpu().numpy()[:250], q_ref[:250], "codes below offsets[-1]")
+    assert np.all(s2.cpu().numpy()[250:] == 1.0)   # rows past the kept total untouched
+
+
+def test_pack_fp8_layouts(gpu):
+    rng = np.random.default_rng(92)
+    N, D, F = 3, 256, 384
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+    pgu, sgu = K.pack_fp8_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    pd, sd = K.pack_fp8_down(dev_f32(wd, gpu))
+    torch.cuda.synchronize()
+    wq = O.quantize_expert_weights({"expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd})
+    p = np.arange(2 * F)
+    col = (p // 64) * 32 + p % 32
+    is_up = (p % 64) >= 32
+    exp_codes = np.where(is_up[None, :, None], np.transpose(wq["wu_q"], (0, 2, 1))[:, col],
+                         np.transpose(wq["wg_q"], (0, 2, 1))[:, col])
+    exp_scales = np.where(is_up[None, :], wq["wu_s"][:, col], wq["wg_s"][:, col])
+    assert_bits_equal(pgu.cpu().numpy(), exp_codes, "packed fp8 gate/up")
+    assert_bits_equal(sgu.cpu().numpy(), exp_scales, "gate/up scales")
+    assert_bits_equal(pd.cpu().numpy(), np.transpose(wq["wd_q"], (0, 2, 1)), "packed fp8 down")
+    assert_bits_equal(sd.cpu().numpy(), wq["wd_s"], "down scales")
+
+
+FP8_GEMM_CASES = [
+    # name, D, F, segment sizes
+    ("ragged", 256, 128, [0, 1, 255, 256, 257, 600, 0, 31]),
+    ("wide", 4096, 2048, [300, 1024, 513]),
+]
+
+
+@pytest.mark.parametrize("case", FP8_GEMM_CASES, ids=lambda c: c[0])
+def test_grouped_gemm_fp8(gpu, case):
+    """fp8 GEMMs against float64 dot products of the same decoded operands and
+    scales: h = bf16(silu(g)*u) and ys = bf16(y), fp32 accumulation."""
+    name, D, F, sizes = case
+    print(f"fp8 gemm case {case}", flush=True)
+    rng = np.random.default_rng(93 + D)
+    N = len(sizes)
+    offsets = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(offsets[-1])
+    xq, xs = O.quantize_rows_e4m3(rng.standard_normal((R, D)).astype(np.float32))
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+    off_t = torch.from_numpy(offsets).to(gpu)
+    pgu, sgu = K.pack_fp8_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    pd, sd = K.pack_fp8_down(dev_f32(wd, gpu))
+    h = K.grouped_gate_up_fp8(torch.from_numpy(xq).to(gpu), torch.from_numpy(xs).to(gpu), off_t, pgu, sgu)
+    h_host = host(h)
+    hq, hs = O.quantize_rows_e4m3(h_host)
+    ys = K.grouped_down_fp8(torch.from_numpy(hq).to(gpu), torch.from_numpy(hs).to(gpu), off_t, pd, sd)
+    ys_host = host(ys)
+    torch.cuda.synchronize()
+    wq = O.quantize_expert_weights({"expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd})
+    x64 = O.e4m3_decode(xq).astype(np.float64) * xs[:, None]
+    h64 = O.e4m3_decode(hq).astype(np.float64) * hs[:, None]
+    for e in range(N):
+        a, b = offsets[e], offsets[e + 1]
+        if b == a:
+            continue
+        g = (x64[a:b] @ O.e4m3_decode(wq["wg_q"][e]).astype(np.float64)) * wq["wg_s"][e]
+        u = (x64[a:b] @ O.e4m3_decode(wq["wu_q"][e]).astype(np.float64)) * wq["wu_s"][e]
+        h_ref = g / (1 + np.exp(-g)) * u
+        err_h = np.abs(h_host[a:b] - h_ref)
+        assert np.all(err_h <= 8e-3 * np.abs(h_ref) + 1e-3 * np.abs(h_ref).max()), \
+            f"h expert {e}: max err {err_h.max()}"
+        y_ref = (h64[a:b] @ O.e4m3_decode(wq["wd_q"][e]).astype(np.float64)) * wq["wd_s"][e]
+        err_y = np.abs(ys_host[a:b] - y_ref)
+        assert np.all(err_y <= 8e-3 * np.abs(y_ref) + 1e-3 * np.abs(y_ref).max()), \
+            f"ys expert {e}: max err {err_y.max()}"

@@ -167,3 +167,65 @@ def test_moe_module_capacity_softmax(gpu):
     assert (ref["plan"]["keep"] == 0).any()
     err = O.normwise_rel_err(host(out).reshape(B * S, D), ref["out"])
     assert err < BF16_TOL
+
+
+FP8_TOL = 5e-2
+
+
+def _fp8_refs(inp, wl):
+    params = {"router": inp.router, "expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
+              "expert_w_down": inp.w_down}
+    r8 = O.moe_forward(inp.x, params, top_k=wl.top_k, routing="softmax",
+                       capacity_factor=wl.capacity_factor, expert="swiglu_fp8", out_dtype="bf16")
+    ref = O.moe_forward(inp.x, {**params, **O.dequantized_weights(r8["fp8"])}, top_k=wl.top_k,
+                        routing="softmax", capacity_factor=wl.capacity_factor, precision="fp32")
+    return r8, ref
+
+
+def test_fp8_workload_reduced_tokens(gpu):
+    """fp8 experts (e4m3 activations per token, weights per output channel):
+    routing, plan and dispatched codes bit-exact; output within 5e-2 normwise
+    of the float32 layer on the dequantised weights."""
+    wl = W.WORKLOADS["fp8_experts"].scaled(1024)
+    print(f"layer fp8_experts T={wl.tokens}", flush=True)
+    inp = W.make_inputs(wl, seed=0)
+    r8, ref = _fp8_refs(inp, wl)
+    res = DeviceLayer(inp, gpu).forward()
+    torch.cuda.synchronize()
+    check_routing_and_plan(res, r8["top_idx"], r8["gates"], r8["plan"], r8["logits"])
+    total = int(r8["plan"]["offsets"][-1])
+    assert np.array_equal(res["xs"].cpu().numpy()[:total], r8["xs"][:total]), "xs codes"
+    assert np.array_equal(res["xs_scale"].cpu().numpy()[:total], r8["xs_s"][:total]), "xs scales"
+    out = host(res["out"])
+    assert res["out"].dtype == torch.bfloat16
+    err = O.normwise_rel_err(out, ref["out"])
+    err_emul = O.normwise_rel_err(out, r8["out"])
+    print(f"fp8: normwise err vs fp32 on dequantised weights {err:.3e}, vs fp8 emulation {err_emul:.3e}",
+          flush=True)
+    assert err < FP8_TOL
+    assert err_emul < 1e-2
+
+
+def test_fp8_workload_full_size(gpu):
+    wl = W.WORKLOADS["fp8_experts"]
+    print(f"layer fp8_experts full size T={wl.tokens}", flush=True)
+    inp = W.make_inputs(wl, seed=0)
+    logits = O.router_logits(inp.x, inp.router)
+    idx, gates = O.route_softmax(logits, wl.top_k)
+    plan = O.dispatch_plan(idx, wl.n_experts, wl.capacity)
+    layer = DeviceLayer(inp, gpu)
+    res = layer.forward()
+    torch.cuda.synchronize()
+    check_routing_and_plan(res, idx, gates, plan, logits)
+    # sampled tokens against the float32 layer on the dequantised weights
+    wq = O.quantize_expert_weights({"expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
+                                    "expert_w_down": inp.w_down})
+    deq = O.dequantized_weights(wq)
+    sub = W.Inputs(wl, inp.x, router=inp.router, w_gate=deq["expert_w_gate"],
+                   w_up=deq["expert_w_up"], w_down=deq["expert_w_down"])
+    rng = np.random.default_rng(1)
+    tokens = np.sort(rng.choice(wl.tokens, 128, replace=False))
+    ref = sampled_token_ref(sub, idx, gates, plan, tokens)
+    err = O.normwise_rel_err(host(res["out"])[tokens], ref)
+    print(f"fp8 full size: sampled-token normwise err {err:.3e}", flush=True)
+    assert err < FP8_TOL

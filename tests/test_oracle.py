@@ -297,3 +297,100 @@ def test_aux_closed_forms():
     assert math.isclose(aux["balance_loss"], 1.0, rel_tol=1e-6)   # perfect balance
     assert math.isclose(aux["mean_entropy"], math.log(N), rel_tol=1e-6)
     assert aux["expert_counts"].tolist() == [B * S // 2] * N
+
+
+# ------------------------------------------------------------------- fp8 --
+
+def test_quantize_rows_e4m3_rule_matches_torch_conversion():
+    """Codes are torch's float8_e4m3fn conversion of clamp(a * (448/amax)),
+    the row maximum maps to 448, and an all-zero row gets codes 0, scale 1."""
+    rng = np.random.default_rng(80)
+    a = (rng.standard_normal((16, 300)) * np.exp(rng.uniform(-12, 3, (16, 1)))).astype(np.float32)
+    a[3] = 0.0
+    a[5, :7] = [-0.0, 1e-30, -1e-30, 3e-5, -3e-5, 0.0, 1e-38]
+    q, s = O.quantize_rows_e4m3(a)
+    amax = np.abs(a).max(axis=1)
+    inv = np.where(amax > 0, np.float32(448.0) / np.where(amax > 0, amax, 1), 1).astype(np.float32)
+    ref = torch.from_numpy(np.clip((a * inv[:, None]).astype(np.float32), -448, 448)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(q, ref)
+    assert s[3] == 1.0 and not q[3].any()
+    nz = amax > 0
+    assert np.array_equal(np.abs(O.e4m3_decode(q[nz])).max(axis=1), np.full(nz.sum(), 448.0, np.float32))
+    assert np.array_equal(s[nz], (amax[nz] / np.float32(448.0)).astype(np.float32))
+
+
+def test_quantize_cols_e4m3_is_rowwise_on_the_transpose():
+    rng = np.random.default_rng(81)
+    w = (0.02 * rng.standard_normal((3, 64, 40))).astype(np.float32)
+    q, s = O.quantize_cols_e4m3(w)
+    qt, st = O.quantize_rows_e4m3(np.swapaxes(w, -1, -2))
+    assert np.array_equal(q, np.swapaxes(qt, -1, -2)) and np.array_equal(s, st)
+
+
+def test_quantization_error_bound():
+    """e4m3 keeps 3 mantissa bits: dequantised values are within 2^-4 relative
+    (normal range) or half a subnormal step times the scale."""
+    rng = np.random.default_rng(82)
+    a = rng.standard_normal((8, 1000)).astype(np.float32)
+    q, s = O.quantize_rows_e4m3(a)
+    deq = O.e4m3_decode(q).astype(np.float64) * s[:, None]
+    err = np.abs(deq - a)
+    bound = np.maximum(np.abs(a) * 2.0 ** -4, s[:, None] * 2.0 ** -10) * 1.0001
+    assert np.all(err <= bound)
+
+
+def _e4m3_grid_matrix(rng, shape, axis):
+    """Values on the e4m3 grid whose maximum |v| along `axis` is exactly 448,
+    so per-row/column quantisation is the identity with scale 1."""
+    grid = O.e4m3_decode(np.arange(0, 126, dtype=np.uint8))          # 0 .. 448
+    v = rng.choice(grid[grid <= 64], size=shape) * rng.choice([-1.0, 1.0], size=shape)
+    v = v.astype(np.float32)
+    idx = [slice(None)] * len(shape)
+    idx[axis] = 0
+    v[tuple(idx)] = 448.0
+    return v
+
+
+def test_expert_ffn_fp8_reduces_to_library_matmul_on_exact_operands():
+    rng = np.random.default_rng(83)
+    N, D, F = 3, 64, 32
+    offsets = np.array([0, 5, 5, 17], np.int64)
+    R = int(offsets[-1])
+    x = _e4m3_grid_matrix(rng, (R, D), axis=1)
+    wg, wu = (_e4m3_grid_matrix(rng, (N, D, F), axis=1) for _ in range(2))
+    wd = _e4m3_grid_matrix(rng, (N, F, D), axis=1)
+    xq, xs = O.quantize_rows_e4m3(x)
+    assert np.array_equal(O.e4m3_decode(xq), x) and np.all(xs == 1.0)
+    wq = O.quantize_expert_weights({"expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd})
+    assert all(np.all(wq[k] == 1.0) for k in ("wg_s", "wu_s", "wd_s"))
+    ys, h, hq, hs = O.expert_ffn_fp8(xq, xs, offsets, wq["wg_q"], wq["wg_s"], wq["wu_q"],
+                                     wq["wu_s"], wq["wd_q"], wq["wd_s"])
+    for e in range(N):
+        a, b = offsets[e], offsets[e + 1]
+        if b == a:
+            continue
+        g = np.matmul(x[a:b].astype(np.float64), wg[e].astype(np.float64))
+        u = np.matmul(x[a:b].astype(np.float64), wu[e].astype(np.float64))
+        assert np.array_equal(h[a:b], O.bf16_round((g / (1 + np.exp(-g)) * u).astype(np.float32)))
+        hh = O.e4m3_decode(hq[a:b]).astype(np.float64) * hs[a:b, None]
+        y = np.matmul(hh, wd[e].astype(np.float64))
+        assert np.array_equal(ys[a:b], O.bf16_round(y.astype(np.float32)))
+
+
+def test_fp8_layer_within_tolerance_of_fp32_on_dequantised_weights():
+    """The fp8 rule's expected accuracy at a small shape: normwise error of the
+    e4m3 layer against the float32 layer on the dequantised weights < 5e-2."""
+    from hanuman_amd import workloads as W
+    wl = W.WORKLOADS["fp8_experts"].scaled(128)
+    wl = W.Workload(**{**wl.__dict__, "d_model": 512, "d_ff": 256})
+    inp = W.make_inputs(wl, seed=0)
+    params = {"router": inp.router, "expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
+              "expert_w_down": inp.w_down}
+    r8 = O.moe_forward(inp.x, params, top_k=wl.top_k, routing="softmax",
+                       capacity_factor=wl.capacity_factor, expert="swiglu_fp8", out_dtype="bf16")
+    ref = O.moe_forward(inp.x, {**params, **O.dequantized_weights(r8["fp8"])}, top_k=wl.top_k,
+                        routing="softmax", capacity_factor=wl.capacity_factor, precision="fp32")
+    assert np.array_equal(r8["top_idx"], ref["top_idx"])
+    err = O.normwise_rel_err(r8["out"], ref["out"])
+    assert err < 5e-2, err
