@@ -6,8 +6,11 @@ d_model 2048, 64 experts, top-8, d_ff 1024, capacity factor 1.25), with every
 input resident in HBM before the timed region.  One JSON line on stdout:
 
   value      tokens/s of the whole layer (1 GPU)
-  roofline   grouped GEMM (gate/up + down): algorithmic 6*R_kept*D*F FLOP over
-             the two kernels' HIP-event time, against dense bf16 MFMA peak
+  roofline   the dominant kernel, the gate/up grouped GEMM with the fused SwiGLU:
+             algorithmic 4*R_kept*D*F FLOP over its HIP-event time, against the
+             dense bf16 (or fp8) MFMA peak; traffic = its measured HBM bytes per
+             launch (profiles/hbm_traffic.json)
+  grouped_gemm  gate/up + down together (6*R_kept*D*F FLOP)
   kernels    every stage's HIP-event time and roofline fraction
   cpu_baseline  the NumPy float32 restatement of the layer (oracle/) timed on
              this host's cores on a 4096-token sample of the same workload
@@ -68,6 +71,19 @@ def algorithmic(wl, kept_rows: int) -> dict:
     return w
 
 
+def measured_traffic(workload: str) -> dict:
+    """HBM bytes per launch by kernel name, from the counter summary committed
+    in profiles/hbm_traffic.json (FETCH_SIZE/WRITE_SIZE runs calibrated against
+    a 1 GiB copy); empty when the workload was not measured."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    return {k: v["total"] for k, v in data.get("workloads", {}).get(workload, {}).items()}
+
+
 def cpu_baseline(wl_name: str, sample_tokens: int, seed: int) -> dict:
     import oracle as O
     from hanuman_amd import workloads as W
@@ -109,6 +125,9 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one 1 GiB device-to-device copy before the warm-up, as the "
+                         "known-size reference for HBM byte counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -176,6 +195,15 @@ def main():
         mark()
         return plan, out
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -212,23 +240,31 @@ def main():
                            "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4),
                            "flop": amount}
     tokens_per_s = wl.tokens / (ms_per_step / 1e3)
+    traffic = measured_traffic(name)
+    grouped_gemm = None
     if wl.expert == "swiglu":
-        flop = work["gate_up"][1] + work["down"][1]
-        peak = work["gate_up"][2]
+        # Dominant kernel: the gate/up grouped GEMM with the fused SwiGLU.
+        kname = f"grouped_gemm_kernel<true, {'true' if fp8 else 'false'}>"
+        flop, peak = work["gate_up"][1], work["gate_up"][2]
+        ach = flop / (stage_ms["gate_up"] / 1e3) / 1e12
+        roofline = {"kernel": kname, "bound": "mfma", "achieved": round(ach, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                    "traffic": traffic.get(kname), "flop_per_launch": flop,
+                    "ms": round(stage_ms["gate_up"], 4)}
+        both = work["gate_up"][1] + work["down"][1]
         t_gemm = (stage_ms["gate_up"] + stage_ms["down"]) / 1e3
-        ach = flop / t_gemm / 1e12
-        roofline = {"kernel": "grouped_gemm_kernel (gate/up + down)", "bound": "mfma",
-                    "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-                    "frac": round(ach / peak, 4), "traffic": None,
-                    "flop_per_launch": flop, "ms": round(t_gemm * 1e3, 4)}
+        grouped_gemm = {"kernels": "gate/up + down", "flop": both, "ms": round(t_gemm * 1e3, 4),
+                        "achieved": round(both / t_gemm / 1e12, 1), "unit": "TFLOP/s",
+                        "frac": round(both / t_gemm / 1e12 / peak, 4)}
     else:
-        b = work["permute"][1] + work["combine"][1]
-        t = (stage_ms["permute"] + stage_ms["combine"]) / 1e3
-        ach = b / t / 1e9
-        roofline = {"kernel": "permute_rows_kernel + combine_kernel", "bound": "hbm",
-                    "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": b,
-                    "ms": round(t * 1e3, 4)}
+        # Dispatch-only workload: the dominant kernel is the combine.
+        kname = "combine_kernel"
+        b = work["combine"][1]
+        ach = b / (stage_ms["combine"] / 1e3) / 1e9
+        roofline = {"kernel": kname, "bound": "hbm", "achieved": round(ach, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                    "traffic": next((v for k, v in traffic.items() if k.startswith(kname)), None),
+                    "bytes_per_launch": b, "ms": round(stage_ms["combine"], 4)}
     log(f"[bench] {ms_per_step:.4f} ms/step, {tokens_per_s / 1e6:.3f} M tokens/s; stages "
         + ", ".join(f"{k} {v:.4f}" for k, v in stage_ms.items()))
     del layer
@@ -258,9 +294,10 @@ def main():
                    "capacity_factor": wl.capacity_factor, "routing": wl.routing,
                    "kept_rows": kept, "parallelism": "single GPU, all experts resident"},
         "roofline": roofline,
+        "grouped_gemm": grouped_gemm,
         "kernels": kernels,
         "dispatch_hbm_gbs": kernels["permute"]["achieved"],
-        "grouped_gemm_mfma_util": roofline["frac"] if wl.expert == "swiglu" else None,
+        "grouped_gemm_mfma_util": grouped_gemm["frac"] if grouped_gemm else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
