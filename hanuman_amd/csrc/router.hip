@@ -134,45 +134,56 @@ __device__ __forceinline__ float load_w_f32<uint16_t>(const uint16_t* p, int64_t
 // (the next chunk's global loads are issued before the current chunk's
 // MFMAs).  The float32-rounded logits go through LDS to the wave-per-token
 // selection.
-constexpr int kRTokBlk = 64;
 constexpr int kRTokWave = 16;
 constexpr int kRDc = 32;
 constexpr int kRXPitch = kRDc + 1;
 
-template <int NT>
+// ES waves share a group of 16 tokens and split its expert tiles, so a
+// workgroup of 4 waves takes 64 / ES tokens.  With ES = 2 twice as many
+// workgroups fit the token count, two waves run on every SIMD and each keeps
+// NT/2 independent accumulator chains.
+template <int NT, int ES>
 struct RouterLds {
   static constexpr int kNP = 16 * NT;
   static constexpr int kWPitch = kNP + 8;
-  float x[2][kRTokBlk][kRXPitch];
+  static constexpr int kTB = 64 / ES;
+  float x[2][kTB][kRXPitch];
   float w[2][kRDc][kWPitch];
 };
 
-template <int NT, typename XT, typename WT>
+template <int NT, int ES, typename XT, typename WT>
 __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, const WT* __restrict__ w,
                                                      const float* __restrict__ bias, int64_t tokens,
                                                      int d_model, int n_experts, int top_k, int mode,
                                                      float rsf, float* __restrict__ logits,
                                                      int32_t* __restrict__ top_idx,
                                                      float* __restrict__ gates) {
-  constexpr int kNP = RouterLds<NT>::kNP;
+  static_assert(NT % ES == 0, "expert tiles must split evenly");
+  constexpr int kNP = RouterLds<NT, ES>::kNP;
+  constexpr int kTB = RouterLds<NT, ES>::kTB;
+  constexpr int kTG = kTB / kRTokWave;                // token groups per workgroup
+  constexpr int kNTW = NT / ES;                       // expert tiles per wave
   constexpr int kEPL = (kNP + 63) / 64;
-  constexpr int kXPer = kRTokBlk * kRDc / 256;        // x elements per thread per chunk (8)
   constexpr int kWPer = (kRDc * kNP + 255) / 256;     // w elements per thread per chunk
-  __shared__ RouterLds<NT> lds;
+  __shared__ RouterLds<NT, ES> lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRTokBlk;
+  const int tg = wave % kTG;
+  const int ep = wave / kTG;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTB;
 
-  // Staging assignment: x elements (tt, dd..dd+7) = (tid / 4, (tid % 4) * 8).
-  // d_model is a multiple of 8, so a group of 8 is wholly inside or outside
-  // the row.  Every load is unconditional from an in-range address (clamped
-  // token row, d or expert 0) and masked afterwards, so the loads of a chunk
-  // stay in flight together until they are parked in LDS.
-  static_assert(kXPer == 8, "x staging assumes eight activations per thread");
+  // Staging assignment: x elements (tt, dd..dd+7) = (tid / 4, (tid % 4) * 8)
+  // for the first 4*kTB threads.  d_model is a multiple of 8, so a group of 8
+  // is wholly inside or outside the row.  Every load is unconditional from an
+  // in-range address (clamped token row, d or expert 0) and masked
+  // afterwards, so the loads of a chunk stay in flight together until they
+  // are parked in LDS.
   const int xs_tt = tid >> 2;
+  const bool x_thread = xs_tt < kTB;
   const int xs_dd = (tid & 3) * 8;
-  const int64_t xs_row = (t0 + xs_tt < tokens ? t0 + xs_tt : tokens - 1) * static_cast<int64_t>(d_model);
+  const int64_t xs_tok = t0 + (x_thread ? xs_tt : 0);
+  const int64_t xs_row = (xs_tok < tokens ? xs_tok : tokens - 1) * static_cast<int64_t>(d_model);
   X8<XT> xr;
   float wr[kWPer];
   auto w_ok = [&](int q, int d0) {
@@ -192,9 +203,11 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     __builtin_amdgcn_sched_barrier(0);
   };
   auto park = [&](int buf, int d0) {
-    const bool x_ok = d0 + xs_dd < d_model;
+    if (x_thread) {
+      const bool x_ok = d0 + xs_dd < d_model;
 #pragma unroll
-    for (int q = 0; q < kXPer; ++q) lds.x[buf][xs_tt][xs_dd + q] = x_ok ? xr.get(q) : 0.0f;
+      for (int q = 0; q < 8; ++q) lds.x[buf][xs_tt][xs_dd + q] = x_ok ? xr.get(q) : 0.0f;
+    }
 #pragma unroll
     for (int q = 0; q < kWPer; ++q) {
       const int idx = q * 256 + tid;
@@ -202,14 +215,15 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     }
   };
 
-  f64x4 acc[NT];
+  f64x4 acc[kNTW];
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < kNTW; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[t][r] = 0.0;
 
-  const int a_row = wave * kRTokWave + (lane & 15);
+  const int a_row = tg * kRTokWave + (lane & 15);
   const int k_of_lane = lane >> 4;
+  const int col0 = ep * kNTW * 16 + (lane & 15);
   const int nchunks = (d_model + kRDc - 1) / kRDc;
   fetch(0);
   park(0, 0);
@@ -221,8 +235,8 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     for (int s = 0; s < kRDc / 4; ++s) {
       const double a = static_cast<double>(lds.x[buf][a_row][4 * s + k_of_lane]);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const double b = static_cast<double>(lds.w[buf][4 * s + k_of_lane][t * 16 + (lane & 15)]);
+      for (int t = 0; t < kNTW; ++t) {
+        const double b = static_cast<double>(lds.w[buf][4 * s + k_of_lane][col0 + t * 16]);
         acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
       }
     }
@@ -230,26 +244,29 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     __syncthreads();
   }
 
-  // Logits (float32) of this wave's 16 tokens into LDS, row = token, col = expert.
-  float* lg = &lds.w[0][0][0];  // kRTokBlk x kNP floats fit in the two W stages
-  static_assert(sizeof(float) * kRTokBlk * kNP <= sizeof(lds.w), "logit staging does not fit");
+  // float32 logits into LDS, row = token of the workgroup, col = expert.
+  float* lg = &lds.w[0][0][0];
+  static_assert(sizeof(float) * kTB * kNP <= sizeof(lds.w), "logit staging does not fit");
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < kNTW; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      lg[(wave * kRTokWave + (lane >> 4) + 4 * r) * kNP + t * 16 + (lane & 15)] =
+      lg[(tg * kRTokWave + (lane >> 4) + 4 * r) * kNP + col0 - (lane & 15) + t * 16 + (lane & 15)] =
           static_cast<float>(acc[t][r]);
   __syncthreads();
 
+  // Selection: wave w takes tokens w*kTB/4 .. (w+1)*kTB/4 - 1 of the workgroup.
+  constexpr int kSel = kTB / 4;
 #pragma unroll 1
-  for (int i = 0; i < kRTokWave; ++i) {
-    const int64_t tok = t0 + wave * kRTokWave + i;
+  for (int i = 0; i < kSel; ++i) {
+    const int row = wave * kSel + i;
+    const int64_t tok = t0 + row;
     if (tok >= tokens) break;
     float l[kEPL];
 #pragma unroll
     for (int j = 0; j < kEPL; ++j) {
       const int e = lane + 64 * j;
-      l[j] = e < kNP ? lg[(wave * kRTokWave + i) * kNP + e] : 0.0f;
+      l[j] = e < kNP ? lg[row * kNP + e] : 0.0f;
       if (e < n_experts) logits[tok * n_experts + e] = l[j];
     }
     select_and_gate<kEPL>(l, bias, n_experts, top_k, mode, rsf, top_idx + tok * top_k,
@@ -281,8 +298,9 @@ template <int NT, typename XT, typename WT>
 void launch_router(const void* x, const void* w, const float* bias, int64_t tokens, int d_model,
                    int n_experts, int top_k, int mode, float rsf, float* logits, int32_t* top_idx,
                    float* gates, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, kRTokBlk)));
-  hipLaunchKernelGGL((router_kernel<NT, XT, WT>), grid, dim3(256), 0, stream,
+  constexpr int ES = NT >= 2 ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, RouterLds<NT, ES>::kTB)));
+  hipLaunchKernelGGL((router_kernel<NT, ES, XT, WT>), grid, dim3(256), 0, stream,
                      static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
                      n_experts, top_k, mode, rsf, logits, top_idx, gates);
 }
