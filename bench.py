@@ -243,8 +243,11 @@ def main():
     traffic = measured_traffic(name)
     grouped_gemm = None
     if wl.expert == "swiglu":
-        # Dominant kernel: the gate/up grouped GEMM with the fused SwiGLU.
-        kname = f"grouped_gemm_kernel<true, {'true' if fp8 else 'false'}>"
+        # Dominant kernel: the gate/up grouped GEMM with the fused SwiGLU
+        # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
+        odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
+        kname = ("grouped_gemm_dma<true, true>" if fp8
+                 else f"grouped_gemm_regs<true, {'true' if odd else 'false'}>")
         flop, peak = work["gate_up"][1], work["gate_up"][2]
         ach = flop / (stage_ms["gate_up"] / 1e3) / 1e12
         roofline = {"kernel": kname, "bound": "mfma", "achieved": round(ach, 1), "peak": peak,

@@ -17,17 +17,18 @@
 // an XCD works on a few consecutive m-tiles of one expert and shares their A
 // rows and B columns in its L2.
 //
-// Main loop (per 64-wide K step): the next step's A and B tiles (2 x 32 KB)
-// go straight from global memory into the other LDS stage with
-// global_load_lds_dwordx4 (no register staging), while the current stage feeds
-// 4 x 16 v_mfma_f32_32x32x16_bf16 per wave (each wave owns a 128 x 128
-// quarter).  An LDS row holds 64 bf16 as eight 16-byte chunks; chunk c of row
-// r is stored at position c ^ (r & 7), so the eight lanes that read one MFMA
-// fragment row-group hit eight different bank groups.  Fragments are
-// double-buffered in registers and the instruction order is fenced: the next
-// sub-step's LDS reads and DMA issues go out before the current sub-step's 16
-// MFMAs.  The next tile's first stage is prefetched during the current tile's
-// last K step, so the pipeline does not drain between tiles.
+// Main loop (per K step of 128 bytes per row: 64 bf16 or 128 e4m3): each
+// wave owns a 128 x 128 quarter of the tile and runs 4 x 16 bf16 MFMAs
+// (v_mfma_f32_32x32x16_bf16) or 2 x 16 fp8 MFMAs per step from the current
+// LDS stage.  Global loads run two K steps ahead into two register slots
+// (2 x 64 KB per workgroup in flight) and each slot is written into the other
+// LDS stage during the step before it is used; the loads, LDS writes and
+// fragment reads of each sub-step are interleaved between its MFMAs, and a
+// step ends with one barrier that never waits for global memory.  An LDS row
+// holds 128 bytes as eight 16-byte chunks; chunk c of row r is stored at
+// position c ^ (r & 7), so the eight lanes that read one MFMA fragment
+// row-group hit eight different bank groups.  The load side runs on into the
+// next tile, so the pipeline does not drain between tiles.
 #include <atomic>
 
 #include "hmoe_common.h"
@@ -153,10 +154,80 @@ struct GemmElem<true> {
   }
 };
 
-// With FP8, a_scale [a_rows] and b_scale [n_experts * ncols] dequantise the
-// float32 accumulators in the epilogue (before the SwiGLU).
+// Epilogue of one tile: acc[i][j] lane L, element r is token row
+// wm*128 + i*32 + (L&31) and column wn*128 + j*32 + (r/4)*8 + (L/32)*4 + r%4.
+// With FP8 the accumulators are dequantised by the row and column scales;
+// with SWIGLU the gate/up column pairs become h = bf16(silu(gate) * up).
 template <bool SWIGLU, bool FP8>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], uint16_t* __restrict__ C,
+                                           int64_t ldc, const float* __restrict__ a_scale,
+                                           const float* __restrict__ b_scale, int ncols, int e,
+                                           int64_t row0, int64_t row_end, int n0, int wm, int wn,
+                                           int lane) {
+  const int frow = lane & 31;
+  const int col_lane = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = row0 + wm * 128 + i * 32 + frow;
+    if (row < row_end) {
+      uint16_t* crow = C + row * ldc;
+      const float sa = FP8 ? a_scale[row] : 1.0f;
+      const float* sb = FP8 ? b_scale + static_cast<int64_t>(e) * ncols + n0 + wn * 128 + col_lane : nullptr;
+      if (SWIGLU) {
+        const int hbase = (n0 + wn * 128) / 2;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float h[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float gv = acc[i][2 * p][g * 4 + q];
+              float uv = acc[i][2 * p + 1][g * 4 + q];
+              if (FP8) {
+                gv = gv * sa * sb[(2 * p) * 32 + g * 8 + q];
+                uv = uv * sa * sb[(2 * p + 1) * 32 + g * 8 + q];
+              }
+              h[q] = silu_f32(gv) * uv;
+            }
+            uint2 pk;
+            pk.x = pack_bf16x2_rne(h[0], h[1]);
+            pk.y = pack_bf16x2_rne(h[2], h[3]);
+            *reinterpret_cast<uint2*>(crow + hbase + p * 32 + g * 8 + col_lane) = pk;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              v[q] = acc[i][j][g * 4 + q];
+              if (FP8) v[q] = v[q] * sa * sb[j * 32 + g * 8 + q];
+            }
+            uint2 pk;
+            pk.x = pack_bf16x2_rne(v[0], v[1]);
+            pk.y = pack_bf16x2_rne(v[2], v[3]);
+            *reinterpret_cast<uint2*>(crow + n0 + wn * 128 + j * 32 + g * 8 + col_lane) = pk;
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Main loop with direct global -> LDS loads (used for the e4m3 operands,
+// whose 32-byte MFMA fragments leave no registers for load staging): the next
+// K step's A and B tiles (2 x 32 KB) go straight into the other LDS stage with
+// global_load_lds_dwordx4 while the current stage feeds the MFMAs; fragments
+// are double-buffered in registers and each sub-step's LDS reads and DMA
+// issues go out before its MFMAs.  With FP8, a_scale [a_rows] and b_scale
+// [n_experts * ncols] dequantise the float32 accumulators in the epilogue.
+template <bool SWIGLU, bool FP8>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
     const float* __restrict__ a_scale, const float* __restrict__ b_scale,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
@@ -286,7 +357,6 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
   __syncthreads();
   read_frags(0, 0, 0);
 
-  const int col_lane = (lane >> 5) * 4;
   for (int t = first; t < hi; t += per_xcd) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -303,64 +373,234 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     if (next) set_load_tile(t + per_xcd);
     kstep(next, 0);
 
-    // ---- epilogue: acc[i][j] lane L, element r = token row
-    // wm*128 + i*32 + (L&31), column wn*128 + j*32 + (r/4)*8 + (L/32)*4 + r%4.
     int e, n0;
     int64_t row0, row_end;
     decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    store_tile<SWIGLU, FP8>(acc, C, ldc, a_scale, b_scale, ncols, e, row0, row_end, n0, wm, wn, lane);
+    if (next) read_frags(0, cur ^ 1, 0);
+    cur ^= 1;
+  }
+}
+
+// Workgroup barrier that waits for this wave's LDS operations only.  Global
+// loads in flight stay in flight: their results land in registers, and the
+// compiler waits for each one before its register is read.
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maximum
+  __builtin_amdgcn_s_barrier();
+}
+
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+// Main loop with register-staged loads (bf16): global loads run two K steps
+// ahead of the MFMAs.  ODD: the K dimension has an odd number of 64-element
+// steps; every tile then runs one more step whose LDS stage is filled with
+// zeros, so tiles always start on an even step and the two register slots
+// alternate statically.
+template <bool SWIGLU, bool ODD>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+    const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
+    uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n) {
+  typedef GemmElem<false> E;
+  constexpr int kParts = 4 / E::kSub;  // load parts per MFMA sub-step
+  // The two stages live in dynamic LDS: stage g & 1 holds global K step g.
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int32_t tstart[kMaxExperts + 1];
+  __shared__ int32_t scan_tmp[kThreads];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  const int total =
+      __builtin_amdgcn_readfirstlane(scan_tiles(offsets, n_experts, tstart, scan_tmp) * n_tiles_n);
+  const int xcd = blockIdx.x % kNumXcd;
+  const int per_xcd = gridDim.x / kNumXcd;
+  const int slot = blockIdx.x / kNumXcd;
+  const int lo = static_cast<int>((static_cast<int64_t>(total) * xcd) / kNumXcd);
+  const int hi = static_cast<int>((static_cast<int64_t>(total) * (xcd + 1)) / kNumXcd);
+  const int first = lo + slot;
+  if (first >= hi) return;  // uniform per workgroup
+  const int row_bytes = kdim * E::kBytes;
+  const int ksteps = row_bytes / 128;
+  const int kpad = ODD ? ksteps + 1 : ksteps;  // steps per tile, even
+  const int n_my = (hi - first + per_xcd - 1) / per_xcd;
+  const int iters = n_my * kpad;  // K steps this workgroup runs, over all its tiles
+
+  // ---- global -> registers -> LDS --------------------------------------------
+  // Round i (0..7) of a K step: this thread loads 16-byte chunk ld_c of A row
+  // and B row i*32 + ld_r (eight threads cover a row's 128 bytes) and stores it
+  // at position ld_c ^ (row & 7) of the LDS row.  Loads run two K steps ahead
+  // of the MFMAs in two register slots; a slot is written to the idle LDS
+  // stage one step ahead, so the barrier at the end of a step never waits for
+  // global memory.
+  const int ld_r = tid >> 3;
+  const int ld_c = tid & 7;
+  const int st_pos = (ld_c ^ (ld_r & 7)) * 16;
+  const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
+  uint32_t a_off[8];
+  const uint8_t* a_tile = A;
+  const uint8_t* b_tile = B;
+  int ld_t = first, ld_kb = 0, ld_g = 0;  // load side: tile, K step in it, global step
+  auto set_load_tile = [&](int t) __attribute__((always_inline)) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    e = __builtin_amdgcn_readfirstlane(e);
+    n0 = __builtin_amdgcn_readfirstlane(n0);
+    const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
+    a_tile = A + static_cast<int64_t>(r0) * row_bytes;
+    b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes;
+    // Rows past the buffer (the last tile of the last segment) are clamped to
+    // its last row; their results are never stored.
+    const int64_t lim = a_rows - 1 - r0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int rr = i * 32 + ld_r;
+      rr = rr < lim ? rr : static_cast<int>(lim);
+      a_off[i] = static_cast<uint32_t>(rr * row_bytes + ld_c * 16);
+    }
+  };
+  // Part p (0..3): rounds 2p and 2p+1 of A and of B of load step ld_g.
+  auto issue_part = [&](u32x4* ra, u32x4* rb, int p) __attribute__((always_inline)) {
+    const int kb = ODD && ld_kb == ksteps ? ksteps - 1 : ld_kb;  // the zero step reloads a real one
+    const uint8_t* ab = a_tile + kb * 128;
+    const uint8_t* bb = b_tile + kb * 128;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * p + q;
+      ra[i] = *reinterpret_cast<const u32x4*>(ab + a_off[i]);
+      rb[i] = *reinterpret_cast<const u32x4*>(bb + b_off0 + static_cast<uint32_t>(i * 32 * row_bytes));
+    }
+  };
+  // Once every step is loaded the load side repeats the last one, so every
+  // K step issues the same loads.
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (ld_g + 1 < iters) {
+      ++ld_g;
+      if (++ld_kb == kpad) {
+        ld_kb = 0;
+        ld_t += per_xcd;
+        set_load_tile(ld_t);
+      }
+    }
+  };
+  auto park_part = [&](const u32x4* ra, const u32x4* rb, int stage, int p, uint32_t keep)
+      __attribute__((always_inline)) {
+    uint8_t* base = smem + stage * kStageBytes;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * p + q;
+      const int row = i * 32 + ld_r;
+      u32x4 va = ra[i], vb = rb[i];
+      if (ODD) {
+        va &= keep;
+        vb &= keep;
+      }
+      *reinterpret_cast<u32x4*>(base + row * 128 + st_pos) = va;
+      *reinterpret_cast<u32x4*>(base + 32768 + row * 128 + st_pos) = vb;
+    }
+  };
+  u32x4 ra0[8], rb0[8], ra1[8], rb1[8];
+
+  // ---- MFMA fragments -------------------------------------------------------
+  // The weight fragment is the first MFMA operand, so an accumulator lane
+  // holds one token row and groups of four consecutive output columns.
+  // Fragment i of the wave's 128 rows is 32 rows (4096 bytes) further down.
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31;
+  const int fhalf = lane >> 5;
+  const int fa_row = wm * 128 + frow;
+  const int fb_row = wn * 128 + frow;
+  typename E::frag_t fa[2][4], fb[2][4];
+  auto read_frags = [&](int buf, int stage, int s) __attribute__((always_inline)) {
+    const uint8_t* base = smem + stage * kStageBytes;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t row = row0 + wm * 128 + i * 32 + frow;
-      if (row < row_end) {
-        uint16_t* crow = C + row * ldc;
-        const float sa = FP8 ? a_scale[row] : 1.0f;
-        const float* sb = FP8 ? b_scale + static_cast<int64_t>(e) * ncols + n0 + wn * 128 + col_lane : nullptr;
-        if (SWIGLU) {
-          const int hbase = (n0 + wn * 128) / 2;
+      fa[buf][i] = E::read(base, (fa_row + 32 * i) * 128, fa_row, s, fhalf);
+      fb[buf][i] = E::read(base + 32768, (fb_row + 32 * i) * 128, fb_row, s, fhalf);
+    }
+  };
+  f32x16 acc[4][4];
+
+  // K step kb of a tile on stage P (= parity of the global step g; fragments
+  // for sub-step 0 are already in buffer 0).  Each sub-step issues a quarter
+  // of step g+2's loads into the free register slot, writes a quarter of step
+  // g+1's slot into stage P^1 (zeros if g+1 is a tile's padding step), reads
+  // the next sub-step's fragments and runs 16 MFMAs; the memory operations
+  // are spread between the MFMAs.
+  auto step = [&](auto Pc, int kb) __attribute__((always_inline)) {
+    constexpr int P = decltype(Pc)::value;
+    const uint32_t keep = ODD && kb + 1 == ksteps ? 0u : ~0u;
+    u32x4* ld_a = P == 0 ? ra0 : ra1;
+    u32x4* ld_b = P == 0 ? rb0 : rb1;
+    const u32x4* pk_a = P == 0 ? ra1 : ra0;
+    const u32x4* pk_b = P == 0 ? rb1 : rb0;
 #pragma unroll
-          for (int p = 0; p < 2; ++p) {
+    for (int s = 0; s < E::kSub; ++s) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              float h[4];
+      for (int pp = 0; pp < kParts; ++pp) issue_part(ld_a, ld_b, s * kParts + pp);
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                float gv = acc[i][2 * p][g * 4 + q];
-                float uv = acc[i][2 * p + 1][g * 4 + q];
-                if (FP8) {
-                  gv = gv * sa * sb[(2 * p) * 32 + g * 8 + q];
-                  uv = uv * sa * sb[(2 * p + 1) * 32 + g * 8 + q];
-                }
-                h[q] = silu_f32(gv) * uv;
-              }
-              uint2 pk;
-              pk.x = pack_bf16x2_rne(h[0], h[1]);
-              pk.y = pack_bf16x2_rne(h[2], h[3]);
-              *reinterpret_cast<uint2*>(crow + hbase + p * 32 + g * 8 + col_lane) = pk;
-            }
-          }
-        } else {
+      for (int pp = 0; pp < kParts; ++pp) park_part(pk_a, pk_b, P ^ 1, s * kParts + pp, keep);
+      if (s + 1 < E::kSub) read_frags((s + 1) & 1, P, s + 1);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              float v[4];
+        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
+      // Per 4 MFMAs: kParts global loads, kParts LDS writes, 2 * kParts LDS reads.
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                v[q] = acc[i][j][g * 4 + q];
-                if (FP8) v[q] = v[q] * sa * sb[j * 32 + g * 8 + q];
-              }
-              uint2 pk;
-              pk.x = pack_bf16x2_rne(v[0], v[1]);
-              pk.y = pack_bf16x2_rne(v[2], v[3]);
-              *reinterpret_cast<uint2*>(crow + n0 + wn * 128 + j * 32 + g * 8 + col_lane) = pk;
-            }
-          }
-        }
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, kParts, 0);      // global load
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, kParts, 0);      // LDS write
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kParts, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (next) read_frags(0, cur ^ 1, 0);
-    cur ^= 1;
+    advance();
+    barrier_lds();
+  };
+
+  set_load_tile(first);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) issue_part(ra0, rb0, p);
+  advance();
+#pragma unroll
+  for (int p = 0; p < 4; ++p) issue_part(ra1, rb1, p);
+  advance();
+#pragma unroll
+  for (int p = 0; p < 4; ++p) park_part(ra0, rb0, 0, p, ODD && ksteps == 0 ? 0u : ~0u);
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  int g = 0;
+  for (int t = first; t < hi; t += per_xcd) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int kb = 0; kb < kpad; kb += 2) {
+      step(IntC<0>{}, kb);
+      read_frags(0, 1, 0);
+      step(IntC<1>{}, kb + 1);
+      if (kb + 2 < kpad) read_frags(0, 0, 0);
+    }
+    g += kpad;
+
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    store_tile<SWIGLU, false>(acc, C, ldc, nullptr, nullptr, ncols, e, row0, row_end, n0, wm, wn, lane);
+    if (g < iters) read_frags(0, 0, 0);
   }
 }
 
@@ -389,10 +629,8 @@ int persistent_grid(hipStream_t s, int* grid, int* dev_out) {
   return HMOE_OK;
 }
 
-template <bool SWIGLU, bool FP8>
-bool set_lds_limit(int bytes) {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<SWIGLU, FP8>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+bool set_lds_limit(const void* kernel, int bytes) {
+  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
 }
 
 // Allows 2 * kStageBytes of dynamic LDS for every kernel variant, once per device.
@@ -400,8 +638,17 @@ int allow_dynamic_lds(int dev) {
   static std::atomic<bool> done[64];
   if (dev >= 0 && dev < 64 && done[dev].load(std::memory_order_acquire)) return HMOE_OK;
   const int bytes = 2 * kStageBytes;
-  if (!set_lds_limit<true, false>(bytes) || !set_lds_limit<false, false>(bytes) ||
-      !set_lds_limit<true, true>(bytes) || !set_lds_limit<false, true>(bytes)) {
+  const void* kernels[] = {
+      reinterpret_cast<const void*>(grouped_gemm_regs<true, false>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<true, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, false>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_dma<true, true>),
+      reinterpret_cast<const void*>(grouped_gemm_dma<false, true>),
+  };
+  bool ok = true;
+  for (const void* k : kernels) ok = ok && set_lds_limit(k, bytes);
+  if (!ok) {
     set_error("grouped GEMM: cannot allow %d bytes of dynamic LDS on device %d", bytes, dev);
     return HMOE_ERR_HIP;
   }
@@ -426,14 +673,24 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
   const uint8_t* a = static_cast<const uint8_t*>(A);
   const uint8_t* b = static_cast<const uint8_t*>(B);
   uint16_t* c = static_cast<uint16_t*>(C);
-#define HMOE_LAUNCH_GEMM(SW, F8)                                                                  \
-  hipLaunchKernelGGL((grouped_gemm_kernel<SW, F8>), dim3(grid), dim3(kThreads), lds, s, a, b,   \
-                     a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n)
-  if (swiglu && !fp8) HMOE_LAUNCH_GEMM(true, false);
-  else if (!swiglu && !fp8) HMOE_LAUNCH_GEMM(false, false);
-  else if (swiglu && fp8) HMOE_LAUNCH_GEMM(true, true);
-  else HMOE_LAUNCH_GEMM(false, true);
-#undef HMOE_LAUNCH_GEMM
+  const bool odd = ((static_cast<int64_t>(kdim) * (fp8 ? 1 : 2) / 128) & 1) != 0;
+  if (fp8) {
+    if (swiglu)
+      hipLaunchKernelGGL((grouped_gemm_dma<true, true>), dim3(grid), dim3(kThreads), lds, s, a, b,
+                         a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n);
+    else
+      hipLaunchKernelGGL((grouped_gemm_dma<false, true>), dim3(grid), dim3(kThreads), lds, s, a, b,
+                         a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n);
+  } else {
+#define HMOE_LAUNCH_REGS(SW, OD)                                                                  \
+  hipLaunchKernelGGL((grouped_gemm_regs<SW, OD>), dim3(grid), dim3(kThreads), lds, s, a, b,      \
+                     offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n)
+    if (swiglu && odd) HMOE_LAUNCH_REGS(true, true);
+    else if (swiglu) HMOE_LAUNCH_REGS(true, false);
+    else if (odd) HMOE_LAUNCH_REGS(false, true);
+    else HMOE_LAUNCH_REGS(false, false);
+#undef HMOE_LAUNCH_REGS
+  }
   return check_launch(what);
 }
 
