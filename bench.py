@@ -15,7 +15,7 @@ input resident in HBM before the timed region.  One JSON line on stdout:
   cpu_baseline  the NumPy float32 restatement of the layer (oracle/) timed on
              this host's cores on a 4096-token sample of the same workload
 
-Usage: python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+Usage: python bench.py [--steps K] [--warmup W] [--spinup-ms MS] [--workload NAME] [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -121,6 +121,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--spinup-ms", type=float, default=400.0,
+                    help="keep running untimed warm-up steps until this much time has passed")
     ap.add_argument("--workload", default=None)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -204,8 +206,16 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
 
-    for _ in range(args.warmup):
+    # Warm-up: at least `warmup` steps and at least `spinup_ms` of back-to-back
+    # work, because the GPU clock ramps up over tens of milliseconds of load
+    # (a 20-step burst right after set-up runs ~10 % slower than steady state).
+    t_warm = time.perf_counter()
+    warm_steps = 0
+    while warm_steps < args.warmup or (time.perf_counter() - t_warm) * 1e3 < args.spinup_ms:
         step()
+        warm_steps += 1
+        if warm_steps % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
 
     # Timed region: exactly `steps` layer forwards, events between stages.
@@ -286,6 +296,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
