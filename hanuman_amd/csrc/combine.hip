@@ -3,8 +3,10 @@
 //
 // One wave per token.  Lane k < K loads slot k's row index and gate; the wave
 // then streams the D columns in 8-element (16-byte bf16) chunks, issuing the
-// K row loads of a chunk pair before accumulating so that up to 2*K loads are
-// in flight per lane.  Accumulation order is k ascending from +0.0; the
+// K row loads of several chunks before accumulating (up to 32 loads in flight
+// per lane for bf16 rows).  Rows are read and outputs written exactly once, so
+// both use non-temporal accesses (measured 138 -> 120 us at 16384 tokens x 8
+// slots x 2048).  Accumulation order is k ascending from +0.0; the
 // product of two bf16 values is exact in float32, so a fused multiply-add and
 // the oracle's multiply-then-add round identically.
 #include "hmoe_common.h"
@@ -17,7 +19,9 @@ struct Row8;
 template <>
 struct Row8<uint16_t> {
   u32x4 v;
-  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  }
   __device__ __forceinline__ float get(int i) const {
     const uint32_t w = v[i >> 1];
     return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
@@ -27,8 +31,8 @@ template <>
 struct Row8<float> {
   f32x4 a, b;
   __device__ __forceinline__ void load(const float* p) {
-    a = *reinterpret_cast<const f32x4*>(p);
-    b = *reinterpret_cast<const f32x4*>(p + 4);
+    a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
   }
   __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
 };
@@ -39,18 +43,25 @@ template <>
 __device__ __forceinline__ void store_out8<float>(float* dst, const float (&acc)[8]) {
   f32x4 a = {acc[0], acc[1], acc[2], acc[3]};
   f32x4 b = {acc[4], acc[5], acc[6], acc[7]};
-  *reinterpret_cast<f32x4*>(dst) = a;
-  *reinterpret_cast<f32x4*>(dst + 4) = b;
+  __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(dst));
+  __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(dst + 4));
 }
 template <>
 __device__ __forceinline__ void store_out8<uint16_t>(uint16_t* dst, const float (&acc)[8]) {
   u32x4 o = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
              pack_bf16x2(acc[6], acc[7])};
-  *reinterpret_cast<u32x4*>(dst) = o;
+  __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst));
 }
 
 constexpr int kMaxK = 16;
-constexpr int kChunksInFlight = 2;
+
+// Chunks whose K row loads are issued together: 32 row loads per lane for
+// bf16 rows (4 VGPRs each), 16 for float32 rows (8 VGPRs each).
+template <typename TY, int KMAX>
+constexpr int chunks_in_flight() {
+  constexpr int loads = sizeof(TY) == 2 ? 32 : 16;
+  return loads / KMAX < 1 ? 1 : (loads / KMAX > 4 ? 4 : loads / KMAX);
+}
 
 // acc + g*y.  For bf16 rows the product is exact in float32, so the fused
 // form rounds like the oracle's multiply-then-add; float32 rows need the
@@ -92,6 +103,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const TY* __restrict__ ys,
     pos[k] = __shfl(my_pos, k, 64);
     g[k] = __shfl(my_g, k, 64);
   }
+  constexpr int kChunksInFlight = chunks_in_flight<TY, KMAX>();
   const int chunks = d_model / 8;
   for (int c0 = lane; c0 < chunks; c0 += 64 * kChunksInFlight) {
     Row8<TY> rows[kChunksInFlight][KMAX];

@@ -154,6 +154,11 @@ template <>
 struct Chunk8<uint16_t> {
   u32x4 v;
   __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
+  // For data read exactly once (no reuse through the caches).
+  __device__ __forceinline__ void load_nt(const uint16_t* p) {
+    v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  }
+  __device__ __forceinline__ void zero() { v = u32x4{0u, 0u, 0u, 0u}; }
   __device__ __forceinline__ float get(int i) const {
     const uint32_t w = v[i >> 1];
     return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
@@ -165,6 +170,14 @@ struct Chunk8<float> {
   __device__ __forceinline__ void load(const float* p) {
     a = *reinterpret_cast<const f32x4*>(p);
     b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ void load_nt(const float* p) {
+    a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
+  }
+  __device__ __forceinline__ void zero() {
+    a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    b = a;
   }
   __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
 };
@@ -239,6 +252,14 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const TI* __restrict_
 // amax/448 (both divisions correctly rounded); an all-zero row gets scale 1.
 constexpr float kE4m3Max = 448.0f;
 
+// Scale and its inverse from the lane-partial amax (reduced over the wave).
+__device__ __forceinline__ void scales_from_amax(float amax, float& s, float& inv) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  s = amax > 0.0f ? amax / kE4m3Max : 1.0f;
+  inv = amax > 0.0f ? kE4m3Max / amax : 1.0f;
+}
+
 template <typename TI>
 __device__ __forceinline__ void wave_row_scales(const TI* __restrict__ row, int chunks, float& s,
                                                 float& inv) {
@@ -250,10 +271,27 @@ __device__ __forceinline__ void wave_row_scales(const TI* __restrict__ row, int 
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v.get(i)));
   }
+  scales_from_amax(amax, s, inv);
+}
+
+// Rows of up to 64 * kRowRegs 8-element chunks (4096 elements) are read once
+// and kept in registers between the amax reduction and the quantisation.
+constexpr int kRowRegs = 8;
+
+template <typename TI>
+__device__ __forceinline__ void load_row_regs(const TI* __restrict__ row, int chunks,
+                                              Chunk8<TI> (&v)[kRowRegs], float& s, float& inv) {
+  const int lane = threadIdx.x & 63;
+  float amax = 0.0f;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  s = amax > 0.0f ? amax / kE4m3Max : 1.0f;
-  inv = amax > 0.0f ? kE4m3Max / amax : 1.0f;
+  for (int u = 0; u < kRowRegs; ++u) {
+    const int c = u * 64 + lane;
+    v[u].zero();
+    if (c < chunks) v[u].load_nt(row + static_cast<int64_t>(c) * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[u].get(i)));
+  }
+  scales_from_amax(amax, s, inv);
 }
 
 template <typename TI>
@@ -270,7 +308,9 @@ __device__ __forceinline__ uint2 quant8_e4m3(const Chunk8<TI>& v, float inv) {
 }
 
 // One wave per token: quantise the row once and write it to every kept slot.
-template <typename TI>
+// REGS: the row fits in registers (d_model <= 64 * kRowRegs * 8) and is read
+// once; otherwise it is read twice (amax pass, then quantisation).
+template <typename TI, bool REGS>
 __global__ __launch_bounds__(256) void permute_rows_fp8_kernel(
     const TI* __restrict__ x, int64_t tokens, int d_model, int top_k,
     const int32_t* __restrict__ slot_pos, uint8_t* __restrict__ xs_q, float* __restrict__ xs_scale) {
@@ -281,6 +321,23 @@ __global__ __launch_bounds__(256) void permute_rows_fp8_kernel(
   const int chunks = d_model / 8;
   const TI* src = x + t * d_model;
   float s, inv;
+  if (REGS) {
+    Chunk8<TI> v[kRowRegs];
+    load_row_regs(src, chunks, v, s, inv);
+    if (lane < top_k && my_pos >= 0) xs_scale[my_pos] = s;
+#pragma unroll
+    for (int u = 0; u < kRowRegs; ++u) {
+      if (u * 64 >= chunks) break;  // uniform
+      const int c = u * 64 + lane;
+      const uint2 q = quant8_e4m3(v[u], inv);
+      for (int k = 0; k < top_k; ++k) {
+        const int32_t pos = __shfl(my_pos, k, 64);
+        if (pos >= 0 && c < chunks)
+          *reinterpret_cast<uint2*>(xs_q + static_cast<int64_t>(pos) * d_model + c * 8) = q;
+      }
+    }
+    return;
+  }
   wave_row_scales(src, chunks, s, inv);
   if (lane < top_k && my_pos >= 0) xs_scale[my_pos] = s;
   // Wave-uniform loop: every lane takes part in the slot broadcasts.
@@ -299,7 +356,8 @@ __global__ __launch_bounds__(256) void permute_rows_fp8_kernel(
 }
 
 // One wave per row of a bf16 matrix; rows at or past offsets[n_experts] (when
-// given) are skipped.
+// given) are skipped.  REGS as for the permutation.
+template <bool REGS>
 __global__ __launch_bounds__(256) void quantize_rows_fp8_kernel(
     const uint16_t* __restrict__ a, int64_t rows, int cols, const int32_t* __restrict__ offsets,
     int n_experts, uint8_t* __restrict__ q, float* __restrict__ scale) {
@@ -310,6 +368,17 @@ __global__ __launch_bounds__(256) void quantize_rows_fp8_kernel(
   const int chunks = cols / 8;
   const uint16_t* src = a + r * cols;
   float s, inv;
+  if (REGS) {
+    Chunk8<uint16_t> v[kRowRegs];
+    load_row_regs(src, chunks, v, s, inv);
+    if (lane == 0) scale[r] = s;
+#pragma unroll
+    for (int u = 0; u < kRowRegs; ++u) {
+      const int c = u * 64 + lane;
+      if (c < chunks) *reinterpret_cast<uint2*>(q + r * cols + c * 8) = quant8_e4m3(v[u], inv);
+    }
+    return;
+  }
   wave_row_scales(src, chunks, s, inv);
   if (lane == 0) scale[r] = s;
   for (int c = lane; c < chunks; c += 64) {
@@ -336,14 +405,15 @@ extern "C" int hmoe_permute_rows_fp8(const void* x, int x_dtype, int64_t tokens,
   HMOE_REQUIRE(x && slot_pos && xs_q && xs_scale, "permute_rows_fp8: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4)));
-  if (x_dtype == HMOE_BF16)
-    hipLaunchKernelGGL(permute_rows_fp8_kernel<uint16_t>, grid, dim3(256), 0, s,
-                       static_cast<const uint16_t*>(x), tokens, d_model, top_k, slot_pos, xs_q,
-                       xs_scale);
-  else
-    hipLaunchKernelGGL(permute_rows_fp8_kernel<float>, grid, dim3(256), 0, s,
-                       static_cast<const float*>(x), tokens, d_model, top_k, slot_pos, xs_q,
-                       xs_scale);
+  const bool regs = d_model <= 64 * kRowRegs * 8;
+#define HMOE_LAUNCH_PERM8(TI, REGS)                                                              \
+  hipLaunchKernelGGL((permute_rows_fp8_kernel<TI, REGS>), grid, dim3(256), 0, s,                 \
+                     static_cast<const TI*>(x), tokens, d_model, top_k, slot_pos, xs_q, xs_scale)
+  if (x_dtype == HMOE_BF16 && regs) HMOE_LAUNCH_PERM8(uint16_t, true);
+  else if (x_dtype == HMOE_BF16) HMOE_LAUNCH_PERM8(uint16_t, false);
+  else if (regs) HMOE_LAUNCH_PERM8(float, true);
+  else HMOE_LAUNCH_PERM8(float, false);
+#undef HMOE_LAUNCH_PERM8
   return check_launch("hmoe_permute_rows_fp8");
 }
 
@@ -359,9 +429,13 @@ extern "C" int hmoe_quantize_rows_fp8(const void* a, int64_t rows, int cols,
   if (rows == 0) return HMOE_OK;
   HMOE_REQUIRE(a && q && scale, "quantize_rows_fp8: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(quantize_rows_fp8_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))),
-                     dim3(256), 0, s, static_cast<const uint16_t*>(a), rows, cols, offsets,
-                     n_experts, q, scale);
+  const dim3 grid(static_cast<unsigned>(ceil_div(rows, 4)));
+  if (cols <= 64 * kRowRegs * 8)
+    hipLaunchKernelGGL(quantize_rows_fp8_kernel<true>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(a), rows, cols, offsets, n_experts, q, scale);
+  else
+    hipLaunchKernelGGL(quantize_rows_fp8_kernel<false>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(a), rows, cols, offsets, n_experts, q, scale);
   return check_launch("hmoe_quantize_rows_fp8");
 }
 
