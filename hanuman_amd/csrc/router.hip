@@ -130,13 +130,14 @@ __device__ __forceinline__ float load_w_f32<uint16_t>(const uint16_t* p, int64_t
 //
 // A workgroup of 4 waves takes 64 tokens; each wave 16 tokens against all
 // experts (NT tiles of 16 experts, zero-padded past n_experts).  x and W are
-// staged in LDS as float32, 32 d at a time, double-buffered through registers
+// staged in LDS as float32, 64 (or 32) d at a time, double-buffered through registers
 // (the next chunk's global loads are issued before the current chunk's
 // MFMAs).  The float32-rounded logits go through LDS to the wave-per-token
 // selection.
 constexpr int kRTokWave = 16;
-constexpr int kRDc = 32;
-constexpr int kRXPitch = kRDc + 1;
+// d per LDS chunk (one barrier per chunk): 64 while the staging of up to 64
+// experts fits two workgroups per CU, 32 beyond.
+constexpr int router_dc(int nt) { return nt <= 4 ? 64 : 32; }
 
 // ES waves share a group of 16 tokens and split its expert tiles, so a
 // workgroup of 4 waves takes 64 / ES tokens.  With ES = 2 twice as many
@@ -147,8 +148,9 @@ struct RouterLds {
   static constexpr int kNP = 16 * NT;
   static constexpr int kWPitch = kNP + 8;
   static constexpr int kTB = 64 / ES;
-  float x[2][kTB][kRXPitch];
-  float w[2][kRDc][kWPitch];
+  static constexpr int kDc = router_dc(NT);
+  float x[2][kTB][kDc + 1];
+  float w[2][kDc][kWPitch];
 };
 
 template <int NT, int ES, typename XT, typename WT>
@@ -161,6 +163,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   static_assert(NT % ES == 0, "expert tiles must split evenly");
   constexpr int kNP = RouterLds<NT, ES>::kNP;
   constexpr int kTB = RouterLds<NT, ES>::kTB;
+  constexpr int kRDc = RouterLds<NT, ES>::kDc;
   constexpr int kTG = kTB / kRTokWave;                // token groups per workgroup
   constexpr int kNTW = NT / ES;                       // expert tiles per wave
   constexpr int kEPL = (kNP + 63) / 64;
@@ -173,26 +176,39 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   const int ep = wave / kTG;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTB;
 
-  // Staging assignment: x elements (tt, dd..dd+7) = (tid / 4, (tid % 4) * 8)
-  // for the first 4*kTB threads.  d_model is a multiple of 8, so a group of 8
-  // is wholly inside or outside the row.  Every load is unconditional from an
+  // Staging assignment: x elements (tt, dd..dd+7) = (g / kXT, (g % kXT) * 8) for
+  // the groups g = tid + 256 r < kXT*kTB (kXT = kRDc / 8 groups per token
+  // row).  d_model is a multiple of 8, so a group of 8 is wholly inside or
+  // outside the row.  Every load is unconditional from an
   // in-range address (clamped token row, d or expert 0) and masked
   // afterwards, so the loads of a chunk stay in flight together until they
   // are parked in LDS.
-  const int xs_tt = tid >> 2;
-  const bool x_thread = xs_tt < kTB;
-  const int xs_dd = (tid & 3) * 8;
-  const int64_t xs_tok = t0 + (x_thread ? xs_tt : 0);
-  const int64_t xs_row = (xs_tok < tokens ? xs_tok : tokens - 1) * static_cast<int64_t>(d_model);
-  X8<XT> xr;
+  constexpr int kXT = kRDc / 8;
+  constexpr int kXR = (kXT * kTB + 255) / 256;  // x groups per thread
+  int xs_tt[kXR], xs_dd[kXR];
+  bool x_thread[kXR];
+  int64_t xs_row[kXR];
+#pragma unroll
+  for (int r = 0; r < kXR; ++r) {
+    const int g = tid + 256 * r;
+    xs_tt[r] = g / kXT;
+    x_thread[r] = xs_tt[r] < kTB;
+    xs_dd[r] = (g % kXT) * 8;
+    const int64_t tok = t0 + (x_thread[r] ? xs_tt[r] : 0);
+    xs_row[r] = (tok < tokens ? tok : tokens - 1) * static_cast<int64_t>(d_model);
+  }
+  X8<XT> xr[kXR];
   float wr[kWPer];
   auto w_ok = [&](int q, int d0) {
     const int idx = q * 256 + tid;
     return idx < kRDc * kNP && idx % kNP < n_experts && d0 + idx / kNP < d_model;
   };
   auto fetch = [&](int d0) {
-    const int dx = d0 + xs_dd;
-    xr.load(x + xs_row + (dx < d_model ? dx : 0));
+#pragma unroll
+    for (int r = 0; r < kXR; ++r) {
+      const int dx = d0 + xs_dd[r];
+      xr[r].load(x + xs_row[r] + (dx < d_model ? dx : 0));
+    }
 #pragma unroll
     for (int q = 0; q < kWPer; ++q) {
       const int idx = q * 256 + tid;
@@ -203,10 +219,13 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     __builtin_amdgcn_sched_barrier(0);
   };
   auto park = [&](int buf, int d0) {
-    if (x_thread) {
-      const bool x_ok = d0 + xs_dd < d_model;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) lds.x[buf][xs_tt][xs_dd + q] = x_ok ? xr.get(q) : 0.0f;
+    for (int r = 0; r < kXR; ++r) {
+      if (x_thread[r]) {
+        const bool x_ok = d0 + xs_dd[r] < d_model;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) lds.x[buf][xs_tt[r]][xs_dd[r] + q] = x_ok ? xr[r].get(q) : 0.0f;
+      }
     }
 #pragma unroll
     for (int q = 0; q < kWPer; ++q) {
