@@ -280,6 +280,52 @@ def test_grouped_gemm(gpu, case):
             f"ys expert {e}: max err {err_y.max()}"
 
 
+ODD_K_CASES = [
+    # name, D, F, segment sizes: gate/up reduces over D, down over F; an odd
+    # number of 64-element K steps takes the zero-padded extra step per tile
+    ("gate_up_k192", 192, 128, [0, 5, 300, 256, 1]),
+    ("down_k192", 256, 192, [7, 0, 513, 64]),
+    ("down_k64", 256, 64, [200, 1, 300]),
+]
+
+
+@pytest.mark.parametrize("case", ODD_K_CASES, ids=lambda c: c[0])
+def test_grouped_gemm_odd_k_steps(gpu, case):
+    name, D, F, sizes = case
+    print(f"gemm odd-k case {case}", flush=True)
+    rng = np.random.default_rng(90 + D + F)
+    N = len(sizes)
+    offsets = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(offsets[-1])
+    off_t = torch.from_numpy(offsets).to(gpu)
+    if name.startswith("gate_up"):
+        xs = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
+        wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+        out = host(K.grouped_gate_up(dev_bf16(xs, gpu), off_t, K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))))
+        wgb, wub = (O.bf16_round(w).astype(np.float64) for w in (wg, wu))
+        for e in range(N):
+            a, b = offsets[e], offsets[e + 1]
+            if b == a:
+                continue
+            x64 = xs[a:b].astype(np.float64)
+            g, u = x64 @ wgb[e], x64 @ wub[e]
+            ref = g / (1 + np.exp(-g)) * u
+            err = np.abs(out[a:b] - ref)
+            assert np.all(err <= 8e-3 * np.abs(ref) + 1e-3 * np.abs(ref).max()), f"h expert {e}: {err.max()}"
+    else:
+        h = O.bf16_round(rng.standard_normal((R, F)).astype(np.float32))
+        wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+        out = host(K.grouped_down(dev_bf16(h, gpu), off_t, K.pack_down(dev_f32(wd, gpu))))
+        wdb = O.bf16_round(wd).astype(np.float64)
+        for e in range(N):
+            a, b = offsets[e], offsets[e + 1]
+            if b == a:
+                continue
+            ref = h[a:b].astype(np.float64) @ wdb[e]
+            err = np.abs(out[a:b] - ref)
+            assert np.all(err <= 8e-3 * np.abs(ref) + 1e-3 * np.abs(ref).max()), f"ys expert {e}: {err.max()}"
+
+
 # --------------------------------------------------------------------- aux --
 
 def test_router_aux(gpu):
