@@ -155,7 +155,10 @@ def main():
     torch.cuda.synchronize()
 
     fp8 = wl.expert_dtype == "fp8"
-    stages = ["router", "plan", "permute"]
+    # bf16 SwiGLU experts: the row permutation is done by the gate/up GEMM's
+    # own loads (no dispatched copy of x), so there is no separate stage.
+    fused = layer.fused_dispatch
+    stages = ["router", "plan"] + ([] if fused else ["permute"])
     if wl.expert == "swiglu":
         stages += ["gate_up", "quant_h", "down"] if fp8 else ["gate_up", "down"]
     stages += ["combine"]
@@ -182,6 +185,11 @@ def main():
             h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
             mark()
             ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, layer.w_down, layer.w_down_scale)
+            mark()
+        elif fused:
+            h = K.grouped_gate_up_gather(layer.x, plan, layer.w_gate_up)
+            mark()
+            ys = K.grouped_down(h, plan.offsets, layer.w_down)
             mark()
         else:
             xs = K.permute_rows(layer.x, plan, torch.bfloat16)
@@ -257,7 +265,8 @@ def main():
         # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
         kname = ("grouped_gemm_dma<true, true>" if fp8
-                 else f"grouped_gemm_regs<true, {'true' if odd else 'false'}>")
+                 else f"grouped_gemm_regs<true, {'true' if odd else 'false'}, "
+                      f"{'true' if fused else 'false'}>")
         flop, peak = work["gate_up"][1], work["gate_up"][2]
         ach = flop / (stage_ms["gate_up"] / 1e3) / 1e12
         roofline = {"kernel": kname, "bound": "mfma", "achieved": round(ach, 1), "peak": peak,
@@ -310,7 +319,9 @@ def main():
         "roofline": roofline,
         "grouped_gemm": grouped_gemm,
         "kernels": kernels,
-        "dispatch_hbm_gbs": kernels["permute"]["achieved"],
+        "dispatch_hbm_gbs": kernels["permute"]["achieved"] if "permute" in kernels else None,
+        "dispatch": ("fused into the gate/up GEMM's row loads (standalone rate: the "
+                     "dispatch_identity workload)") if fused else "hmoe_permute_rows",
         "grouped_gemm_mfma_util": grouped_gemm["frac"] if grouped_gemm else None,
         "cpu_baseline": cpu,
     }

@@ -46,6 +46,8 @@ SIGNATURES = {
     "hmoe_packed_down_bytes": (_sz, [_i32, _i32, _i32]),
     "hmoe_pack_down": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "hmoe_grouped_gate_up": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32, _i32, _vp,
+                                           _vp, _vp]),
     "hmoe_grouped_down": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "hmoe_combine": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp]),
     "hmoe_permute_rows_fp8": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),

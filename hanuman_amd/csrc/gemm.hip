@@ -489,12 +489,16 @@ struct IntC {
 // ahead of the MFMAs.  ODD: the K dimension has an odd number of 64-element
 // steps; every tile then runs one more step whose LDS stage is filled with
 // zeros, so tiles always start on an even step and the two register slots
-// alternate statically.
-template <bool SWIGLU, bool ODD>
+// alternate statically.  GATHER: A is the token matrix x and row r of the
+// dispatched operand is x[gather_src[r] / gather_k] (gather_src = perm_src,
+// -1 past the kept rows), so the row permutation is done by the GEMM's own
+// loads and the dispatched copy of x is never written.
+template <bool SWIGLU, bool ODD, bool GATHER>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
-    uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n) {
+    uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n,
+    const int32_t* __restrict__ gather_src, int gather_k, int gather_rows) {
   typedef GemmElem<false> E;
   constexpr int kParts = 4 / E::kSub;  // load parts per MFMA sub-step
   // The two stages live in dynamic LDS: stage g & 1 holds global K step g.
@@ -536,6 +540,22 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   const uint8_t* a_tile = A;
   const uint8_t* b_tile = B;
   int ld_t = first, ld_kb = 0, ld_g = 0;  // load side: tile, K step in it, global step
+  // GATHER: perm_src of the 8 rows this thread loads in the next tile the load
+  // side enters.
+  int32_t pf_src[8];
+  auto fetch_src = [&](int t) __attribute__((always_inline)) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
+    const int64_t lim = a_rows - 1 - r0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int rr = i * 32 + ld_r;
+      rr = rr < lim ? rr : static_cast<int>(lim);
+      pf_src[i] = gather_src[r0 + rr];
+    }
+  };
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
@@ -543,16 +563,32 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
-    a_tile = A + static_cast<int64_t>(r0) * row_bytes;
     b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes;
     // Rows past the buffer (the last tile of the last segment) are clamped to
     // its last row; their results are never stored.
     const int64_t lim = a_rows - 1 - r0;
+    if (GATHER) {
+      // Row offsets into x from the sources prefetched one tile earlier; rows
+      // without a source (-1) read token 0, and a source past the token count
+      // is clamped (x is never read out of range).  Then prefetch the sources
+      // of this workgroup's next tile, so that their load latency is hidden.
+      a_tile = A;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int rr = i * 32 + ld_r;
-      rr = rr < lim ? rr : static_cast<int>(lim);
-      a_off[i] = static_cast<uint32_t>(rr * row_bytes + ld_c * 16);
+      for (int i = 0; i < 8; ++i) {
+        int tk = pf_src[i] >= 0 ? pf_src[i] / gather_k : 0;
+        tk = tk < gather_rows ? tk : gather_rows - 1;
+        a_off[i] = static_cast<uint32_t>(tk) * static_cast<uint32_t>(row_bytes) +
+                   static_cast<uint32_t>(ld_c * 16);
+      }
+      if (t + per_xcd < hi) fetch_src(t + per_xcd);
+    } else {
+      a_tile = A + static_cast<int64_t>(r0) * row_bytes;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int rr = i * 32 + ld_r;
+        rr = rr < lim ? rr : static_cast<int>(lim);
+        a_off[i] = static_cast<uint32_t>(rr * row_bytes + ld_c * 16);
+      }
     }
   };
   // Part p (0..3): rounds 2p and 2p+1 of A and of B of load step ld_g.
@@ -658,6 +694,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     barrier_lds();
   };
 
+  if (GATHER) fetch_src(first);
   set_load_tile(first);
 #pragma unroll
   for (int p = 0; p < 4; ++p) issue_part(ra0, rb0, p);
@@ -736,10 +773,12 @@ int allow_dynamic_lds(int dev) {
   if (dev >= 0 && dev < 64 && done[dev].load(std::memory_order_acquire)) return HMOE_OK;
   const int bytes = 2 * kStageBytes;
   const void* kernels[] = {
-      reinterpret_cast<const void*>(grouped_gemm_regs<true, false>),
-      reinterpret_cast<const void*>(grouped_gemm_regs<true, true>),
-      reinterpret_cast<const void*>(grouped_gemm_regs<false, false>),
-      reinterpret_cast<const void*>(grouped_gemm_regs<false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<true, false, false>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<true, true, false>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, false, false>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, true, false>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<true, false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<true, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<false, true>),
   };
@@ -755,7 +794,8 @@ int allow_dynamic_lds(int dev) {
 
 int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const float* a_scale,
                    const float* b_scale, const int32_t* offsets, int n_experts, int64_t rows_cap,
-                   int kdim, int ncols, void* C, int64_t ldc, hipStream_t s, const char* what) {
+                   int kdim, int ncols, void* C, int64_t ldc, hipStream_t s, const char* what,
+                   const int32_t* gather_src = nullptr, int gather_k = 1, int gather_rows = 1) {
   const int n_tiles_n = ncols / kBN;
   const int64_t max_tiles = (ceil_div(rows_cap, kBM) + n_experts) * n_tiles_n;
   HMOE_REQUIRE(max_tiles < (int64_t(1) << 31), "%s: too many tiles", what);
@@ -780,13 +820,17 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
       hipLaunchKernelGGL((grouped_gemm_dma<false, true>), dim3(grid), dim3(kThreads), lds, s, a, b,
                          a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n);
   } else {
-#define HMOE_LAUNCH_REGS(SW, OD)                                                                  \
-  hipLaunchKernelGGL((grouped_gemm_regs<SW, OD>), dim3(grid), dim3(kThreads), lds, s, a, b,      \
-                     offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n)
-    if (swiglu && odd) HMOE_LAUNCH_REGS(true, true);
-    else if (swiglu) HMOE_LAUNCH_REGS(true, false);
-    else if (odd) HMOE_LAUNCH_REGS(false, true);
-    else HMOE_LAUNCH_REGS(false, false);
+#define HMOE_LAUNCH_REGS(SW, OD, GA)                                                              \
+  hipLaunchKernelGGL((grouped_gemm_regs<SW, OD, GA>), dim3(grid), dim3(kThreads), lds, s, a, b,  \
+                     offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n, gather_src,     \
+                     gather_k, gather_rows)
+    if (gather_src != nullptr) {
+      if (odd) HMOE_LAUNCH_REGS(true, true, true);
+      else HMOE_LAUNCH_REGS(true, false, true);
+    } else if (swiglu && odd) HMOE_LAUNCH_REGS(true, true, false);
+    else if (swiglu) HMOE_LAUNCH_REGS(true, false, false);
+    else if (odd) HMOE_LAUNCH_REGS(false, true, false);
+    else HMOE_LAUNCH_REGS(false, false, false);
 #undef HMOE_LAUNCH_REGS
   }
   return check_launch(what);
@@ -811,6 +855,33 @@ extern "C" int hmoe_grouped_gate_up(const void* xs, const int32_t* offsets, int 
   return launch_grouped(true, false, xs, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
                         rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
                         "hmoe_grouped_gate_up");
+}
+
+extern "C" int hmoe_grouped_gate_up_gather(const void* x, int64_t tokens, int top_k,
+                                           const int32_t* perm_src, const int32_t* offsets,
+                                           int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                           const void* w_gate_up_packed, void* h,
+                                           hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
+               n_experts);
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
+               "grouped_gate_up_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_gather: d_model must be a multiple of %d (got %d)", kBK,
+                    d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_gather: d_ff must be a multiple of %d (got %d)", kBN / 2,
+                    d_ff);
+  HMOE_REQUIRE(tokens * d_model * 2 < (int64_t(1) << 31),
+               "grouped_gate_up_gather: x must be smaller than 2 GiB");
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && perm_src && offsets && w_gate_up_packed && h,
+               "grouped_gate_up_gather: null pointer argument");
+  return launch_grouped(true, false, x, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_gather", perm_src, top_k, static_cast<int>(tokens));
 }
 
 extern "C" int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,

@@ -252,6 +252,24 @@ def grouped_gate_up(xs: torch.Tensor, offsets: torch.Tensor, w_gate_up: torch.Te
     return h
 
 
+def grouped_gate_up_gather(x: torch.Tensor, plan: Plan, w_gate_up: torch.Tensor) -> torch.Tensor:
+    """``h`` of :func:`grouped_gate_up` on the dispatched rows of ``x`` without
+    materialising them: the GEMM loads row ``r`` from ``x[perm_src[r] // K]``
+    (``moe.py:56`` fused into ``moe.py:70-72``)."""
+    _check(x, "x", 2)
+    _check(w_gate_up, "w_gate_up", 3)
+    if x.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16:
+        raise TypeError("grouped_gate_up_gather takes bf16 operands")
+    T, D = x.shape
+    N, F2, D2 = w_gate_up.shape
+    if D2 != D or plan.n_experts != N or plan.slot_pos.numel() != T * plan.top_k:
+        raise ValueError("grouped_gate_up_gather: inconsistent shapes")
+    h = torch.empty((plan.rows_cap, F2 // 2), dtype=torch.bfloat16, device=x.device)
+    call("hmoe_grouped_gate_up_gather", _ptr(x), T, plan.top_k, _ptr(plan.perm_src),
+         _ptr(plan.offsets), N, plan.rows_cap, D, F2 // 2, _ptr(w_gate_up), _ptr(h), _stream())
+    return h
+
+
 def grouped_down(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor,
                  rows: int | None = None) -> torch.Tensor:
     """``ys = bf16(h Wd)`` per expert segment (``moe.py:73-74``)."""

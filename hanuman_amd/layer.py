@@ -3,7 +3,8 @@
 ``DeviceLayer`` uploads one workload's inputs, packs its expert weights once
 and runs the layer (router -> plan -> permute -> grouped SwiGLU -> combine)
 entirely through ``libhanuman_moe.so``; ``forward`` is the step ``bench.py``
-times and the GPU tests check.
+times and the GPU tests check.  With bf16 tokens and SwiGLU experts the
+permutation is fused into the gate/up GEMM (``xs`` is then ``None``).
 """
 from __future__ import annotations
 
@@ -52,6 +53,10 @@ class DeviceLayer:
             else:
                 self.w_down = K.pack_down(wd)
             del wd
+        # bf16 SwiGLU experts on bf16 tokens: the gate/up GEMM gathers its rows
+        # from x itself (hmoe_grouped_gate_up_gather), no dispatched copy.
+        self.fused_dispatch = (wl.expert == "swiglu" and not self.fp8
+                               and self.x.dtype == torch.bfloat16)
         ws = int(_lib.lib().hmoe_plan_workspace_bytes(wl.tokens, wl.top_k, wl.n_experts))
         self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
         self.out_dtype = _TORCH_DT[wl.out_dtype]
@@ -81,6 +86,10 @@ class DeviceLayer:
         if self.fp8:
             xs, xs_s, h, h_q, h_s, ys = self.experts_fp8(plan)
             extra = {"xs_scale": xs_s, "h_q": h_q, "h_scale": h_s}
+        elif self.fused_dispatch:
+            xs = None
+            h = K.grouped_gate_up_gather(self.x, plan, self.w_gate_up)
+            ys = K.grouped_down(h, plan.offsets, self.w_down)
         else:
             xs = K.permute_rows(self.x, plan, torch.bfloat16)
             if wl.expert == "identity":

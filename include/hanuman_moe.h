@@ -163,13 +163,27 @@ int hmoe_pack_fp8_down(const void* w_down, int w_dtype, int n_experts, int d_ff,
 /* h[r, :] = bf16( silu(xs[r]·Wg[e]) * (xs[r]·Wu[e]) ) for rows r of expert e's
  * segment [offsets[e], offsets[e+1]).  xs [rows_cap, D] bf16, packed gate/up
  * from hmoe_pack_gate_up, h [rows_cap, F] bf16.  fp32 accumulation.
- * D % 256 == 0, F % 128 == 0, N <= 1024. */
+ * D % 64 == 0, F % 128 == 0, N <= 1024. */
 int hmoe_grouped_gate_up(const void* xs, const int32_t* offsets, int n_experts,
                          int64_t rows_cap, int d_model, int d_ff,
                          const void* w_gate_up_packed, void* h, hmoe_stream_t stream);
 
+/* The same h with the row permutation (moe.py:56, `x_flat[order // K]`) done
+ * by the GEMM's own loads: row r of the dispatched operand is
+ * x[perm_src[r] / top_k], so the dispatched copy of x is never written (a
+ * fusion of hmoe_permute_rows and hmoe_grouped_gate_up; bit-identical h).
+ * x [tokens, D] bf16, perm_src [rows_cap] from hmoe_dispatch_plan (rows with
+ * -1 are computed from token 0 and not meaningful, as past the kept rows
+ * above).  tokens * D * 2 < 2^31. */
+int hmoe_grouped_gate_up_gather(const void* x, int64_t tokens, int top_k,
+                                const int32_t* perm_src, const int32_t* offsets,
+                                int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                const void* w_gate_up_packed, void* h,
+                                hmoe_stream_t stream);
+
 /* ys[r, :] = bf16( h[r]·Wd[e] ) per expert segment.  h [rows_cap, F] bf16,
- * packed down from hmoe_pack_down, ys [rows_cap, D] bf16. */
+ * packed down from hmoe_pack_down, ys [rows_cap, D] bf16.  F % 64 == 0,
+ * D % 256 == 0. */
 int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
                       int64_t rows_cap, int d_ff, int d_model,
                       const void* w_down_packed, void* ys, hmoe_stream_t stream);

@@ -326,6 +326,33 @@ def test_grouped_gemm_odd_k_steps(gpu, case):
             assert np.all(err <= 8e-3 * np.abs(ref) + 1e-3 * np.abs(ref).max()), f"ys expert {e}: {err.max()}"
 
 
+GATHER_CASES = [
+    # T, D, N, K, F, capacity (rows per expert; small values drop slots)
+    (700, 256, 8, 2, 128, 10**6),
+    (1000, 192, 6, 4, 256, 300),
+    (333, 512, 16, 8, 128, 90),
+]
+
+
+@pytest.mark.parametrize("case", GATHER_CASES, ids=lambda c: f"T{c[0]}_D{c[1]}_N{c[2]}_K{c[3]}_cap{c[5]}")
+def test_grouped_gate_up_gather_matches_unfused(gpu, case):
+    """The gate/up GEMM that gathers its rows from x through perm_src gives the
+    same h, bit for bit, as the permutation followed by the plain GEMM."""
+    T, D, N, Kk, F, cap = case
+    print(f"gather case {case}", flush=True)
+    rng = np.random.default_rng(7 + T)
+    x = dev_bf16(O.bf16_round(rng.standard_normal((T, D)).astype(np.float32)), gpu)
+    top = np.stack([rng.choice(N, Kk, replace=False) for _ in range(T)]).astype(np.int32)
+    plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, cap)
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    w = K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    h_fused = K.grouped_gate_up_gather(x, plan, w)
+    h_ref = K.grouped_gate_up(K.permute_rows(x, plan, torch.bfloat16), plan.offsets, w)
+    total = int(plan.offsets[-1].item())
+    assert total > 0
+    assert torch.equal(h_fused[:total], h_ref[:total])
+
+
 # --------------------------------------------------------------------- aux --
 
 def test_router_aux(gpu):

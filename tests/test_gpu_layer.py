@@ -106,11 +106,18 @@ def test_workload_full_size(gpu, name):
     err = O.normwise_rel_err(got, ref)
     print(f"{name}: sampled-token normwise rel err {err:.3e}", flush=True)
     assert err < BF16_TOL
-    # size-independent properties: every kept row of xs is its token's row
-    xs = res["xs"]
+    # size-independent property: the fused gate/up (rows gathered from x by
+    # the GEMM) equals the unfused permute + gate/up on the kept rows, bit for bit
+    import hanuman_amd.kernels as K
+    p = res["plan"]
+    total = int(plan["offsets"][-1])
+    xs = K.permute_rows(layer.x, p, torch.bfloat16)
     j = torch.from_numpy(np.nonzero(plan["perm_src"] >= 0)[0][::997]).to(gpu)
     src_tok = torch.from_numpy(plan["perm_src"]).to(gpu)[j] // wl.top_k
     assert torch.equal(xs[j], layer.x[src_tok].to(torch.bfloat16))
+    h_unfused = K.grouped_gate_up(xs, p.offsets, layer.w_gate_up)
+    assert res["h"] is not None and torch.equal(res["h"][:total], h_unfused[:total]), "fused gate/up"
+
 
 
 def test_dispatch_identity_full_size(gpu):
