@@ -118,8 +118,12 @@ def ragged_dispatch(x_flat: torch.Tensor, top_idx: torch.Tensor, weights: torch.
     T, Kk = top_idx.shape
     N = w_gate.shape[0]
     plan = K.dispatch_plan(top_idx.to(torch.int32).contiguous(), N, T * Kk)
-    xs = K.permute_rows(x_flat.contiguous(), plan, dt)
-    h = K.grouped_gate_up(xs, plan.offsets, K.pack_gate_up(w_gate, w_up))
+    wgu = K.pack_gate_up(w_gate, w_up)
+    if x_flat.dtype == torch.bfloat16:
+        # the gate/up GEMM gathers its rows from x (moe.py:56 fused)
+        h = K.grouped_gate_up_gather(x_flat.contiguous(), plan, wgu)
+    else:
+        h = K.grouped_gate_up(K.permute_rows(x_flat.contiguous(), plan, dt), plan.offsets, wgu)
     ys = K.grouped_down(h, plan.offsets, K.pack_down(w_down))
     return K.combine(ys, plan, weights.float().contiguous(), None, torch.float32)
 
@@ -234,9 +238,12 @@ class MoE:
                                           bias, Kk, mode, rsf)
         cap = K.capacity(T, Kk, N, self.capacity_factor)
         plan = K.dispatch_plan(top_idx, N, cap)
-        xs = K.permute_rows(x2, plan, self.dtype)
         wgu, wd = self._packed_routed()
-        h = K.grouped_gate_up(xs, plan.offsets, wgu)
+        if x2.dtype == torch.bfloat16:
+            # the gate/up GEMM gathers its rows from x (moe.py:56 fused)
+            h = K.grouped_gate_up_gather(x2, plan, wgu)
+        else:
+            h = K.grouped_gate_up(K.permute_rows(x2, plan, self.dtype), plan.offsets, wgu)
         ys = K.grouped_down(h, plan.offsets, wd)
         xc = x2 if x2.dtype == self.dtype else x2.to(self.dtype)
         shared = self._shared_ffn(xc)
