@@ -1,14 +1,16 @@
-// Ragged grouped GEMM on gfx950 bf16 MFMA (model/moe.py:67-74: the three
+// Ragged grouped GEMM on gfx950 MFMA (model/moe.py:67-74: the three
 // `jax.lax.ragged_dot` calls and the SwiGLU between them).
 //
 //   C[r, n] = sum_k A[r, k] * B_e[n, k]     for rows r of expert e's segment
 //
 // A is the dispatched activation buffer (rows grouped by expert, K contiguous)
-// and B_e the packed expert weight (one row per output column, K contiguous).
-// With SWIGLU the packed columns alternate 32 gate / 32 up columns of the same
-// h columns and the epilogue writes h = bf16(silu(gate) * up).
+// or, for the gathered gate/up GEMM, the token matrix x read through the
+// dispatch plan's perm_src (row r = x[perm_src[r] / K]); B_e is the packed
+// expert weight (one row per output column, K contiguous).  With SWIGLU the
+// packed columns alternate 32 gate / 32 up columns of the same h columns and
+// the epilogue writes h = bf16(silu(gate) * up).
 //
-// Persistent kernel: one workgroup (4 waves) per CU loops over 256 x 256
+// Persistent kernels: one workgroup (4 waves) per CU loops over 256 x 256
 // output tiles.  Tiles are numbered expert by expert (ceil(rows_e / 256)
 // m-tiles each, n fastest); every workgroup computes the numbering from
 // `offsets`, so the launch never depends on the routing.  The tile range is
@@ -20,15 +22,19 @@
 // Main loop (per K step of 128 bytes per row: 64 bf16 or 128 e4m3): each
 // wave owns a 128 x 128 quarter of the tile and runs 4 x 16 bf16 MFMAs
 // (v_mfma_f32_32x32x16_bf16) or 2 x 16 fp8 MFMAs per step from the current
-// LDS stage.  Global loads run two K steps ahead into two register slots
-// (2 x 64 KB per workgroup in flight) and each slot is written into the other
-// LDS stage during the step before it is used; the loads, LDS writes and
-// fragment reads of each sub-step are interleaved between its MFMAs, and a
-// step ends with one barrier that never waits for global memory.  An LDS row
-// holds 128 bytes as eight 16-byte chunks; chunk c of row r is stored at
-// position c ^ (r & 7), so the eight lanes that read one MFMA fragment
-// row-group hit eight different bank groups.  The load side runs on into the
-// next tile, so the pipeline does not drain between tiles.
+// LDS stage; two stages alternate.  An LDS row holds 128 bytes as eight
+// 16-byte chunks; chunk c of row r is stored at position c ^ (r & 7).
+//   * bf16 (grouped_gemm_regs): global loads run two K steps ahead into two
+//     register slots (2 x 64 KB per workgroup in flight) and each slot is
+//     written into the other stage during the step before it is used; the
+//     loads, LDS writes and fragment reads of each sub-step are interleaved
+//     between its MFMAs, and a step ends with one barrier that never waits
+//     for global memory.
+//   * fp8 (grouped_gemm_dma): the next step's tiles go straight from global
+//     memory into the other stage (global_load_lds_dwordx4), because the
+//     32-byte fp8 fragments leave no registers for load staging.
+// The load side runs on into the next tile, so the pipeline does not drain
+// between tiles.
 #include <atomic>
 
 #include "hmoe_common.h"
