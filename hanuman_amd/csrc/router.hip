@@ -134,6 +134,11 @@ __device__ __forceinline__ float load_w_f32<uint16_t>(const uint16_t* p, int64_t
 // (the next chunk's global loads are issued before the current chunk's
 // MFMAs).  The float32-rounded logits go through LDS to the wave-per-token
 // selection.
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
 constexpr int kRTokWave = 16;
 // d per LDS chunk (one barrier per chunk): 64 while the staging of up to 64
 // experts fits two workgroups per CU, 32 beyond.
@@ -197,13 +202,15 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     const int64_t tok = t0 + (x_thread[r] ? xs_tt[r] : 0);
     xs_row[r] = (tok < tokens ? tok : tokens - 1) * static_cast<int64_t>(d_model);
   }
-  X8<XT> xr[kXR];
-  float wr[kWPer];
-  auto w_ok = [&](int q, int d0) {
+  // Two register sets: the loads of chunk c + 2 are issued at the start of
+  // chunk c, so a load has two chunks of MFMAs to arrive before it is parked.
+  X8<XT> xr0[kXR], xr1[kXR];
+  float wr0[kWPer], wr1[kWPer];
+  auto w_ok = [&](int q, int d0) __attribute__((always_inline)) {
     const int idx = q * 256 + tid;
     return idx < kRDc * kNP && idx % kNP < n_experts && d0 + idx / kNP < d_model;
   };
-  auto fetch = [&](int d0) {
+  auto fetch = [&](X8<XT>* xr, float* wr, int d0) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < kXR; ++r) {
       const int dx = d0 + xs_dd[r];
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     // Keep the loads ahead of the MFMAs; the masking happens in park().
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto park = [&](int buf, int d0) {
+  auto park = [&](const X8<XT>* xr, const float* wr, int buf, int d0) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < kXR; ++r) {
       if (x_thread[r]) {
@@ -244,23 +251,35 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   const int k_of_lane = lane >> 4;
   const int col0 = ep * kNTW * 16 + (lane & 15);
   const int nchunks = (d_model + kRDc - 1) / kRDc;
-  fetch(0);
-  park(0, 0);
-  __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nchunks) fetch((c + 1) * kRDc);
+  // Chunk c (S = c % 2): prefetch chunk c + 2 into register set S, run the
+  // MFMAs on LDS buffer S, park chunk c + 1 (register set S ^ 1) into buffer
+  // S ^ 1.
+  auto chunk = [&](auto Sc, int c) __attribute__((always_inline)) {
+    constexpr int S = decltype(Sc)::value;
+    X8<XT>* xs_ld = S == 0 ? xr0 : xr1;
+    float* ws_ld = S == 0 ? wr0 : wr1;
+    const X8<XT>* xs_pk = S == 0 ? xr1 : xr0;
+    const float* ws_pk = S == 0 ? wr1 : wr0;
+    if (c + 2 < nchunks) fetch(xs_ld, ws_ld, (c + 2) * kRDc);
 #pragma unroll
     for (int s = 0; s < kRDc / 4; ++s) {
-      const double a = static_cast<double>(lds.x[buf][a_row][4 * s + k_of_lane]);
+      const double a = static_cast<double>(lds.x[S][a_row][4 * s + k_of_lane]);
 #pragma unroll
       for (int t = 0; t < kNTW; ++t) {
-        const double b = static_cast<double>(lds.w[buf][4 * s + k_of_lane][col0 + t * 16]);
+        const double b = static_cast<double>(lds.w[S][4 * s + k_of_lane][col0 + t * 16]);
         acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
       }
     }
-    if (c + 1 < nchunks) park(buf ^ 1, (c + 1) * kRDc);
+    if (c + 1 < nchunks) park(xs_pk, ws_pk, S ^ 1, (c + 1) * kRDc);
     __syncthreads();
+  };
+  fetch(xr0, wr0, 0);
+  if (nchunks > 1) fetch(xr1, wr1, kRDc);
+  park(xr0, wr0, 0, 0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; c += 2) {
+    chunk(IntC<0>{}, c);
+    if (c + 1 < nchunks) chunk(IntC<1>{}, c + 1);
   }
 
   // float32 logits into LDS, row = token of the workgroup, col = expert.
