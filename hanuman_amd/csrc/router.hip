@@ -149,16 +149,20 @@ constexpr int router_dc(int nt) { return nt <= 4 ? 64 : 32; }
 // workgroups fit the token count, two waves run on every SIMD and each keeps
 // NT/2 independent accumulator chains.
 template <int NT, int ES>
-struct RouterLds {
+struct alignas(16) RouterLds {
   static constexpr int kNP = 16 * NT;
   static constexpr int kWPitch = kNP + 8;
   static constexpr int kTB = 64 / ES;
   static constexpr int kDc = router_dc(NT);
-  float x[2][kTB][kDc + 1];
+  static constexpr int kXPitch = kDc + 4;  // 16-byte aligned rows
+  float x[2][kTB][kXPitch];
   float w[2][kDc][kWPitch];
 };
 
-template <int NT, int ES, typename XT, typename WT>
+// WV: n_experts is a multiple of the W elements in 16 bytes, so a chunk of W
+// (kRDc consecutive rows of n_experts values, contiguous in memory) is staged
+// with 16-byte loads and LDS writes.
+template <int NT, int ES, typename XT, typename WT, bool WV>
 __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, const WT* __restrict__ w,
                                                      const float* __restrict__ bias, int64_t tokens,
                                                      int d_model, int n_experts, int top_k, int mode,
@@ -173,6 +177,8 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   constexpr int kNTW = NT / ES;                       // expert tiles per wave
   constexpr int kEPL = (kNP + 63) / 64;
   constexpr int kWPer = (kRDc * kNP + 255) / 256;     // w elements per thread per chunk
+  constexpr int kE16 = 16 / static_cast<int>(sizeof(WT));  // W elements per 16-byte load
+  constexpr int kWV = (kRDc * kNP / kE16 + 255) / 256;     // 16-byte W loads per thread per chunk
   __shared__ RouterLds<NT, ES> lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -205,41 +211,103 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   // Two register sets: the loads of chunk c + 2 are issued at the start of
   // chunk c, so a load has two chunks of MFMAs to arrive before it is parked.
   X8<XT> xr0[kXR], xr1[kXR];
-  float wr0[kWPer], wr1[kWPer];
+  // W staging registers: kWPer scalars, or kWV 16-byte vectors (WV).
+  constexpr int kWRegs = WV ? 4 * kWV : kWPer;
+  uint32_t wr0[kWRegs], wr1[kWRegs];
   auto w_ok = [&](int q, int d0) __attribute__((always_inline)) {
     const int idx = q * 256 + tid;
     return idx < kRDc * kNP && idx % kNP < n_experts && d0 + idx / kNP < d_model;
   };
-  auto fetch = [&](X8<XT>* xr, float* wr, int d0) __attribute__((always_inline)) {
+  // WV: vector q covers elements idx .. idx + kE16 - 1 (idx = (q*256 + tid) *
+  // kE16) of the chunk, i.e. row idx / n_experts, experts idx % n_experts ...
+  auto wv_idx = [&](int q) __attribute__((always_inline)) { return (q * 256 + tid) * kE16; };
+  auto fetch = [&](X8<XT>* xr, uint32_t* wr, int d0) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < kXR; ++r) {
       const int dx = d0 + xs_dd[r];
       xr[r].load(x + xs_row[r] + (dx < d_model ? dx : 0));
     }
+    if (WV) {
 #pragma unroll
-    for (int q = 0; q < kWPer; ++q) {
-      const int idx = q * 256 + tid;
-      const int64_t off = static_cast<int64_t>(d0 + idx / kNP) * n_experts + idx % kNP;
-      wr[q] = load_w_f32(w, w_ok(q, d0) ? off : 0);
+      for (int q = 0; q < kWV; ++q) {
+        const int idx = wv_idx(q);
+        const bool ok = idx < kRDc * n_experts && d0 + idx / n_experts < d_model;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(
+            w + (ok ? static_cast<int64_t>(d0) * n_experts + idx : 0));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wr[4 * q + j] = v[j];
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) {
+        const int idx = q * 256 + tid;
+        const int64_t off = static_cast<int64_t>(d0 + idx / kNP) * n_experts + idx % kNP;
+        wr[q] = __float_as_uint(load_w_f32(w, w_ok(q, d0) ? off : 0));
+      }
     }
     // Keep the loads ahead of the MFMAs; the masking happens in park().
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto park = [&](const X8<XT>* xr, const float* wr, int buf, int d0) __attribute__((always_inline)) {
+  auto park = [&](const X8<XT>* xr, const uint32_t* wr, int buf, int d0) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < kXR; ++r) {
       if (x_thread[r]) {
         const bool x_ok = d0 + xs_dd[r] < d_model;
+        f32x4 lo, hi;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) lds.x[buf][xs_tt[r]][xs_dd[r] + q] = x_ok ? xr[r].get(q) : 0.0f;
+        for (int q = 0; q < 4; ++q) {
+          lo[q] = x_ok ? xr[r].get(q) : 0.0f;
+          hi[q] = x_ok ? xr[r].get(4 + q) : 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(&lds.x[buf][xs_tt[r]][xs_dd[r]]) = lo;
+        *reinterpret_cast<f32x4*>(&lds.x[buf][xs_tt[r]][xs_dd[r] + 4]) = hi;
       }
     }
+    if (WV) {
 #pragma unroll
-    for (int q = 0; q < kWPer; ++q) {
-      const int idx = q * 256 + tid;
-      if (idx < kRDc * kNP) lds.w[buf][idx / kNP][idx % kNP] = w_ok(q, d0) ? wr[q] : 0.0f;
+      for (int q = 0; q < kWV; ++q) {
+        const int idx = wv_idx(q);
+        if (idx < kRDc * n_experts) {
+          const int d = idx / n_experts;
+          const int n = idx - d * n_experts;
+          const bool ok = d0 + d < d_model;
+          float* dst = &lds.w[buf][d][n];
+          if (sizeof(WT) == 4) {
+            f32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = ok ? __uint_as_float(wr[4 * q + j]) : 0.0f;
+            *reinterpret_cast<f32x4*>(dst) = v;
+          } else {
+            f32x4 lo, hi;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const uint32_t a = wr[4 * q + j], b = wr[4 * q + 2 + j];
+              lo[2 * j] = ok ? __uint_as_float(a << 16) : 0.0f;
+              lo[2 * j + 1] = ok ? __uint_as_float(a & 0xffff0000u) : 0.0f;
+              hi[2 * j] = ok ? __uint_as_float(b << 16) : 0.0f;
+              hi[2 * j + 1] = ok ? __uint_as_float(b & 0xffff0000u) : 0.0f;
+            }
+            *reinterpret_cast<f32x4*>(dst) = lo;
+            *reinterpret_cast<f32x4*>(dst + 4) = hi;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) {
+        const int idx = q * 256 + tid;
+        if (idx < kRDc * kNP) lds.w[buf][idx / kNP][idx % kNP] = w_ok(q, d0) ? __uint_as_float(wr[q]) : 0.0f;
+      }
     }
   };
+  if (WV && n_experts < kNP) {
+    // Expert columns past n_experts are never written by the vector staging:
+    // zero them once in both buffers.
+    for (int i = tid; i < 2 * kRDc * kNP; i += 256) {
+      const int n = i % kNP;
+      if (n >= n_experts) lds.w[i / (kRDc * kNP)][(i / kNP) % kRDc][n] = 0.0f;
+    }
+  }
 
   f64x4 acc[kNTW];
 #pragma unroll
@@ -257,9 +325,9 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   auto chunk = [&](auto Sc, int c) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value;
     X8<XT>* xs_ld = S == 0 ? xr0 : xr1;
-    float* ws_ld = S == 0 ? wr0 : wr1;
+    uint32_t* ws_ld = S == 0 ? wr0 : wr1;
     const X8<XT>* xs_pk = S == 0 ? xr1 : xr0;
-    const float* ws_pk = S == 0 ? wr1 : wr0;
+    const uint32_t* ws_pk = S == 0 ? wr1 : wr0;
     if (c + 2 < nchunks) fetch(xs_ld, ws_ld, (c + 2) * kRDc);
 #pragma unroll
     for (int s = 0; s < kRDc / 4; ++s) {
@@ -338,9 +406,15 @@ void launch_router(const void* x, const void* w, const float* bias, int64_t toke
                    float* gates, hipStream_t stream) {
   constexpr int ES = NT >= 2 ? 2 : 1;
   const dim3 grid(static_cast<unsigned>(ceil_div(tokens, RouterLds<NT, ES>::kTB)));
-  hipLaunchKernelGGL((router_kernel<NT, ES, XT, WT>), grid, dim3(256), 0, stream,
-                     static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
-                     n_experts, top_k, mode, rsf, logits, top_idx, gates);
+  if (n_experts % (16 / static_cast<int>(sizeof(WT))) == 0 &&
+      reinterpret_cast<uintptr_t>(w) % 16 == 0)
+    hipLaunchKernelGGL((router_kernel<NT, ES, XT, WT, true>), grid, dim3(256), 0, stream,
+                       static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
+                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
+  else
+    hipLaunchKernelGGL((router_kernel<NT, ES, XT, WT, false>), grid, dim3(256), 0, stream,
+                       static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
+                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
 }
 
 template <int NT>
