@@ -17,8 +17,8 @@ namespace hmoe {
 namespace {
 
 constexpr int kPlanThreads = 256;
-constexpr int kSlotsPerWave = 1024;
-constexpr int kSlotsPerBlock = 4 * kSlotsPerWave;
+constexpr int kSlotsPerWave = 256;
+constexpr int kSlotsPerBlock = 4 * kSlotsPerWave;  // 128 blocks at 16384 tokens x top-8
 constexpr int kMaxExperts = 1024;
 
 int64_t plan_blocks(int64_t rows) { return ceil_div(rows, kSlotsPerBlock); }
@@ -42,34 +42,57 @@ __global__ __launch_bounds__(kPlanThreads) void plan_histogram_kernel(
 }
 
 // One workgroup of 1024 threads.  hist is rewritten in place into the
-// per-block exclusive bases.
+// per-block exclusive bases.  Each expert is served by a group of P lanes
+// (P = 1024 / N rounded down to a power of two, at most 64, so a group lies
+// inside one wave): lane j of the group sums blocks [j*L, (j+1)*L), the group
+// scans those partial sums with shuffles, and each lane then writes its
+// blocks' bases.  Totals and kept-row offsets follow as before.
 __global__ __launch_bounds__(1024) void plan_scan_kernel(int32_t* __restrict__ hist, int nblk,
                                                           int n_experts, int64_t capacity,
                                                           int32_t* __restrict__ counts,
                                                           int32_t* __restrict__ offsets) {
   __shared__ int32_t kept[kMaxExperts];
-  const int e = threadIdx.x;
-  int32_t total = 0;
+  const int tid = threadIdx.x;
+  int P = 1;
+  while (P < 64 && 2 * P * n_experts <= 1024) P *= 2;
+  const int e = tid / P;          // expert of this lane (>= n_experts: idle)
+  const int j = tid % P;          // position in the expert's group
+  const int L = (nblk + P - 1) / P;
+  const int b0 = j * L;
+  const int b1 = b0 + L < nblk ? b0 + L : nblk;
+  int32_t part = 0;
+  if (e < n_experts)
+    for (int b = b0; b < b1; ++b) part += hist[static_cast<int64_t>(b) * n_experts + e];
+  // Inclusive scan of the partial sums within the group (P lanes, aligned).
+  int32_t incl = part;
+  for (int off = 1; off < P; off <<= 1) {
+    const int32_t v = __shfl_up(incl, off, P);
+    if (j >= off) incl += v;
+  }
+  const int32_t total = __shfl(incl, P - 1, P);
   if (e < n_experts) {
-    for (int b = 0; b < nblk; ++b) {
+    int32_t run = incl - part;  // exclusive base of block b0
+    for (int b = b0; b < b1; ++b) {
       const int64_t idx = static_cast<int64_t>(b) * n_experts + e;
       const int32_t c = hist[idx];
-      hist[idx] = total;
-      total += c;
+      hist[idx] = run;
+      run += c;
     }
-    counts[e] = total;
+    if (j == 0) counts[e] = total;
   }
-  kept[e] = (e < n_experts) ? static_cast<int32_t>(total < capacity ? total : capacity) : 0;
+  if (tid < kMaxExperts) kept[tid] = 0;
+  __syncthreads();
+  if (e < n_experts && j == 0) kept[e] = static_cast<int32_t>(total < capacity ? total : capacity);
   __syncthreads();
   // Inclusive Hillis-Steele scan over 1024 entries.
   for (int off = 1; off < 1024; off <<= 1) {
-    const int32_t v = e >= off ? kept[e - off] : 0;
+    const int32_t v = tid >= off ? kept[tid - off] : 0;
     __syncthreads();
-    kept[e] += v;
+    kept[tid] += v;
     __syncthreads();
   }
-  if (e < n_experts) offsets[e + 1] = kept[e];
-  if (e == 0) offsets[0] = 0;
+  if (tid < n_experts) offsets[tid + 1] = kept[tid];
+  if (tid == 0) offsets[0] = 0;
 }
 
 __global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(

@@ -38,7 +38,9 @@ def test_capacity_and_rows_cap_match_oracle(lib, T, K, N, cf):
 
 
 def test_workspace_sizes(lib):
-    assert lib.hmoe_plan_workspace_bytes(16384, 8, 64) == 32 * 64 * 4
+    # one int32 per (block of 1024 slots, expert)
+    assert lib.hmoe_plan_workspace_bytes(16384, 8, 64) == 128 * 64 * 4
+    assert lib.hmoe_plan_workspace_bytes(1000, 3, 7) == 3 * 7 * 4
     assert lib.hmoe_plan_workspace_bytes(0, 8, 64) == 0
     assert lib.hmoe_packed_gate_up_bytes(64, 2048, 1024) == 64 * 2048 * 2048 * 2
     assert lib.hmoe_packed_down_bytes(64, 1024, 2048) == 64 * 1024 * 2048 * 2
