@@ -11,13 +11,18 @@ namespace {
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+// Wave-wide maxima of NTOK independent values (their shuffle chains
+// interleave).
+template <int NTOK>
+__device__ __forceinline__ void wave_max_u64(uint64_t (&v)[NTOK]) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    uint64_t o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
+#pragma unroll
+    for (int q = 0; q < NTOK; ++q) {
+      const uint64_t o = __shfl_xor(v[q], off, 64);
+      v[q] = o > v[q] ? o : v[q];
+    }
   }
-  return v;
 }
 
 __device__ __forceinline__ uint64_t pack_key(float key, int e) {
@@ -25,65 +30,82 @@ __device__ __forceinline__ uint64_t pack_key(float key, int e) {
   return (static_cast<uint64_t>(u) << 32) | static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(e));
 }
 
-// Selection + gates for one token whose logits are spread over the wave
-// (lane owns experts lane + 64*j).  Lane k < K writes slot k.
-template <int EPL>
-__device__ __forceinline__ void select_and_gate(const float (&logit)[EPL], const float* __restrict__ bias,
-                                                int n_experts, int top_k, int mode, float rsf,
-                                                int32_t* __restrict__ top_idx_row,
-                                                float* __restrict__ gates_row) {
+// Selection + gates for NTOK tokens whose logits are spread over the wave
+// (lane owns experts lane + 64*j); the tokens' reduction chains interleave.
+// Lane k < K writes slot k of every token q with store[q].
+template <int EPL, int NTOK>
+__device__ __forceinline__ void select_and_gate(const float (&logit)[NTOK][EPL],
+                                                const bool (&store)[NTOK],
+                                                const float* __restrict__ bias, int n_experts,
+                                                int top_k, int mode, float rsf,
+                                                int32_t* const (&top_idx_row)[NTOK],
+                                                float* const (&gates_row)[NTOK]) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  float val[EPL];  // value the gate is built from: sigmoid score or logit
-  uint64_t packed[EPL];
+  float val[NTOK][EPL];  // value the gate is built from: sigmoid score or logit
+  uint64_t packed[NTOK][EPL];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    float key = logit[j];
-    if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
-      const float s = sigmoid_det(logit[j]);
-      val[j] = s;
-      key = s + ((bias != nullptr && e < n_experts) ? bias[e] : 0.0f);
-    } else {
-      val[j] = logit[j];
+  for (int q = 0; q < NTOK; ++q)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      float key = logit[q][j];
+      if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
+        const float sg = sigmoid_det(logit[q][j]);
+        val[q][j] = sg;
+        key = sg + ((bias != nullptr && e < n_experts) ? bias[e] : 0.0f);
+      } else {
+        val[q][j] = logit[q][j];
+      }
+      packed[q][j] = e < n_experts ? pack_key(key, e) : 0ull;
     }
-    packed[j] = e < n_experts ? pack_key(key, e) : 0ull;
-  }
-  int my_e = 0;
+  int my_e[NTOK];
+#pragma unroll
+  for (int q = 0; q < NTOK; ++q) my_e[q] = 0;
   for (int k = 0; k < top_k; ++k) {
-    uint64_t best = packed[0];
+    uint64_t best[NTOK];
 #pragma unroll
-    for (int j = 1; j < EPL; ++j) best = packed[j] > best ? packed[j] : best;
-    best = wave_max_u64(best);
-    const int e_win = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best));
-    if (lane == k) my_e = e_win;
+    for (int q = 0; q < NTOK; ++q) {
+      best[q] = packed[q][0];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j == e_win) packed[j] = 0ull;
-  }
-  // Fetch the selected experts' values from their owner lanes.
-  float my_v = 0.0f;
+      for (int j = 1; j < EPL; ++j) best[q] = packed[q][j] > best[q] ? packed[q][j] : best[q];
+    }
+    wave_max_u64<NTOK>(best);
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const float v = __shfl(val[j], my_e & 63, 64);
-    if ((my_e >> 6) == j) my_v = v;
+    for (int q = 0; q < NTOK; ++q) {
+      const int e_win = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best[q]));
+      if (lane == k) my_e[q] = e_win;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (lane + 64 * j == e_win) packed[q][j] = 0ull;
+    }
   }
-  float w;
-  if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
-    float denom = 0.0f;
-    for (int k = 0; k < top_k; ++k) denom = denom + __shfl(my_v, k, 64);
-    denom = denom + 1e-9f;
-    w = (my_v / denom) * rsf;
-  } else {
-    const float m = __shfl(my_v, 0, 64);
-    const float ex = exp_det(my_v - m);
-    float denom = 0.0f;
-    for (int k = 0; k < top_k; ++k) denom = denom + __shfl(ex, k, 64);
-    w = ex / denom;
-  }
-  if (lane < top_k) {
-    top_idx_row[lane] = my_e;
-    gates_row[lane] = w;
+#pragma unroll
+  for (int q = 0; q < NTOK; ++q) {
+    // Fetch the selected experts' values from their owner lanes.
+    float my_v = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const float v = __shfl(val[q][j], my_e[q] & 63, 64);
+      if ((my_e[q] >> 6) == j) my_v = v;
+    }
+    float w;
+    if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
+      float denom = 0.0f;
+      for (int k = 0; k < top_k; ++k) denom = denom + __shfl(my_v, k, 64);
+      denom = denom + 1e-9f;
+      w = (my_v / denom) * rsf;
+    } else {
+      const float m = __shfl(my_v, 0, 64);
+      const float ex = exp_det(my_v - m);
+      float denom = 0.0f;
+      for (int k = 0; k < top_k; ++k) denom = denom + __shfl(ex, k, 64);
+      w = ex / denom;
+    }
+    if (store[q] && lane < top_k) {
+      top_idx_row[q][lane] = my_e[q];
+      gates_row[q][lane] = w;
+    }
   }
 }
 
@@ -363,20 +385,30 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
 
   // Selection: wave w takes tokens w*kTB/4 .. (w+1)*kTB/4 - 1 of the workgroup.
   constexpr int kSel = kTB / 4;
+  static_assert(kSel % 2 == 0, "selection takes tokens in pairs");
 #pragma unroll 1
-  for (int i = 0; i < kSel; ++i) {
+  for (int i = 0; i < kSel; i += 2) {
     const int row = wave * kSel + i;
     const int64_t tok = t0 + row;
     if (tok >= tokens) break;
-    float l[kEPL];
+    float l[2][kEPL];
+    bool st[2];
+    int32_t* ti[2];
+    float* gt[2];
 #pragma unroll
-    for (int j = 0; j < kEPL; ++j) {
-      const int e = lane + 64 * j;
-      l[j] = e < kNP ? lg[row * kNP + e] : 0.0f;
-      if (e < n_experts) logits[tok * n_experts + e] = l[j];
+    for (int q = 0; q < 2; ++q) {
+      st[q] = tok + q < tokens;
+      const int64_t tq = st[q] ? tok + q : tok;
+      ti[q] = top_idx + tq * top_k;
+      gt[q] = gates + tq * top_k;
+#pragma unroll
+      for (int j = 0; j < kEPL; ++j) {
+        const int e = lane + 64 * j;
+        l[q][j] = e < kNP ? lg[(row + q) * kNP + e] : 0.0f;
+        if (st[q] && e < n_experts) logits[tq * n_experts + e] = l[q][j];
+      }
     }
-    select_and_gate<kEPL>(l, bias, n_experts, top_k, mode, rsf, top_idx + tok * top_k,
-                          gates + tok * top_k);
+    select_and_gate<kEPL, 2>(l, st, bias, n_experts, top_k, mode, rsf, ti, gt);
   }
 }
 
@@ -390,14 +422,16 @@ __global__ __launch_bounds__(256) void select_kernel(const float* __restrict__ l
   const int lane = threadIdx.x & 63;
   const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (tok >= tokens) return;
-  float l[EPL];
+  float l[1][EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
-    l[j] = e < n_experts ? logits[tok * n_experts + e] : 0.0f;
+    l[0][j] = e < n_experts ? logits[tok * n_experts + e] : 0.0f;
   }
-  select_and_gate<EPL>(l, bias, n_experts, top_k, mode, rsf, top_idx + tok * top_k,
-                       gates + tok * top_k);
+  const bool st[1] = {true};
+  int32_t* const ti[1] = {top_idx + tok * top_k};
+  float* const gt[1] = {gates + tok * top_k};
+  select_and_gate<EPL, 1>(l, st, bias, n_experts, top_k, mode, rsf, ti, gt);
 }
 
 template <int NT, typename XT, typename WT>
