@@ -398,15 +398,14 @@ __device__ __forceinline__ void barrier_lds() {
   __builtin_amdgcn_s_barrier();
 }
 
-// Epilogue of one bf16 tile through an idle 64 KB LDS stage, so that every
-// global store writes whole 256- or 512-byte row segments.  The stores are
-// raw-buffer stores whose range ends at the expert segment's last row: rows
-// past it are dropped by the hardware range check rather than by a branch.
-// Without SWIGLU the 256 x 256 tile goes in two passes of 128 rows (rows
-// i = 2q, 2q+1 of every wave in pass q); with SWIGLU the 256 x 128 h tile goes
-// in one.  The barriers wait for LDS operations only: the stores stay in
-// flight while the next tile starts.
-template <bool SWIGLU>
+// Epilogue of one bf16 tile without SwiGLU (the down GEMM) through an idle
+// 64 KB LDS stage, so that every global store writes a whole 512-byte row
+// segment.  The stores are raw-buffer stores whose range ends at the expert
+// segment's last row: rows past it are dropped by the hardware range check
+// rather than by a branch.  The 256 x 256 tile goes in two passes of 128 rows
+// (rows i = 2q, 2q+1 of every wave in pass q).  The barriers wait for LDS
+// operations only: the stores stay in flight while the next tile starts.
+// (For the SwiGLU tile, half the bytes, direct stores measured faster.)
 __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_t* lds,
                                                uint16_t* __restrict__ C, int64_t ldc, int64_t row0,
                                                int64_t row_end, int n0, int wm, int wn, int lane,
@@ -414,75 +413,41 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_
   const int frow = lane & 31;
   const int half = lane >> 5;
   const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
-  const int col0 = SWIGLU ? n0 / 2 : n0;  // first output column of the tile
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
   const int row_bytes = static_cast<int>(ldc * 2);
-  if (SWIGLU) {
-    // LDS: 256 rows x 16 chunks of 8 h values; chunk c of row r at position c ^ (r & 15).
+  // LDS row l (0..127) of pass q holds tile row (l >> 6) * 128 + q * 64 + (l & 63):
+  // 32 chunks of 8 values; chunk c of row l at position c ^ (l & 31).
+  const int c = tid & 31;
+  const int voff = ((tid >> 5) * static_cast<int>(ldc) + n0 + c * 8) * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = wm * 128 + i * 32 + frow;
+  for (int q = 0; q < 2; ++q) {
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * q + ii;
+      const int l = wm * 64 + ii * 32 + frow;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          float h[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) h[q] = silu_f32(acc[i][2 * p][g * 4 + q]) * acc[i][2 * p + 1][g * 4 + q];
           uint2 pk;
-          pk.x = pack_bf16x2_rne(h[0], h[1]);
-          pk.y = pack_bf16x2_rne(h[2], h[3]);
-          const int c = wn * 8 + p * 4 + g;
-          *reinterpret_cast<uint2*>(lds + r * 256 + ((c ^ (r & 15)) * 16) + half * 8) = pk;
+          pk.x = pack_bf16x2_rne(acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1]);
+          pk.y = pack_bf16x2_rne(acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]);
+          const int cc = wn * 16 + j * 4 + g;
+          *reinterpret_cast<uint2*>(lds + l * 512 + ((cc ^ (l & 31)) * 16) + half * 8) = pk;
         }
       __builtin_amdgcn_sched_barrier(0);
     }
     barrier_lds();
-    // Thread tid: chunk tid & 15 of rows (tid >> 4) + 16 m.
-    const int c = tid & 15;
-    const int voff = ((tid >> 4) * static_cast<int>(ldc) + col0 + c * 8) * 2;
+    // Thread tid: chunk tid & 31 of LDS rows (tid >> 5) + 8 m.
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
-      const int r = m * 16 + (tid >> 4);
-      const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * 256 + ((c ^ (r & 15)) * 16));
-      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, __builtin_amdgcn_readfirstlane(m * 16 * row_bytes), 0);
+      const int l = m * 8 + (tid >> 5);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 512 + ((c ^ (l & 31)) * 16));
+      const int trow0 = (m >> 3) * 128 + q * 64 + (m & 7) * 8;  // tile row of l, less tid >> 5
+      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, __builtin_amdgcn_readfirstlane(trow0 * row_bytes), 0);
     }
     barrier_lds();
-  } else {
-    // LDS row l (0..127) of pass q holds tile row (l >> 6) * 128 + q * 64 + (l & 63):
-    // 32 chunks of 8 values; chunk c of row l at position c ^ (l & 31).
-    const int c = tid & 31;
-    const int voff = ((tid >> 5) * static_cast<int>(ldc) + col0 + c * 8) * 2;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-#pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
-        const int i = 2 * q + ii;
-        const int l = wm * 64 + ii * 32 + frow;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            uint2 pk;
-            pk.x = pack_bf16x2_rne(acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1]);
-            pk.y = pack_bf16x2_rne(acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]);
-            const int cc = wn * 16 + j * 4 + g;
-            *reinterpret_cast<uint2*>(lds + l * 512 + ((cc ^ (l & 31)) * 16) + half * 8) = pk;
-          }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      barrier_lds();
-      // Thread tid: chunk tid & 31 of LDS rows (tid >> 5) + 8 m.
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int l = m * 8 + (tid >> 5);
-        const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 512 + ((c ^ (l & 31)) * 16));
-        const int trow0 = (m >> 3) * 128 + q * 64 + (m & 7) * 8;  // tile row of l, less tid >> 5
-        __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, __builtin_amdgcn_readfirstlane(trow0 * row_bytes), 0);
-      }
-      barrier_lds();
-    }
   }
 }
 
@@ -738,7 +703,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     } else {
       // stage 1 is idle here: the tile's last step (odd) read it, step 0 of
       // the next tile writes it only after this epilogue's last barrier
-      store_tile_lds<false>(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
+      store_tile_lds(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
     }
     if (g < iters) read_frags(0, 0, 0);
   }
