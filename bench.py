@@ -13,7 +13,8 @@ input resident in HBM before the timed region.  One JSON line on stdout:
   grouped_gemm  gate/up + down together (6*R_kept*D*F FLOP)
   kernels    every stage's HIP-event time and roofline fraction
   cpu_baseline  the NumPy float32 restatement of the layer (oracle/) timed on
-             this host's cores on a 4096-token sample of the same workload
+             this host's cores on up to 16384 tokens of the same workload (all of
+             the headline workload)
 
 Usage: python bench.py [--steps K] [--warmup W] [--spinup-ms MS] [--workload NAME] [--no-cpu-baseline]
 """
@@ -88,7 +89,8 @@ def cpu_baseline(wl_name: str, sample_tokens: int, seed: int) -> dict:
     import oracle as O
     from hanuman_amd import workloads as W
     cores = len(os.sched_getaffinity(0))
-    wl = W.WORKLOADS[wl_name].scaled(sample_tokens)
+    full = W.WORKLOADS[wl_name]
+    wl = full.scaled(min(sample_tokens, full.tokens))
     inp = W.make_inputs(wl, seed=seed)
     params = {"router": inp.router, "expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
               "expert_w_down": inp.w_down}
@@ -126,7 +128,9 @@ def main():
     ap.add_argument("--workload", default=None)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=16384,
+                    help="tokens of the CPU-baseline sample (capped at the workload's; the "
+                         "default is the whole headline workload, ~10 s of CPU work)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the warm-up, as the "
                          "known-size reference for HBM byte counters")
@@ -294,7 +298,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"[bench] cpu baseline on {args.cpu_sample_tokens} tokens, {cores} cores")
+        log(f"[bench] cpu baseline on up to {args.cpu_sample_tokens} tokens, {cores} cores")
         cpu = cpu_baseline(name, args.cpu_sample_tokens, args.seed)
         log(f"[bench] cpu baseline {cpu['value']} tokens/s")
 
