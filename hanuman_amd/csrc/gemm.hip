@@ -63,7 +63,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) with the hardware reciprocal (v_rcp_f32, 1 ulp)
+// in place of the correctly rounded division sequence; the result is
+// rounded to bf16 right after.
+__device__ __forceinline__ float silu_f32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
 
 // Exclusive scan of per-expert m-tile counts into tstart[0..n_experts];
 // returns the total.  Every thread takes four experts.
@@ -509,7 +514,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
   uint32_t a_off[8];
   const uint8_t* a_tile = A;
-  const uint8_t* b_tile = B;
+  // B goes through buffer loads on the tile's 256 weight rows: the per-thread
+  // offset b_off0 stays in one VGPR and the step and round offsets are
+  // uniform (soffset), so no 64-bit address is formed per load.
+  const int b_tile_bytes = 256 * row_bytes;
+  __amdgpu_buffer_rsrc_t b_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, b_tile_bytes, kBufferWord3);
   int ld_t = first, ld_kb = 0, ld_g = 0;  // load side: tile, K step in it, global step
   // GATHER: perm_src of the 8 rows this thread loads in the next tile the load
   // side enters.
@@ -534,7 +544,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
-    b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes;
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes), 0,
+        b_tile_bytes, kBufferWord3);
     // Rows past the buffer (the last tile of the last segment) are clamped to
     // its last row; their results are never stored.
     const int64_t lim = a_rows - 1 - r0;
@@ -566,12 +578,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   auto issue_part = [&](u32x4* ra, u32x4* rb, int p) __attribute__((always_inline)) {
     const int kb = ODD && ld_kb == ksteps ? ksteps - 1 : ld_kb;  // the zero step reloads a real one
     const uint8_t* ab = a_tile + kb * 128;
-    const uint8_t* bb = b_tile + kb * 128;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int i = 2 * p + q;
       ra[i] = *reinterpret_cast<const u32x4*>(ab + a_off[i]);
-      rb[i] = *reinterpret_cast<const u32x4*>(bb + b_off0 + static_cast<uint32_t>(i * 32 * row_bytes));
+      rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            b_rsrc, b_off0, kb * 128 + i * 32 * row_bytes, 0));
     }
   };
   // Once every step is loaded the load side repeats the last one, so every
