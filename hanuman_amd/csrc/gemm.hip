@@ -403,14 +403,16 @@ __device__ __forceinline__ void barrier_lds() {
   __builtin_amdgcn_s_barrier();
 }
 
-// Epilogue of one bf16 tile without SwiGLU (the down GEMM) through an idle
-// 64 KB LDS stage, so that every global store writes a whole 512-byte row
-// segment.  The stores are raw-buffer stores whose range ends at the expert
+// Epilogues of the register-staged kernel, both through the idle 64 KB LDS
+// stage: the waves write their bf16 results to LDS, then every thread stores
+// whole 16-byte chunks, so that each store instruction writes complete row
+// segments.  The stores are raw-buffer stores whose range ends at the expert
 // segment's last row: rows past it are dropped by the hardware range check
-// rather than by a branch.  The 256 x 256 tile goes in two passes of 128 rows
-// (rows i = 2q, 2q+1 of every wave in pass q).  The barriers wait for LDS
-// operations only: the stores stay in flight while the next tile starts.
-// (For the SwiGLU tile, half the bytes, direct stores measured faster.)
+// rather than by a branch.  The barriers wait for LDS operations only: the
+// stores stay in flight while the next tile starts.
+
+// Without SwiGLU (the down GEMM): 512-byte rows, so the 256 x 256 tile goes in
+// two passes of 128 rows (rows i = 2q, 2q+1 of every wave in pass q).
 __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_t* lds,
                                                uint16_t* __restrict__ C, int64_t ldc, int64_t row0,
                                                int64_t row_end, int n0, int wm, int wn, int lane,
@@ -454,6 +456,52 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_
     }
     barrier_lds();
   }
+}
+
+// With SwiGLU (the gate/up GEMM): h = bf16(silu(g) * u) from the interleaved
+// gate/up column blocks is half the tile's columns, 256-byte rows, so the
+// whole tile fits the stage in one pass.  LDS row l = tile row l, 16 chunks of
+// 8 h values; chunk c of row l at position c ^ (l & 15).
+__device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4], uint8_t* lds,
+                                                      uint16_t* __restrict__ C, int64_t ldc,
+                                                      int64_t row0, int64_t row_end, int n0, int wm,
+                                                      int wn, int lane, int tid) {
+  const int frow = lane & 31;
+  const int half = lane >> 5;
+  const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
+  const int row_bytes = static_cast<int>(ldc * 2);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int l = wm * 128 + i * 32 + frow;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float h[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          h[q] = silu_f32(acc[i][2 * p][g * 4 + q]) * acc[i][2 * p + 1][g * 4 + q];
+        uint2 pk;
+        pk.x = pack_bf16x2_rne(h[0], h[1]);
+        pk.y = pack_bf16x2_rne(h[2], h[3]);
+        const int cc = wn * 8 + p * 4 + g;
+        *reinterpret_cast<uint2*>(lds + l * 256 + ((cc ^ (l & 15)) * 16) + half * 8) = pk;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  barrier_lds();
+  // Thread tid: chunk tid & 15 of LDS rows (tid >> 4) + 16 m.
+  const int c = tid & 15;
+  const int voff = ((tid >> 4) * static_cast<int>(ldc) + n0 / 2 + c * 8) * 2;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int l = m * 16 + (tid >> 4);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 256 + ((c ^ (l & 15)) * 16));
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, m * 16 * row_bytes, 0);
+  }
+  barrier_lds();
 }
 
 template <int V>
@@ -709,14 +757,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     int e, n0;
     int64_t row0, row_end;
     decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
-    if constexpr (SWIGLU) {
-      // h is half the tile; direct stores measured faster than LDS staging here
-      store_tile<true, false>(acc, C, ldc, nullptr, nullptr, ncols, e, row0, row_end, n0, wm, wn, lane);
-    } else {
-      // stage 1 is idle here: the tile's last step (odd) read it, step 0 of
-      // the next tile writes it only after this epilogue's last barrier
+    // stage 1 is idle here: the tile's last step (odd) read it, step 0 of the
+    // next tile writes it only after the epilogue's last barrier
+    if constexpr (SWIGLU)
+      store_tile_lds_swiglu(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
+    else
       store_tile_lds(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
-    }
     if (g < iters) read_frags(0, 0, 0);
   }
 }
