@@ -232,6 +232,145 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], uint16_t* 
   }
 }
 
+// Workgroup barrier that waits for this wave's LDS operations only.  Global
+// loads in flight stay in flight: their results land in registers, and the
+// compiler waits for each one before its register is read.
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maximum
+  __builtin_amdgcn_s_barrier();
+}
+
+// Epilogues of the register-staged kernel, both through the idle 64 KB LDS
+// stage: the waves write their bf16 results to LDS, then every thread stores
+// whole 16-byte chunks, so that each store instruction writes complete row
+// segments.  The stores are raw-buffer stores whose range ends at the expert
+// segment's last row: rows past it are dropped by the hardware range check
+// rather than by a branch.  The barriers wait for LDS operations only: the
+// stores stay in flight while the next tile starts.
+
+// FP8: the accumulators are dequantised first, acc * s_row * s_col, with the
+// tile's 256 row scales at ssc[0..255] and 256 column scales at ssc[256..511]
+// (LDS).
+
+// Without SwiGLU (the down GEMM): 512-byte rows, so the 256 x 256 tile goes in
+// two passes of 128 rows (rows i = 2q, 2q+1 of every wave in pass q).
+template <bool FP8>
+__device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_t* lds,
+                                               uint16_t* __restrict__ C, int64_t ldc, int64_t row0,
+                                               int64_t row_end, int n0, int wm, int wn, int lane,
+                                               int tid, const float* ssc) {
+  const int frow = lane & 31;
+  const int half = lane >> 5;
+  const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
+  const int row_bytes = static_cast<int>(ldc * 2);
+  // LDS row l (0..127) of pass q holds tile row (l >> 6) * 128 + q * 64 + (l & 63):
+  // 32 chunks of 8 values; chunk c of row l at position c ^ (l & 31).
+  const int c = tid & 31;
+  const int voff = ((tid >> 5) * static_cast<int>(ldc) + n0 + c * 8) * 2;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * q + ii;
+      const int l = wm * 64 + ii * 32 + frow;
+      const float sa = FP8 ? ssc[wm * 128 + i * 32 + frow] : 1.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = acc[i][j][g * 4 + r];
+          if (FP8) {
+            const f32x4 sb =
+                *reinterpret_cast<const f32x4*>(ssc + kBM + wn * 128 + j * 32 + g * 8 + half * 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = v[r] * sa * sb[r];
+          }
+          uint2 pk;
+          pk.x = pack_bf16x2_rne(v[0], v[1]);
+          pk.y = pack_bf16x2_rne(v[2], v[3]);
+          const int cc = wn * 16 + j * 4 + g;
+          *reinterpret_cast<uint2*>(lds + l * 512 + ((cc ^ (l & 31)) * 16) + half * 8) = pk;
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    barrier_lds();
+    // Thread tid: chunk tid & 31 of LDS rows (tid >> 5) + 8 m.
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int l = m * 8 + (tid >> 5);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 512 + ((c ^ (l & 31)) * 16));
+      const int trow0 = (m >> 3) * 128 + q * 64 + (m & 7) * 8;  // tile row of l, less tid >> 5
+      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, __builtin_amdgcn_readfirstlane(trow0 * row_bytes), 0);
+    }
+    barrier_lds();
+  }
+}
+
+// With SwiGLU (the gate/up GEMM): h = bf16(silu(g) * u) from the interleaved
+// gate/up column blocks is half the tile's columns, 256-byte rows, so the
+// whole tile fits the stage in one pass.  LDS row l = tile row l, 16 chunks of
+// 8 h values; chunk c of row l at position c ^ (l & 15).
+template <bool FP8>
+__device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4], uint8_t* lds,
+                                                      uint16_t* __restrict__ C, int64_t ldc,
+                                                      int64_t row0, int64_t row_end, int n0, int wm,
+                                                      int wn, int lane, int tid, const float* ssc) {
+  const int frow = lane & 31;
+  const int half = lane >> 5;
+  const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
+  const int row_bytes = static_cast<int>(ldc * 2);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int l = wm * 128 + i * 32 + frow;
+    const float sa = FP8 ? ssc[l] : 1.0f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float h[4];
+        f32x4 sg, su;
+        if (FP8) {
+          sg = *reinterpret_cast<const f32x4*>(ssc + kBM + wn * 128 + 2 * p * 32 + g * 8 + half * 4);
+          su = *reinterpret_cast<const f32x4*>(ssc + kBM + wn * 128 + (2 * p + 1) * 32 + g * 8 +
+                                               half * 4);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float gv = acc[i][2 * p][g * 4 + q];
+          float uv = acc[i][2 * p + 1][g * 4 + q];
+          if (FP8) {
+            gv = gv * sa * sg[q];
+            uv = uv * sa * su[q];
+          }
+          h[q] = silu_f32(gv) * uv;
+        }
+        uint2 pk;
+        pk.x = pack_bf16x2_rne(h[0], h[1]);
+        pk.y = pack_bf16x2_rne(h[2], h[3]);
+        const int cc = wn * 8 + p * 4 + g;
+        *reinterpret_cast<uint2*>(lds + l * 256 + ((cc ^ (l & 15)) * 16) + half * 8) = pk;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  barrier_lds();
+  // Thread tid: chunk tid & 15 of LDS rows (tid >> 4) + 16 m.
+  const int c = tid & 15;
+  const int voff = ((tid >> 4) * static_cast<int>(ldc) + n0 / 2 + c * 8) * 2;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int l = m * 16 + (tid >> 4);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 256 + ((c ^ (l & 15)) * 16));
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, m * 16 * row_bytes, 0);
+  }
+  barrier_lds();
+}
+
 // Main loop with direct global -> LDS loads (used for the e4m3 operands,
 // whose 32-byte MFMA fragments leave no registers for load staging): the next
 // K step's A and B tiles (2 x 32 KB) go straight into the other LDS stage with
@@ -254,6 +393,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int32_t tstart[kMaxExperts + 1];
   __shared__ int32_t scan_tmp[kThreads];
+  // FP8: the current tile's row scales [0, 256) and column scales [256, 512)
+  __shared__ __attribute__((aligned(16))) float sscale[FP8 ? 2 * kBM : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -371,6 +512,17 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
   read_frags(0, 0, 0);
 
   for (int t = first; t < hi; t += per_xcd) {
+    // FP8 with SwiGLU: this thread's row and column scale of the tile (rows
+    // past the buffer clamped), loaded now and written to LDS after the K loop
+    float sa_own = 0.0f, sb_own = 0.0f;
+    if (FP8 && SWIGLU) {
+      int e, n0;
+      int64_t row0, row_end;
+      decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+      const int64_t r = row0 + tid < a_rows ? row0 + tid : a_rows - 1;
+      sa_own = a_scale[r];
+      sb_own = b_scale[static_cast<int64_t>(e) * ncols + n0 + tid];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -389,119 +541,26 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
     int e, n0;
     int64_t row0, row_end;
     decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
-    store_tile<SWIGLU, FP8>(acc, C, ldc, a_scale, b_scale, ncols, e, row0, row_end, n0, wm, wn, lane);
+    if constexpr (SWIGLU) {
+      if (FP8) {
+        // the previous tile's epilogue read sscale before its last barrier
+        sscale[tid] = sa_own;
+        sscale[kBM + tid] = sb_own;
+        barrier_lds();
+      }
+      // Stage cur is idle here: the last step read it and the next tile's
+      // loads go into it only after the epilogue's last barrier.
+      store_tile_lds_swiglu<FP8>(acc, smem + cur * kStageBytes, C, ldc, row0, row_end, n0, wm, wn,
+                                 lane, tid, sscale);
+    } else {
+      // direct stores measured faster than LDS staging for this kernel's
+      // 256-column tiles
+      store_tile<false, FP8>(acc, C, ldc, a_scale, b_scale, ncols, e, row0, row_end, n0, wm, wn,
+                             lane);
+    }
     if (next) read_frags(0, cur ^ 1, 0);
     cur ^= 1;
   }
-}
-
-// Workgroup barrier that waits for this wave's LDS operations only.  Global
-// loads in flight stay in flight: their results land in registers, and the
-// compiler waits for each one before its register is read.
-__device__ __forceinline__ void barrier_lds() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maximum
-  __builtin_amdgcn_s_barrier();
-}
-
-// Epilogues of the register-staged kernel, both through the idle 64 KB LDS
-// stage: the waves write their bf16 results to LDS, then every thread stores
-// whole 16-byte chunks, so that each store instruction writes complete row
-// segments.  The stores are raw-buffer stores whose range ends at the expert
-// segment's last row: rows past it are dropped by the hardware range check
-// rather than by a branch.  The barriers wait for LDS operations only: the
-// stores stay in flight while the next tile starts.
-
-// Without SwiGLU (the down GEMM): 512-byte rows, so the 256 x 256 tile goes in
-// two passes of 128 rows (rows i = 2q, 2q+1 of every wave in pass q).
-__device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_t* lds,
-                                               uint16_t* __restrict__ C, int64_t ldc, int64_t row0,
-                                               int64_t row_end, int n0, int wm, int wn, int lane,
-                                               int tid) {
-  const int frow = lane & 31;
-  const int half = lane >> 5;
-  const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
-  const int row_bytes = static_cast<int>(ldc * 2);
-  // LDS row l (0..127) of pass q holds tile row (l >> 6) * 128 + q * 64 + (l & 63):
-  // 32 chunks of 8 values; chunk c of row l at position c ^ (l & 31).
-  const int c = tid & 31;
-  const int voff = ((tid >> 5) * static_cast<int>(ldc) + n0 + c * 8) * 2;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const int i = 2 * q + ii;
-      const int l = wm * 64 + ii * 32 + frow;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          uint2 pk;
-          pk.x = pack_bf16x2_rne(acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1]);
-          pk.y = pack_bf16x2_rne(acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]);
-          const int cc = wn * 16 + j * 4 + g;
-          *reinterpret_cast<uint2*>(lds + l * 512 + ((cc ^ (l & 31)) * 16) + half * 8) = pk;
-        }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    barrier_lds();
-    // Thread tid: chunk tid & 31 of LDS rows (tid >> 5) + 8 m.
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const int l = m * 8 + (tid >> 5);
-      const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 512 + ((c ^ (l & 31)) * 16));
-      const int trow0 = (m >> 3) * 128 + q * 64 + (m & 7) * 8;  // tile row of l, less tid >> 5
-      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, __builtin_amdgcn_readfirstlane(trow0 * row_bytes), 0);
-    }
-    barrier_lds();
-  }
-}
-
-// With SwiGLU (the gate/up GEMM): h = bf16(silu(g) * u) from the interleaved
-// gate/up column blocks is half the tile's columns, 256-byte rows, so the
-// whole tile fits the stage in one pass.  LDS row l = tile row l, 16 chunks of
-// 8 h values; chunk c of row l at position c ^ (l & 15).
-__device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4], uint8_t* lds,
-                                                      uint16_t* __restrict__ C, int64_t ldc,
-                                                      int64_t row0, int64_t row_end, int n0, int wm,
-                                                      int wn, int lane, int tid) {
-  const int frow = lane & 31;
-  const int half = lane >> 5;
-  const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
-  const int row_bytes = static_cast<int>(ldc * 2);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int l = wm * 128 + i * 32 + frow;
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float h[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          h[q] = silu_f32(acc[i][2 * p][g * 4 + q]) * acc[i][2 * p + 1][g * 4 + q];
-        uint2 pk;
-        pk.x = pack_bf16x2_rne(h[0], h[1]);
-        pk.y = pack_bf16x2_rne(h[2], h[3]);
-        const int cc = wn * 8 + p * 4 + g;
-        *reinterpret_cast<uint2*>(lds + l * 256 + ((cc ^ (l & 15)) * 16) + half * 8) = pk;
-      }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  barrier_lds();
-  // Thread tid: chunk tid & 15 of LDS rows (tid >> 4) + 16 m.
-  const int c = tid & 15;
-  const int voff = ((tid >> 4) * static_cast<int>(ldc) + n0 / 2 + c * 8) * 2;
-#pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int l = m * 16 + (tid >> 4);
-    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 256 + ((c ^ (l & 15)) * 16));
-    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, m * 16 * row_bytes, 0);
-  }
-  barrier_lds();
 }
 
 template <int V>
@@ -760,9 +819,11 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     // stage 1 is idle here: the tile's last step (odd) read it, step 0 of the
     // next tile writes it only after the epilogue's last barrier
     if constexpr (SWIGLU)
-      store_tile_lds_swiglu(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
+      store_tile_lds_swiglu<false>(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane,
+                                   tid, nullptr);
     else
-      store_tile_lds(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
+      store_tile_lds<false>(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid,
+                            nullptr);
     if (g < iters) read_frags(0, 0, 0);
   }
 }
