@@ -387,7 +387,10 @@ __global__ __launch_bounds__(256) void quantize_rows_fp8_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
-  if (offsets != nullptr && r >= offsets[n_experts]) return;
+  if (offsets != nullptr && r >= offsets[n_experts]) {  // past the kept rows: not read
+    if (lane == 0) scale[r] = 1.0f;
+    return;
+  }
   const int chunks = cols / 8;
   const uint16_t* src = a + r * cols;
   float s, inv;

@@ -167,13 +167,14 @@ def permute_rows_fp8(x: torch.Tensor, plan: Plan):
 
 def quantize_rows_fp8(a: torch.Tensor, offsets: torch.Tensor | None = None):
     """Per-row e4m3 codes and scales of a bf16 matrix ``[rows, cols]``; rows at
-    or past ``offsets[-1]`` are skipped (left as allocated) when offsets are given."""
+    or past ``offsets[-1]`` are not read when offsets are given (codes left as
+    allocated, scale 1)."""
     _check(a, "a", 2)
     if a.dtype != torch.bfloat16:
         raise TypeError("quantize_rows_fp8 takes a bf16 matrix")
     rows, cols = a.shape
     q = torch.empty((rows, cols), dtype=torch.uint8, device=a.device)
-    sc = torch.ones(rows, dtype=torch.float32, device=a.device)
+    sc = torch.empty(rows, dtype=torch.float32, device=a.device)
     n = 0
     if offsets is not None:
         _check(offsets, "offsets", 1)

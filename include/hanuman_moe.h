@@ -126,7 +126,8 @@ int hmoe_permute_rows_fp8(const void* x, int x_dtype, int64_t tokens, int d_mode
 
 /* Same per-row rule for a bf16 matrix a [rows, cols] (the SwiGLU output h
  * before the fp8 down GEMM).  With offsets != NULL, rows at or past
- * offsets[n_experts] are left untouched.  cols % 8 == 0. */
+ * offsets[n_experts] are not read: their codes are left untouched and their
+ * scale is set to 1.  cols % 8 == 0. */
 int hmoe_quantize_rows_fp8(const void* a, int64_t rows, int cols, const int32_t* offsets,
                            int n_experts, uint8_t* q, float* scale, hmoe_stream_t stream);
 

@@ -410,7 +410,7 @@ def test_quantize_rows_fp8_bit_exact_and_skips_past_offsets(gpu):
     q2, s2 = K.quantize_rows_fp8(dev_bf16(h, gpu), offsets)
     torch.cuda.synchronize()
     assert_bits_equal(q2.cpu().numpy()[:250], q_ref[:250], "codes below offsets[-1]")
-    assert np.all(s2.cpu().numpy()[250:] == 1.0)   # rows past the kept total untouched
+    assert np.all(s2.cpu().numpy()[250:] == 1.0)   # rows past the kept total: scale 1, not read
 
 
 def test_pack_fp8_layouts(gpu):
