@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const TY* __restrict__ ys,
   float my_g = 0.0f;
   if (lane < top_k) {
     my_pos = slot_pos[t * top_k + lane];
-    my_g = bf16_bits_to_f32(f32_to_bf16_bits(gates[t * top_k + lane]));
+    my_g = gates != nullptr ? bf16_bits_to_f32(f32_to_bf16_bits(gates[t * top_k + lane])) : 1.0f;
   }
   int32_t pos[KMAX];
   float g[KMAX];
@@ -189,7 +189,7 @@ extern "C" int hmoe_combine(const void* ys, int ys_dtype, const int32_t* slot_po
   HMOE_REQUIRE(residual == nullptr || residual_dtype == HMOE_BF16 || residual_dtype == HMOE_F32,
                "combine: residual dtype must be F32 or BF16");
   if (tokens == 0) return HMOE_OK;
-  HMOE_REQUIRE(ys && slot_pos && gates && out, "combine: null pointer argument");
+  HMOE_REQUIRE(ys && slot_pos && out, "combine: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4)));
   if (top_k <= 2)
@@ -201,4 +201,14 @@ extern "C" int hmoe_combine(const void* ys, int ys_dtype, const int32_t* slot_po
   else
     launch_combine<16>(ys, ys_dtype, slot_pos, gates, residual, residual_dtype, tokens, top_k, d_model, out, out_dtype, grid, s);
   return check_launch("hmoe_combine");
+}
+
+// The VJP of the row gather xs[j] = x_flat[perm_src[j] / K] (moe.py:56):
+// dx[t] = sum_k d_xs[slot_pos[t*K+k]] over kept slots, k ascending in float32
+// -- the combine with unit weights.
+extern "C" int hmoe_gather_bwd(const void* d_xs, int d_xs_dtype, const int32_t* slot_pos,
+                               int64_t tokens, int top_k, int d_model, void* dx, int dx_dtype,
+                               hmoe_stream_t stream) {
+  return hmoe_combine(d_xs, d_xs_dtype, slot_pos, nullptr, nullptr, HMOE_F32, tokens, top_k,
+                      d_model, dx, dx_dtype, stream);
 }

@@ -869,6 +869,8 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, false>),
       reinterpret_cast<const void*>(grouped_gemm_regs<true, false, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<true, true, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<false, true>),
   };
@@ -915,8 +917,10 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
                      offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n, gather_src,     \
                      gather_k, gather_rows)
     if (gather_src != nullptr) {
-      if (odd) HMOE_LAUNCH_REGS(true, true, true);
-      else HMOE_LAUNCH_REGS(true, false, true);
+      if (swiglu && odd) HMOE_LAUNCH_REGS(true, true, true);
+      else if (swiglu) HMOE_LAUNCH_REGS(true, false, true);
+      else if (odd) HMOE_LAUNCH_REGS(false, true, true);
+      else HMOE_LAUNCH_REGS(false, false, true);
     } else if (swiglu && odd) HMOE_LAUNCH_REGS(true, true, false);
     else if (swiglu) HMOE_LAUNCH_REGS(true, false, false);
     else if (odd) HMOE_LAUNCH_REGS(false, true, false);
@@ -990,6 +994,76 @@ extern "C" int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_ex
   return launch_grouped(false, false, h, w_down_packed, nullptr, nullptr, offsets, n_experts,
                         rows_cap, d_ff, d_model, ys, d_model, static_cast<hipStream_t>(stream),
                         "hmoe_grouped_down");
+}
+
+// ---- backward (the VJP of moe.py:70-74) -------------------------------------
+
+extern "C" int hmoe_grouped_gate_up_raw_gather(const void* x, int64_t tokens, int top_k,
+                                               const int32_t* perm_src, const int32_t* offsets,
+                                               int n_experts, int64_t rows_cap, int d_model,
+                                               int d_ff, const void* w_gate_up_packed, void* gu,
+                                               hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_raw_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
+               n_experts);
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
+               "grouped_gate_up_raw_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_raw_gather: d_model must be a multiple of %d (got %d)", kBK,
+                    d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_raw_gather: d_ff must be a multiple of %d (got %d)", kBN / 2,
+                    d_ff);
+  HMOE_REQUIRE(tokens * d_model * 2 < (int64_t(1) << 31),
+               "grouped_gate_up_raw_gather: x must be smaller than 2 GiB");
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && perm_src && offsets && w_gate_up_packed && gu,
+               "grouped_gate_up_raw_gather: null pointer argument");
+  return launch_grouped(false, false, x, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, gu, 2 * d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_raw_gather", perm_src, top_k,
+                        static_cast<int>(tokens));
+}
+
+extern "C" int hmoe_grouped_dgrad_down(const void* d_ys, const int32_t* offsets, int n_experts,
+                                       int64_t rows_cap, int d_model, int d_ff,
+                                       const void* w_down_dgrad, void* dh, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_dgrad_down: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "grouped_dgrad_down: rows_cap must be >= 0");
+  HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
+                    "grouped_dgrad_down: d_model must be a multiple of %d (got %d)", kBK, d_model);
+  HMOE_REQUIRE_CODE(d_ff % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_dgrad_down: d_ff must be a multiple of %d (got %d)", kBN, d_ff);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(d_ys && offsets && w_down_dgrad && dh, "grouped_dgrad_down: null pointer argument");
+  return launch_grouped(false, false, d_ys, w_down_dgrad, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, d_ff, dh, d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_dgrad_down");
+}
+
+extern "C" int hmoe_grouped_dgrad_gate_up(const void* dgu, const int32_t* offsets, int n_experts,
+                                          int64_t rows_cap, int d_model, int d_ff,
+                                          const void* w_gate_up_dgrad, void* d_xs,
+                                          hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_dgrad_gate_up: n_experts must be in [1, %d] (got %d)", kMaxExperts,
+               n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "grouped_dgrad_gate_up: rows_cap must be >= 0");
+  HMOE_REQUIRE_CODE(d_ff % (kBK / 2) == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_dgrad_gate_up: d_ff must be a multiple of %d (got %d)", kBK / 2, d_ff);
+  HMOE_REQUIRE_CODE(d_model % kBN == 0 && d_model > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_dgrad_gate_up: d_model must be a multiple of %d (got %d)", kBN,
+                    d_model);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(dgu && offsets && w_gate_up_dgrad && d_xs,
+               "grouped_dgrad_gate_up: null pointer argument");
+  return launch_grouped(false, false, dgu, w_gate_up_dgrad, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, 2 * d_ff, d_model, d_xs, d_model,
+                        static_cast<hipStream_t>(stream), "hmoe_grouped_dgrad_gate_up");
 }
 
 extern "C" int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_scale,

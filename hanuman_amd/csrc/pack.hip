@@ -63,6 +63,37 @@ __global__ __launch_bounds__(256) void pack_transpose_kernel(const TW* __restric
   }
 }
 
+// Operands of the backward's data-gradient GEMMs, which contract over the
+// forward's output columns: the masters are already "K contiguous" for them,
+// so packing is a bf16 cast row by row.  GATE_UP interleaves row r of w_gate
+// and w_up in 32-column blocks (destination column p holds gate column
+// (p / 64) * 32 + p % 32 when p % 64 < 32, else that up column), the column
+// order of the gate/up GEMM's output.  One thread per 8 destination values.
+template <typename TW, bool GATE_UP>
+__global__ __launch_bounds__(256) void pack_rows_kernel(const TW* __restrict__ src0,
+                                                        const TW* __restrict__ src1,
+                                                        int64_t rows, int cols_c,
+                                                        uint16_t* __restrict__ dst) {
+  const int dst_cols = GATE_UP ? 2 * cols_c : cols_c;
+  const int64_t groups = rows * (dst_cols / 8);
+  for (int64_t gi = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; gi < groups;
+       gi += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = gi / (dst_cols / 8);
+    const int p0 = static_cast<int>(gi - r * (dst_cols / 8)) * 8;
+    const TW* src = src0;
+    int c0 = p0;
+    if (GATE_UP) {
+      src = (p0 & 63) < 32 ? src0 : src1;
+      c0 = (p0 >> 6) * 32 + (p0 & 31);
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[q] = pack_bf16x2(load_w(src, r * cols_c + c0 + 2 * q), load_w(src, r * cols_c + c0 + 2 * q + 1));
+    *reinterpret_cast<u32x4*>(dst + r * dst_cols + p0) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
 // ----------------------------------------------------------- e4m3 packing --
 // Per-output-channel e4m3 codes (same rule as the activations: codes
 // e4m3(clamp(w * (448/amax), +-448)), scale amax/448, amax over the reduction
@@ -266,4 +297,50 @@ extern "C" int hmoe_pack_down(const void* w_down, int w_dtype, int n_experts, in
                        static_cast<const uint16_t*>(w_down), static_cast<const uint16_t*>(nullptr),
                        d_ff, d_model, static_cast<uint16_t*>(packed));
   return check_launch("hmoe_pack_down");
+}
+
+// ---- backward operands --------------------------------------------------------
+
+extern "C" int hmoe_pack_down_dgrad(const void* w_down, int w_dtype, int n_experts, int d_ff,
+                                    int d_model, void* packed, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && d_model >= 1 && d_ff >= 1, "pack_down_dgrad: sizes must be >= 1");
+  HMOE_REQUIRE(d_model % 8 == 0, "pack_down_dgrad: d_model must be a multiple of 8 (got %d)", d_model);
+  HMOE_REQUIRE(w_dtype == HMOE_F32 || w_dtype == HMOE_BF16, "pack_down_dgrad: dtype must be F32 or BF16");
+  HMOE_REQUIRE(w_down && packed, "pack_down_dgrad: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows = static_cast<int64_t>(n_experts) * d_ff;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(rows * (d_model / 8), 256), 65536)));
+  if (w_dtype == HMOE_F32)
+    hipLaunchKernelGGL((pack_rows_kernel<float, false>), grid, dim3(256), 0, s,
+                       static_cast<const float*>(w_down), static_cast<const float*>(nullptr), rows,
+                       d_model, static_cast<uint16_t*>(packed));
+  else
+    hipLaunchKernelGGL((pack_rows_kernel<uint16_t, false>), grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(w_down), static_cast<const uint16_t*>(nullptr),
+                       rows, d_model, static_cast<uint16_t*>(packed));
+  return check_launch("hmoe_pack_down_dgrad");
+}
+
+extern "C" int hmoe_pack_gate_up_dgrad(const void* w_gate, const void* w_up, int w_dtype,
+                                       int n_experts, int d_model, int d_ff, void* packed,
+                                       hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && d_model >= 1 && d_ff >= 1, "pack_gate_up_dgrad: sizes must be >= 1");
+  HMOE_REQUIRE(d_ff % 32 == 0, "pack_gate_up_dgrad: d_ff must be a multiple of 32 (got %d)", d_ff);
+  HMOE_REQUIRE(w_dtype == HMOE_F32 || w_dtype == HMOE_BF16,
+               "pack_gate_up_dgrad: dtype must be F32 or BF16");
+  HMOE_REQUIRE(w_gate && w_up && packed, "pack_gate_up_dgrad: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows = static_cast<int64_t>(n_experts) * d_model;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(rows * (2 * d_ff / 8), 256), 65536)));
+  if (w_dtype == HMOE_F32)
+    hipLaunchKernelGGL((pack_rows_kernel<float, true>), grid, dim3(256), 0, s,
+                       static_cast<const float*>(w_gate), static_cast<const float*>(w_up), rows,
+                       d_ff, static_cast<uint16_t*>(packed));
+  else
+    hipLaunchKernelGGL((pack_rows_kernel<uint16_t, true>), grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(w_gate), static_cast<const uint16_t*>(w_up), rows,
+                       d_ff, static_cast<uint16_t*>(packed));
+  return check_launch("hmoe_pack_gate_up_dgrad");
 }

@@ -363,3 +363,159 @@ def router_aux(logits: torch.Tensor, top_idx: torch.Tensor, batch: int, seq: int
     call("hmoe_router_aux", _ptr(logits), _ptr(top_idx), batch, seq, N, top_idx.shape[1],
          _ptr(losses), _ptr(counts), _ptr(work), work.numel(), _stream())
     return losses, counts
+
+
+# ---------------------------------------------------------------- backward --
+# Data gradients of the layer (the VJP of moe.py:170-246 with the routing held
+# fixed); see hanuman_amd.backward for the composed pass.
+
+def combine_bwd(dy: torch.Tensor, ys: torch.Tensor, plan: Plan, gates: torch.Tensor):
+    """VJP of :func:`combine`: ``(d_ys bf16 [rows, D], d_gates f32 [T, K])``;
+    rows of ``d_ys`` no kept slot maps to are left as allocated."""
+    _check(dy, "dy", 2)
+    _check(ys, "ys", 2)
+    _check(gates, "gates", 2)
+    T, D = dy.shape
+    K = plan.top_k
+    if (dy.dtype != torch.float32 or ys.dtype != torch.bfloat16 or ys.shape[1] != D
+            or tuple(gates.shape) != (T, K) or gates.dtype != torch.float32
+            or plan.slot_pos.numel() != T * K):
+        raise ValueError("combine_bwd: inconsistent shapes or dtypes")
+    d_ys = torch.empty_like(ys)
+    d_g = torch.empty((T, K), dtype=torch.float32, device=dy.device)
+    call("hmoe_combine_bwd", _ptr(dy), _ptr(ys), _ptr(plan.slot_pos), _ptr(gates), T, K, D,
+         _ptr(d_ys), _ptr(d_g), _stream())
+    return d_ys, d_g
+
+
+def grouped_gate_up_raw_gather(x: torch.Tensor, plan: Plan, w_gate_up: torch.Tensor) -> torch.Tensor:
+    """g and u (``moe.py:70-71``) of the dispatched rows of ``x``, bf16
+    ``[rows_cap, 2F]`` in the packed gate/up column order."""
+    _check(x, "x", 2)
+    _check(w_gate_up, "w_gate_up", 3)
+    if x.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16:
+        raise TypeError("grouped_gate_up_raw_gather takes bf16 operands")
+    T, D = x.shape
+    N, F2, D2 = w_gate_up.shape
+    if D2 != D or plan.n_experts != N or plan.slot_pos.numel() != T * plan.top_k:
+        raise ValueError("grouped_gate_up_raw_gather: inconsistent shapes")
+    gu = torch.empty((plan.rows_cap, F2), dtype=torch.bfloat16, device=x.device)
+    call("hmoe_grouped_gate_up_raw_gather", _ptr(x), T, plan.top_k, _ptr(plan.perm_src),
+         _ptr(plan.offsets), N, plan.rows_cap, D, F2 // 2, _ptr(w_gate_up), _ptr(gu), _stream())
+    return gu
+
+
+def swiglu_bwd(dh: torch.Tensor, gu: torch.Tensor, offsets: torch.Tensor | None) -> torch.Tensor:
+    """VJP of ``h = silu(g) * u`` (``moe.py:72``): ``dgu`` bf16 ``[rows, 2F]`` in
+    ``gu``'s column order; rows at or past ``offsets[-1]`` left as allocated."""
+    _check(dh, "dh", 2)
+    _check(gu, "gu", 2)
+    rows, F = dh.shape
+    if (dh.dtype != torch.bfloat16 or gu.dtype != torch.bfloat16
+            or tuple(gu.shape) != (rows, 2 * F)):
+        raise ValueError("swiglu_bwd: inconsistent shapes or dtypes")
+    n = 1
+    if offsets is not None:
+        _check(offsets, "offsets", 1)
+        n = offsets.numel() - 1
+    dgu = torch.empty_like(gu)
+    call("hmoe_swiglu_bwd", _ptr(dh), _ptr(gu), _ptr(offsets), n, rows, F, _ptr(dgu), _stream())
+    return dgu
+
+
+def pack_down_dgrad(w_down: torch.Tensor) -> torch.Tensor:
+    """bf16 ``[N, F, D]`` operand of :func:`grouped_dgrad_down` from the ``[N,F,D]`` master."""
+    _check(w_down, "w_down", 3)
+    N, F, D = w_down.shape
+    out = torch.empty((N, F, D), dtype=torch.bfloat16, device=w_down.device)
+    call("hmoe_pack_down_dgrad", _ptr(w_down), _dtype_code(w_down), N, F, D, _ptr(out), _stream())
+    return out
+
+
+def pack_gate_up_dgrad(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """bf16 ``[N, D, 2F]`` operand of :func:`grouped_dgrad_gate_up` from the
+    ``[N,D,F]`` masters (columns in the packed gate/up order)."""
+    _check(w_gate, "w_gate", 3)
+    _check(w_up, "w_up", 3)
+    if w_gate.shape != w_up.shape or w_gate.dtype != w_up.dtype:
+        raise ValueError("w_gate and w_up must have the same shape and dtype")
+    N, D, F = w_gate.shape
+    out = torch.empty((N, D, 2 * F), dtype=torch.bfloat16, device=w_gate.device)
+    call("hmoe_pack_gate_up_dgrad", _ptr(w_gate), _ptr(w_up), _dtype_code(w_gate), N, D, F,
+         _ptr(out), _stream())
+    return out
+
+
+def grouped_dgrad_down(d_ys: torch.Tensor, offsets: torch.Tensor, w_down_dgrad: torch.Tensor) -> torch.Tensor:
+    """``dh = bf16(d_ys Wd[e]^T)`` per expert segment (VJP of ``moe.py:73``)."""
+    _check(d_ys, "d_ys", 2)
+    _check(offsets, "offsets", 1)
+    _check(w_down_dgrad, "w_down_dgrad", 3)
+    N, F, D = w_down_dgrad.shape
+    if (d_ys.dtype != torch.bfloat16 or w_down_dgrad.dtype != torch.bfloat16
+            or d_ys.shape[1] != D or offsets.numel() != N + 1):
+        raise ValueError("grouped_dgrad_down: inconsistent shapes or dtypes")
+    R = d_ys.shape[0]
+    dh = torch.empty((R, F), dtype=torch.bfloat16, device=d_ys.device)
+    call("hmoe_grouped_dgrad_down", _ptr(d_ys), _ptr(offsets), N, R, D, F, _ptr(w_down_dgrad),
+         _ptr(dh), _stream())
+    return dh
+
+
+def grouped_dgrad_gate_up(dgu: torch.Tensor, offsets: torch.Tensor, w_gate_up_dgrad: torch.Tensor) -> torch.Tensor:
+    """``d_xs = bf16(dg Wg[e]^T + du Wu[e]^T)`` per expert segment (VJP of
+    ``moe.py:70-71``)."""
+    _check(dgu, "dgu", 2)
+    _check(offsets, "offsets", 1)
+    _check(w_gate_up_dgrad, "w_gate_up_dgrad", 3)
+    N, D, F2 = w_gate_up_dgrad.shape
+    if (dgu.dtype != torch.bfloat16 or w_gate_up_dgrad.dtype != torch.bfloat16
+            or dgu.shape[1] != F2 or offsets.numel() != N + 1):
+        raise ValueError("grouped_dgrad_gate_up: inconsistent shapes or dtypes")
+    R = dgu.shape[0]
+    d_xs = torch.empty((R, D), dtype=torch.bfloat16, device=dgu.device)
+    call("hmoe_grouped_dgrad_gate_up", _ptr(dgu), _ptr(offsets), N, R, D, F2 // 2,
+         _ptr(w_gate_up_dgrad), _ptr(d_xs), _stream())
+    return d_xs
+
+
+def gather_bwd(d_xs: torch.Tensor, plan: Plan, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """VJP of the row gather (``moe.py:56``): ``dx[t] = sum_k d_xs[slot_pos[t,k]]``."""
+    _check(d_xs, "d_xs", 2)
+    T = plan.slot_pos.numel() // plan.top_k
+    D = d_xs.shape[1]
+    dx = torch.empty((T, D), dtype=out_dtype, device=d_xs.device)
+    call("hmoe_gather_bwd", _ptr(d_xs), _dtype_code(d_xs), _ptr(plan.slot_pos), T, plan.top_k, D,
+         _ptr(dx), _DT[out_dtype], _stream())
+    return dx
+
+
+def router_bwd(logits: torch.Tensor | None, top_idx: torch.Tensor, gates: torch.Tensor,
+               d_gates: torch.Tensor, n_experts: int, mode: int = _lib.ROUTE_SOFTMAX,
+               routed_scaling_factor: float = 1.0) -> torch.Tensor:
+    """``d_logits`` f32 ``[T, N]`` from ``d_gates`` (VJP of ``moe.py:179-192``)."""
+    _check(top_idx, "top_idx", 2)
+    _check(d_gates, "d_gates", 2)
+    T, K = top_idx.shape
+    if logits is not None:
+        _check(logits, "logits", 2)
+    dl = torch.empty((T, n_experts), dtype=torch.float32, device=top_idx.device)
+    call("hmoe_router_bwd", _ptr(logits), _ptr(top_idx), _ptr(gates), _ptr(d_gates), T,
+         n_experts, K, mode, routed_scaling_factor, _ptr(dl), _stream())
+    return dl
+
+
+def router_dx(d_logits: torch.Tensor, router_w: torch.Tensor, dx: torch.Tensor | None = None) -> torch.Tensor:
+    """``dx (+)= d_logits @ router_w^T`` (VJP of ``moe.py:178`` w.r.t. x), f32 ``[T, D]``."""
+    _check(d_logits, "d_logits", 2)
+    _check(router_w, "router_w", 2)
+    T, N = d_logits.shape
+    D = router_w.shape[0]
+    acc = dx is not None
+    if dx is None:
+        dx = torch.empty((T, D), dtype=torch.float32, device=d_logits.device)
+    elif dx.dtype != torch.float32 or tuple(dx.shape) != (T, D):
+        raise ValueError("router_dx: dx must be float32 [T, D]")
+    call("hmoe_router_dx", _ptr(d_logits), _ptr(router_w), _dtype_code(router_w), T, D, N,
+         _ptr(dx), 1 if acc else 0, _stream())
+    return dx

@@ -207,8 +207,9 @@ int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale, const int32_
 
 /* out[t] = sum_k bf16(gates[t,k]) * ys[slot_pos[t*K+k]] (+ residual[t]),
  * float32 accumulation over k ascending, dropped slots skipped.
- * ys [rows, D] (BF16/F32); residual [T,D] (F32/BF16) or NULL: the shared
- * expert's output, added last (moe.py:249-251); out [T,D] (F32/BF16). */
+ * ys [rows, D] (BF16/F32); gates [T,K] f32, or NULL for unit weights;
+ * residual [T,D] (F32/BF16) or NULL: the shared expert's output, added last
+ * (moe.py:249-251); out [T,D] (F32/BF16). */
 int hmoe_combine(const void* ys, int ys_dtype, const int32_t* slot_pos,
                  const float* gates, const void* residual, int residual_dtype,
                  int64_t tokens, int top_k, int d_model, void* out, int out_dtype,
@@ -225,6 +226,85 @@ size_t hmoe_aux_workspace_bytes(int batch, int seq, int n_experts);
 int hmoe_router_aux(const float* logits, const int32_t* top_idx, int batch, int seq,
                     int n_experts, int top_k, float* losses, float* expert_counts,
                     void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
+
+/* ---- backward, data gradients: the VJP that jax.value_and_grad
+ *      (train.py:266) takes of MoE.__call__ (moe.py:170-246).  Routing
+ *      decisions (top-k, drops, the plan) are held fixed: integer valued.
+ *      Weight gradients of the expert GEMMs are not built yet. ----------- */
+
+/* VJP of the weighted combine (moe.py:80-85) for dy = d out [T,D] f32:
+ * d_ys[slot_pos[t*K+k]] = bf16(dy[t] * bf16(gates[t,k])) (float32 product)
+ * for kept slots (other rows of d_ys are not written), d_gates[t,k] =
+ * bf16(f32(sum_d dy[t,d] * ys[pos,d])) with the sum in float64, 0 for dropped
+ * slots.  ys and d_ys [rows, D] bf16, d_gates [T,K] f32.  D % 8 == 0,
+ * K <= 16. */
+int hmoe_combine_bwd(const float* dy, const void* ys, const int32_t* slot_pos,
+                     const float* gates, int64_t tokens, int top_k, int d_model, void* d_ys,
+                     float* d_gates, hmoe_stream_t stream);
+
+/* Recomputes the gate/up GEMM outputs g and u (moe.py:70-71) on the
+ * dispatched rows of x, as bf16 [rows_cap, 2F] in the packed operand's
+ * column order (blocks of 32 gate columns, then the 32 up columns of the
+ * same h columns), no SwiGLU.  Same operands and limits as
+ * hmoe_grouped_gate_up_gather. */
+int hmoe_grouped_gate_up_raw_gather(const void* x, int64_t tokens, int top_k,
+                                    const int32_t* perm_src, const int32_t* offsets,
+                                    int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                    const void* w_gate_up_packed, void* gu,
+                                    hmoe_stream_t stream);
+
+/* VJP of h = silu(g) * u (moe.py:72): dg = dh * u * silu'(g), du = dh *
+ * silu(g), float32 arithmetic, one bf16 rounding each.  dh [rows, F], gu and
+ * dgu [rows, 2F] bf16 in the column order of hmoe_grouped_gate_up_raw_gather.
+ * Rows at or past offsets[n_experts] are not touched (offsets may be NULL:
+ * all rows).  F % 32 == 0. */
+int hmoe_swiglu_bwd(const void* dh, const void* gu, const int32_t* offsets, int n_experts,
+                    int64_t rows, int d_ff, void* dgu, hmoe_stream_t stream);
+
+/* Backward operands of the expert GEMMs, packed once from the fp32/bf16
+ * masters: w_down [N,F,D] -> bf16 [N,F,D] (rows = h columns, D contiguous);
+ * w_gate, w_up [N,D,F] -> bf16 [N,D,2F] (rows = d, columns in the gate/up
+ * column order). */
+int hmoe_pack_down_dgrad(const void* w_down, int w_dtype, int n_experts, int d_ff,
+                         int d_model, void* packed, hmoe_stream_t stream);
+int hmoe_pack_gate_up_dgrad(const void* w_gate, const void* w_up, int w_dtype, int n_experts,
+                            int d_model, int d_ff, void* packed, hmoe_stream_t stream);
+
+/* dh = bf16(d_ys Wd[e]^T) per expert segment (the VJP of moe.py:73 with
+ * respect to h): d_ys [rows_cap, D], dh [rows_cap, F] bf16, w_down_dgrad
+ * from hmoe_pack_down_dgrad.  D % 64 == 0, F % 256 == 0. */
+int hmoe_grouped_dgrad_down(const void* d_ys, const int32_t* offsets, int n_experts,
+                            int64_t rows_cap, int d_model, int d_ff, const void* w_down_dgrad,
+                            void* dh, hmoe_stream_t stream);
+
+/* d_xs = bf16(dg Wg[e]^T + du Wu[e]^T) per expert segment, one float32
+ * accumulation over the 2F columns (the VJP of moe.py:70-71 with respect to
+ * xs): dgu [rows_cap, 2F] (hmoe_swiglu_bwd), d_xs [rows_cap, D] bf16,
+ * w_gate_up_dgrad from hmoe_pack_gate_up_dgrad.  F % 32 == 0, D % 256 == 0. */
+int hmoe_grouped_dgrad_gate_up(const void* dgu, const int32_t* offsets, int n_experts,
+                               int64_t rows_cap, int d_model, int d_ff,
+                               const void* w_gate_up_dgrad, void* d_xs, hmoe_stream_t stream);
+
+/* VJP of the row gather (moe.py:56): dx[t] = sum_k d_xs[slot_pos[t*K+k]]
+ * over kept slots, float32, k ascending (hmoe_combine with unit weights). */
+int hmoe_gather_bwd(const void* d_xs, int d_xs_dtype, const int32_t* slot_pos, int64_t tokens,
+                    int top_k, int d_model, void* dx, int dx_dtype, hmoe_stream_t stream);
+
+/* VJP of the gates with respect to the logits (moe.py:179-192; mode as in
+ * hmoe_router): d_logits [T,N] f32, zero off the selected experts.
+ * HMOE_ROUTE_SOFTMAX: dl_k = g_k (dg_k - sum_j g_j dg_j) (needs gates);
+ * HMOE_ROUTE_SIGMOID_BIAS: with s = sigmoid(l), Z = sum_j s_j + 1e-9,
+ * dl_k = rsf (dg_k/Z - sum_j dg_j s_j/Z^2) s_k (1 - s_k) (needs logits).
+ * Sums over k in float32, k ascending. */
+int hmoe_router_bwd(const float* logits, const int32_t* top_idx, const float* gates,
+                    const float* d_gates, int64_t tokens, int n_experts, int top_k, int mode,
+                    float routed_scaling_factor, float* d_logits, hmoe_stream_t stream);
+
+/* dx [T,D] f32 (+)= d_logits [T,N] @ router_w^T (router_w [D,N] F32/BF16):
+ * the VJP of l = f32(x) @ router (moe.py:175,178) with respect to x.
+ * accumulate != 0 adds into dx.  D % 64 == 0. */
+int hmoe_router_dx(const float* d_logits, const void* router_w, int w_dtype, int64_t tokens,
+                   int d_model, int n_experts, float* dx, int accumulate, hmoe_stream_t stream);
 
 #ifdef __cplusplus
 }

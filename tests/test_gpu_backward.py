@@ -1,0 +1,248 @@
+"""Parity of the HIP backward (data gradients) against the backward oracle
+(needs an MI355X).
+
+The combine VJP's bf16 cotangent rows and the gather VJP are compared bit for
+bit (their rounding points are fixed: one float32 product, one bf16
+rounding; float32 sums over k ascending).  Values that come out of a dot
+product and are then rounded to bf16 (d_gates) may sit on a bf16 rounding
+boundary that a different float64 summation order crosses: at most one bf16
+ulp apart, and nearly all equal.  The GEMMs are compared with float64 on the
+same bf16 operands (normwise 1e-2: bf16 output rounding is 2^-9 relative);
+elementwise float32 arithmetic (SwiGLU VJP, router VJP) against the float64
+oracle to the stated tolerances.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import moe_backward as B
+from hanuman_amd import _lib
+from hanuman_amd import kernels as K
+from hanuman_amd.backward import BackwardOperands, moe_backward_data
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_f32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def dev_bf16(a, dev):
+    return dev_f32(a, dev).to(torch.bfloat16)
+
+
+def host(t):
+    return t.float().cpu().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+
+def bf16_ulps(a, b):
+    """Distance in bf16 ulps between bf16-valued float32 arrays (-0 == +0)."""
+    def key(v):
+        i = (np.ascontiguousarray(v, np.float32).view(np.int32) >> 16).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFF), i)
+    return np.abs(key(a) - key(b))
+
+
+def plan_on(gpu, rng, T, N, Kk, cf):
+    logits = rng.standard_normal((T, N)).astype(np.float32)
+    idx = O.topk_desc(logits, Kk)
+    cap = O.capacity_of(T, Kk, N, cf)
+    plan = K.dispatch_plan(torch.from_numpy(idx).to(gpu), N, cap)
+    return idx, plan, O.dispatch_plan(idx, N, cap)
+
+
+@pytest.mark.parametrize("T,D,N,Kk,cf", [(1000, 256, 8, 4, 1.0), (513, 2048, 64, 8, 1.25),
+                                         (64, 64, 4, 1, None)])
+def test_combine_bwd(gpu, T, D, N, Kk, cf):
+    rng = np.random.default_rng(T + D)
+    idx, plan, ref_plan = plan_on(gpu, rng, T, N, Kk, cf)
+    R = plan.rows_cap
+    ys = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
+    gates = rng.uniform(0.0, 1.0, (T, Kk)).astype(np.float32)
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    d_ys, d_g = K.combine_bwd(dev_f32(dy, gpu), dev_bf16(ys, gpu), plan, dev_f32(gates, gpu))
+    torch.cuda.synchronize()
+    r_ys, r_g = B.combine_bwd(dy, ys, ref_plan["slot_pos"], gates, T, Kk, "bf16")
+    kept = int(ref_plan["offsets"][-1])
+    got = host(d_ys)[:kept]
+    assert np.array_equal(got.view(np.uint32), r_ys[:kept].view(np.uint32)), "d_ys rows"
+    g = host(d_g)
+    dropped = ref_plan["slot_pos"].reshape(T, Kk) < 0
+    assert np.all(g[dropped] == 0.0)
+    ulps = bf16_ulps(g, r_g)
+    assert ulps.max() <= 1 and (ulps > 0).mean() < 0.01, (ulps.max(), (ulps > 0).mean())
+
+
+@pytest.mark.parametrize("rows,F,kept", [(300, 256, 250), (1024, 1024, 1024), (96, 32, 70)])
+def test_swiglu_bwd(gpu, rows, F, kept):
+    rng = np.random.default_rng(rows + F)
+    dh = O.bf16_round((rng.standard_normal((rows, F)) * 0.5).astype(np.float32))
+    gu = O.bf16_round((rng.standard_normal((rows, 2 * F)) * 2.0).astype(np.float32))
+    offsets = torch.tensor([0, kept // 2, kept], dtype=torch.int32, device=gpu)
+    dgu = host(K.swiglu_bwd(dev_bf16(dh, gpu), dev_bf16(gu, gpu), offsets))
+    col = np.arange(F)
+    gc = (col // 32) * 64 + col % 32
+    g, u = gu[:, gc], gu[:, gc + 32]
+    rdg, rdu = B.swiglu_bwd(dh, g, u, "bf16")
+    for name, got, ref in (("dg", dgu[:kept, gc], rdg[:kept]), ("du", dgu[:kept, gc + 32], rdu[:kept])):
+        scale = np.abs(ref).max()
+        err = np.abs(got - ref)
+        assert np.all(err <= 2 ** -7 * np.abs(ref) + 1e-6 * scale), name
+
+
+def expert_problem(gpu, rng, T, D, N, Kk, F, cf):
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    w = (0.02 * rng.standard_normal((D, N))).astype(np.float32)
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+    logits = O.router_logits(x, w)
+    idx, gates = O.route_softmax(logits, Kk)
+    cap = O.capacity_of(T, Kk, N, cf)
+    ref_plan = O.dispatch_plan(idx, N, cap)
+    plan = K.dispatch_plan(torch.from_numpy(idx).to(gpu), N, cap)
+    return x, w, wg, wu, wd, logits, idx, gates, ref_plan, plan
+
+
+@pytest.mark.parametrize("T,D,N,Kk,F", [(512, 512, 8, 2, 256), (777, 192, 16, 4, 128)])
+def test_gate_up_raw_gather(gpu, T, D, N, Kk, F):
+    rng = np.random.default_rng(T)
+    x, w, wg, wu, wd, logits, idx, gates, ref_plan, plan = expert_problem(gpu, rng, T, D, N, Kk, F, 1.25)
+    xd = dev_bf16(x, gpu)
+    wgu = K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    gu = host(K.grouped_gate_up_raw_gather(xd, plan, wgu))
+    h = host(K.grouped_gate_up_gather(xd, plan, wgu))
+    torch.cuda.synchronize()
+    kept = int(ref_plan["offsets"][-1])
+    xs = O.permute_rows(x, ref_plan["perm_src"], Kk).astype(np.float64)
+    col = np.arange(F)
+    gc = (col // 32) * 64 + col % 32
+    off = ref_plan["offsets"]
+    for e in range(N):
+        a, b = off[e], off[e + 1]
+        if b <= a:
+            continue
+        g = xs[a:b] @ O.bf16_round(wg[e]).astype(np.float64)
+        u = xs[a:b] @ O.bf16_round(wu[e]).astype(np.float64)
+        assert O.normwise_rel_err(gu[a:b, gc], g) < 1e-2
+        assert O.normwise_rel_err(gu[a:b, gc + 32], u) < 1e-2
+    # the SwiGLU of the recomputed g, u is the forward's h, which is formed
+    # from the float32 accumulators (g and u unrounded): within 2 bf16 ulps
+    g16, u16 = gu[:kept, gc], gu[:kept, gc + 32]
+    h_re = O.bf16_round((O.silu(g16.astype(np.float64)) * u16).astype(np.float32))
+    assert bf16_ulps(h_re, h[:kept]).max() <= 2
+
+
+@pytest.mark.parametrize("T,D,N,Kk,F", [(512, 512, 8, 2, 256), (600, 256, 4, 3, 96)])
+def test_dgrad_gemms(gpu, T, D, N, Kk, F):
+    rng = np.random.default_rng(T + 7)
+    x, w, wg, wu, wd, logits, idx, gates, ref_plan, plan = expert_problem(gpu, rng, T, D, N, Kk, F, 1.25)
+    R = plan.rows_cap
+    off = ref_plan["offsets"]
+    ops = BackwardOperands(dev_f32(wg, gpu), dev_f32(wu, gpu), dev_f32(wd, gpu))
+    if F % 256 == 0:
+        d_ys = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
+        dh = host(K.grouped_dgrad_down(dev_bf16(d_ys, gpu), plan.offsets, ops.w_down_dgrad))
+        for e in range(N):
+            a, b = off[e], off[e + 1]
+            if b > a:
+                ref = d_ys[a:b].astype(np.float64) @ O.bf16_round(wd[e]).astype(np.float64).T
+                assert O.normwise_rel_err(dh[a:b], ref) < 1e-2, e
+    dgu = O.bf16_round(rng.standard_normal((R, 2 * F)).astype(np.float32))
+    d_xs = host(K.grouped_dgrad_gate_up(dev_bf16(dgu, gpu), plan.offsets, ops.w_gate_up_dgrad))
+    col = np.arange(F)
+    gc = (col // 32) * 64 + col % 32
+    for e in range(N):
+        a, b = off[e], off[e + 1]
+        if b > a:
+            ref = (dgu[a:b, gc].astype(np.float64) @ O.bf16_round(wg[e]).astype(np.float64).T
+                   + dgu[a:b, gc + 32].astype(np.float64) @ O.bf16_round(wu[e]).astype(np.float64).T)
+            assert O.normwise_rel_err(d_xs[a:b], ref) < 1e-2, e
+
+
+@pytest.mark.parametrize("T,D,N,Kk,cf", [(1000, 256, 8, 4, 1.0), (300, 2048, 64, 8, 1.25)])
+def test_gather_bwd_bit_exact(gpu, T, D, N, Kk, cf):
+    rng = np.random.default_rng(T + 3)
+    idx, plan, ref_plan = plan_on(gpu, rng, T, N, Kk, cf)
+    d_xs = O.bf16_round(rng.standard_normal((plan.rows_cap, D)).astype(np.float32))
+    dx = host(K.gather_bwd(dev_bf16(d_xs, gpu), plan))
+    ref = B.gather_bwd(d_xs, ref_plan["slot_pos"], T, Kk, "bf16")
+    assert np.array_equal(dx.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("T,N,Kk", [(1000, 64, 8), (257, 200, 6), (64, 8, 2)])
+def test_router_bwd(gpu, mode, T, N, Kk):
+    rng = np.random.default_rng(T + N)
+    logits = rng.standard_normal((T, N)).astype(np.float32)
+    dg = rng.standard_normal((T, Kk)).astype(np.float32)
+    if mode == "softmax":
+        idx, gates = O.route_softmax(logits, Kk)
+        ref = B.route_softmax_bwd(logits, idx, gates, dg)
+        m, rsf = _lib.ROUTE_SOFTMAX, 1.0
+    else:
+        idx, gates, _ = O.route_sigmoid(logits, None, Kk, 2.5)
+        ref = B.route_sigmoid_bwd(logits, idx, dg, 2.5)
+        m, rsf = _lib.ROUTE_SIGMOID_BIAS, 2.5
+    dl = host(K.router_bwd(dev_f32(logits, gpu), torch.from_numpy(idx).to(gpu),
+                           dev_f32(gates, gpu), dev_f32(dg, gpu), N, m, rsf))
+    unsel = np.ones((T, N), bool)
+    np.put_along_axis(unsel, idx, False, axis=1)
+    assert np.all(dl[unsel] == 0.0)
+    np.testing.assert_allclose(dl, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("w_dtype", ["f32", "bf16"])
+def test_router_dx(gpu, w_dtype):
+    rng = np.random.default_rng(11)
+    T, D, N = 777, 512, 72
+    dl = rng.standard_normal((T, N)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((D, N))).astype(np.float32)
+    if w_dtype == "bf16":
+        w = O.bf16_round(w)
+        wd = dev_bf16(w, gpu)
+    else:
+        wd = dev_f32(w, gpu)
+    base = rng.standard_normal((T, D)).astype(np.float32)
+    ref = dl.astype(np.float64) @ w.astype(np.float64).T
+    dx = host(K.router_dx(dev_f32(dl, gpu), wd))
+    np.testing.assert_allclose(dx, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+    acc = host(K.router_dx(dev_f32(dl, gpu), wd, dev_f32(base, gpu)))
+    np.testing.assert_allclose(acc, base + ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("T,D,N,Kk,F,cf", [(512, 512, 16, 4, 256, 1.25), (384, 256, 8, 2, 256, 0.9)])
+def test_layer_backward_matches_oracle(gpu, T, D, N, Kk, F, cf):
+    """The composed data-gradient pass against the oracle's bf16-mode VJP,
+    fed with the GPU forward's own intermediates."""
+    rng = np.random.default_rng(T * 3 + N)
+    x, w, wg, wu, wd, logits, idx, gates, ref_plan, plan = expert_problem(gpu, rng, T, D, N, Kk, F, cf)
+    print(f"layer backward T={T} D={D} N={N} K={Kk} F={F} cf={cf}", flush=True)
+    xd = dev_bf16(x, gpu)
+    wdv = dev_f32(w, gpu)
+    lg, top_idx, g = K.router(xd, wdv, None, Kk, _lib.ROUTE_SOFTMAX)
+    plan = K.dispatch_plan(top_idx, N, O.capacity_of(T, Kk, N, cf))
+    wgu = K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    h = K.grouped_gate_up_gather(xd, plan, wgu)
+    ys = K.grouped_down(h, plan.offsets, K.pack_down(dev_f32(wd, gpu)))
+    ops = BackwardOperands(dev_f32(wg, gpu), dev_f32(wu, gpu), dev_f32(wd, gpu))
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    fwd = {"logits": lg, "top_idx": top_idx, "gates": g, "plan": plan, "ys": ys}
+    res = moe_backward_data(xd, wdv, fwd, wgu, ops, dev_f32(dy, gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(top_idx), idx)
+    ref_fwd = {"logits": host(lg), "top_idx": idx, "gates": host(g), "plan": ref_plan,
+               "xs": O.permute_rows(x, ref_plan["perm_src"], Kk), "ys": host(ys)}
+    params = {"router": w, "expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd}
+    ref = B.moe_backward(x, params, dy, ref_fwd, routing="softmax", precision="bf16")
+    kept = int(ref_plan["offsets"][-1])
+    assert np.array_equal(host(res["d_ys"])[:kept].view(np.uint32),
+                          ref["d_ys"][:kept].view(np.uint32)), "d_ys"
+    ulps = bf16_ulps(host(res["d_gates"]), ref["d_gates"])
+    assert ulps.max() <= 1, "d_gates"
+    for name, got, want in (("d_xs", host(res["d_xs"])[:kept], ref["d_xs"][:kept]),
+                            ("dx", host(res["dx"]), ref["dx"]),
+                            ("d_logits", host(res["d_logits"]), ref["d_logits"])):
+        err = O.normwise_rel_err(np.asarray(got, np.float64), np.asarray(want, np.float64))
+        print(f"  {name}: normwise {err:.2e}", flush=True)
+        assert err < 2e-2, (name, err)
