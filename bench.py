@@ -16,7 +16,13 @@ input resident in HBM before the timed region.  One JSON line on stdout:
              this host's cores on up to 16384 tokens of the same workload (all of
              the headline workload)
 
-Usage: python bench.py [--steps K] [--warmup W] [--spinup-ms MS] [--workload NAME] [--no-cpu-baseline]
+With --backward the line is the data-gradient backward pass instead (bf16
+SwiGLU workloads): combine VJP, g/u recompute, both data-gradient GEMMs,
+SwiGLU VJP, gather VJP and router VJP, timed per stage the same way, for the
+cotangent of the layer output; the forward's intermediates are computed once
+before the timed region.
+
+Usage: python bench.py [--steps K] [--warmup W] [--spinup-ms MS] [--workload NAME] [--no-cpu-baseline] [--backward]
 """
 from __future__ import annotations
 
@@ -131,6 +137,8 @@ def main():
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384,
                     help="tokens of the CPU-baseline sample (capped at the workload's; the "
                          "default is the whole headline workload, ~10 s of CPU work)")
+    ap.add_argument("--backward", action="store_true",
+                    help="time the data-gradient backward pass instead of the forward")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the warm-up, as the "
                          "known-size reference for HBM byte counters")
@@ -159,6 +167,9 @@ def main():
     torch.cuda.synchronize()
 
     fp8 = wl.expert_dtype == "fp8"
+    if args.backward:
+        bench_backward(args, name, wl, layer)
+        return
     # bf16 SwiGLU experts: the row permutation is done by the gate/up GEMM's
     # own loads (no dispatched copy of x), so there is no separate stage.
     fused = layer.fused_dispatch
@@ -328,6 +339,123 @@ def main():
                      "dispatch_identity workload)") if fused else "hmoe_permute_rows",
         "grouped_gemm_mfma_util": grouped_gemm["frac"] if grouped_gemm else None,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_backward(args, name, wl, layer):
+    """Times the data-gradient backward (hanuman_amd.backward) on `wl`."""
+    import torch
+    import hanuman_amd.kernels as K
+    from hanuman_amd import _lib
+    from hanuman_amd.backward import BackwardOperands
+    from hanuman_amd import workloads as W
+
+    if not layer.fused_dispatch:
+        raise SystemExit("--backward needs a bf16 SwiGLU workload with bf16 tokens")
+    inp = W.make_inputs(wl, seed=args.seed)
+    dev = layer.device
+    ops = BackwardOperands(torch.from_numpy(inp.w_gate).to(dev), torch.from_numpy(inp.w_up).to(dev),
+                           torch.from_numpy(inp.w_down).to(dev))
+    dy = torch.from_numpy(
+        np.random.default_rng(args.seed + 1).standard_normal((wl.tokens, wl.d_model), dtype=np.float32)).to(dev)
+    del inp
+    fwd = layer.forward()
+    torch.cuda.synchronize()
+    plan = fwd["plan"]
+    N = wl.n_experts
+    # with router logits given (no router weight) the VJP ends at d_logits
+    stages = ["combine_bwd", "gate_up_recompute", "dgrad_down", "swiglu_bwd", "dgrad_gate_up",
+              "gather_bwd", "router_bwd"] + (["router_dx"] if layer.router_w is not None else [])
+
+    def step(ev=None):
+        marks = iter(ev) if ev is not None else None
+
+        def mark():
+            if marks is not None:
+                next(marks).record()
+
+        mark()
+        d_ys, d_g = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"])
+        mark()
+        gu = K.grouped_gate_up_raw_gather(layer.x, plan, layer.w_gate_up)
+        mark()
+        dh = K.grouped_dgrad_down(d_ys, plan.offsets, ops.w_down_dgrad)
+        mark()
+        dgu = K.swiglu_bwd(dh, gu, plan.offsets)
+        mark()
+        d_xs = K.grouped_dgrad_gate_up(dgu, plan.offsets, ops.w_gate_up_dgrad)
+        mark()
+        dx = K.gather_bwd(d_xs, plan)
+        mark()
+        dl = K.router_bwd(fwd["logits"], fwd["top_idx"], fwd["gates"], d_g, N, layer.mode)
+        mark()
+        if layer.router_w is not None:
+            K.router_dx(dl, layer.router_w, dx)
+            mark()
+        return dx
+
+    t_warm = time.perf_counter()
+    warm_steps = 0
+    while warm_steps < args.warmup or (time.perf_counter() - t_warm) * 1e3 < args.spinup_ms:
+        step()
+        warm_steps += 1
+        if warm_steps % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+           for _ in range(args.steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for s_ in range(args.steps):
+        step(evs[s_])
+    t1.record()
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    stage_ms = {st: float(np.mean([evs[s_][j].elapsed_time(evs[s_][j + 1])
+                                   for s_ in range(args.steps)])) for j, st in enumerate(stages)}
+    T, D, F, K_ = wl.tokens, wl.d_model, wl.d_ff, wl.top_k
+    R = T * K_
+    kept = int(plan.offsets[-1].item())
+    w_b = 2 if wl.router_w_dtype == "bf16" else 4
+    work = {
+        "combine_bwd": ("hbm", T * D * 4 + 2 * kept * D * 2 + R * 8, HBM_PEAK_GBS),
+        "gate_up_recompute": ("mfma", 4 * kept * D * F, BF16_PEAK_TFLOPS),
+        "dgrad_down": ("mfma", 2 * kept * D * F, BF16_PEAK_TFLOPS),
+        "swiglu_bwd": ("hbm", kept * (F * 2 + 2 * F * 2 * 2), HBM_PEAK_GBS),
+        "dgrad_gate_up": ("mfma", 4 * kept * D * F, BF16_PEAK_TFLOPS),
+        "gather_bwd": ("hbm", kept * D * 2 + T * D * 4 + R * 4, HBM_PEAK_GBS),
+        "router_bwd": ("hbm", T * N * 4 * 2 + T * K_ * 12, HBM_PEAK_GBS),
+        "router_dx": ("hbm", T * N * 4 + D * N * w_b + 2 * T * D * 4, HBM_PEAK_GBS),
+    }
+    kernels = {}
+    for st in stages:
+        kind, amount, peak = work[st]
+        t = stage_ms[st] / 1e3
+        ach = amount / t / (1e9 if kind == "hbm" else 1e12)
+        kernels[st] = {"ms": round(stage_ms[st], 4), "bound": kind, "achieved": round(ach, 1),
+                       "unit": "GB/s" if kind == "hbm" else "TFLOP/s", "peak": peak,
+                       "frac": round(ach / peak, 4), ("bytes" if kind == "hbm" else "flop"): amount}
+    dom = "dgrad_gate_up"
+    roofline = {"kernel": "grouped_gemm_regs<false, false, false> (dgrad gate/up)", "bound": "mfma",
+                "achieved": kernels[dom]["achieved"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": kernels[dom]["frac"], "traffic": None, "flop_per_launch": work[dom][1],
+                "ms": kernels[dom]["ms"]}
+    log(f"[bench] backward {ms_per_step:.4f} ms/step, {T / ms_per_step / 1e3:.3f} M tokens/s; stages "
+        + ", ".join(f"{k} {v:.4f}" for k, v in stage_ms.items()))
+    line = {
+        "metric": "MoE layer backward (data gradients) tokens/s (1 GPU)",
+        "value": round(T / (ms_per_step / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "warmup_steps_run": warm_steps,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded normal inputs, weights and output cotangent)",
+        "config": {"workload": name + " backward (data gradients)", "tokens": T, "d_model": D,
+                   "n_experts": N, "top_k": K_, "d_ff": F, "capacity_factor": wl.capacity_factor,
+                   "kept_rows": kept, "parallelism": "single GPU, all experts resident"},
+        "roofline": roofline, "kernels": kernels, "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
 

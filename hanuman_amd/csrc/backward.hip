@@ -46,30 +46,49 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
   }
   const int chunks = d_model / 8;
   const float* dy_row = dy + t * d_model;
-  for (int c = lane; c < chunks; c += 64) {
-    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy_row + c * 8));
-    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy_row + c * 8 + 4));
-    const float d[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-    u32x4 yv[KMAX];
+  // Two chunks per lane per iteration: 2 (K + 2) loads in flight.
+  constexpr int kU = KMAX <= 8 ? 2 : 1;
+  for (int c0 = lane; c0 < chunks; c0 += 64 * kU) {
+    float d[kU][8];
+    u32x4 yv[kU][KMAX];
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k)
-      if (k < top_k && pos[k] >= 0)
-        yv[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            ys + static_cast<int64_t>(pos[k]) * d_model + c * 8));
+    for (int u = 0; u < kU; ++u) {
+      const int c = c0 + 64 * u;
+      if (c < chunks) {
+        const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy_row + c * 8));
+        const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy_row + c * 8 + 4));
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-      if (k < top_k && pos[k] >= 0) {
-        u32x4 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          o[q] = pack_bf16x2(d[2 * q] * g[k], d[2 * q + 1] * g[k]);
-          const uint32_t w = yv[k][q];
-          part[k] += static_cast<double>(d[2 * q]) * static_cast<double>(__uint_as_float(w << 16));
-          part[k] += static_cast<double>(d[2 * q + 1]) *
-                     static_cast<double>(__uint_as_float(w & 0xffff0000u));
+        for (int i = 0; i < 4; ++i) {
+          d[u][i] = a[i];
+          d[u][4 + i] = b[i];
         }
-        __builtin_nontemporal_store(
-            o, reinterpret_cast<u32x4*>(d_ys + static_cast<int64_t>(pos[k]) * d_model + c * 8));
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k)
+          if (k < top_k && pos[k] >= 0)
+            yv[u][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                ys + static_cast<int64_t>(pos[k]) * d_model + c * 8));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int c = c0 + 64 * u;
+      if (c >= chunks) break;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k < top_k && pos[k] >= 0) {
+          u32x4 o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            o[q] = pack_bf16x2(d[u][2 * q] * g[k], d[u][2 * q + 1] * g[k]);
+            const uint32_t w = yv[u][k][q];
+            part[k] += static_cast<double>(d[u][2 * q]) *
+                       static_cast<double>(__uint_as_float(w << 16));
+            part[k] += static_cast<double>(d[u][2 * q + 1]) *
+                       static_cast<double>(__uint_as_float(w & 0xffff0000u));
+          }
+          __builtin_nontemporal_store(
+              o, reinterpret_cast<u32x4*>(d_ys + static_cast<int64_t>(pos[k]) * d_model + c * 8));
+        }
       }
     }
   }
@@ -179,30 +198,33 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
 }
 
 // dx[t, d] (+)= sum_n d_logits[t, n] * W[d, n]  (the VJP of x_f @ router,
-// moe.py:178, with respect to x).  Workgroup tile: 32 tokens x 64 columns;
-// thread (tt, dg) = (tid / 8, tid % 8) owns token tt, columns dg*8 .. +8.
-// n runs in chunks of 32 through LDS (W transposed there), ascending.
+// moe.py:178, with respect to x).  Workgroup tile: 128 tokens x 64 columns;
+// thread (tg, dg) = (tid / 8, tid % 8) owns tokens tg*4 .. +4 and columns
+// dg*8 .. +8 (32 accumulators).  n runs in chunks of 32 through LDS, both
+// operands stored n-major there, ascending.
 template <typename TW>
 __global__ __launch_bounds__(256) void router_dx_kernel(const float* __restrict__ d_logits,
                                                         const TW* __restrict__ w, int64_t tokens,
                                                         int d_model, int n_experts,
                                                         float* __restrict__ dx, int accumulate) {
 #pragma clang fp contract(off)
-  __shared__ float sdl[32][33];
+  __shared__ __attribute__((aligned(16))) float sdl[32][128];
   __shared__ __attribute__((aligned(16))) float sw[32][64];
   const int tid = threadIdx.x;
-  const int tt = tid >> 3, dg = tid & 7;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int tg = tid >> 3, dg = tid & 7;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 128;
   const int d0 = blockIdx.y * 64;
-  float acc[8];
+  float acc[4][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[a][i] = 0.0f;
   for (int n0 = 0; n0 < n_experts; n0 += 32) {
     __syncthreads();
-    for (int i = tid; i < 32 * 32; i += 256) {
+    for (int i = tid; i < 128 * 32; i += 256) {
       const int r = i >> 5, c = i & 31;
       const int64_t t = t0 + r;
-      sdl[r][c] = (t < tokens && n0 + c < n_experts) ? d_logits[t * n_experts + n0 + c] : 0.0f;
+      sdl[c][r] = (t < tokens && n0 + c < n_experts) ? d_logits[t * n_experts + n0 + c] : 0.0f;
     }
     for (int i = tid; i < 64 * 32; i += 256) {
       const int dd = i >> 5, c = i & 31;
@@ -217,28 +239,34 @@ __global__ __launch_bounds__(256) void router_dx_kernel(const float* __restrict_
     __syncthreads();
     const int nn = n_experts - n0 < 32 ? n_experts - n0 : 32;
     for (int c = 0; c < nn; ++c) {
-      const float a = sdl[tt][c];
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&sdl[c][tg * 4]);
       const f32x4 w0 = *reinterpret_cast<const f32x4*>(&sw[c][dg * 8]);
       const f32x4 w1 = *reinterpret_cast<const f32x4*>(&sw[c][dg * 8 + 4]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[i] = acc[i] + a * w0[i];
-        acc[4 + i] = acc[4 + i] + a * w1[i];
-      }
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[r][i] = acc[r][i] + a[r] * w0[i];
+          acc[r][4 + i] = acc[r][4 + i] + a[r] * w1[i];
+        }
     }
   }
-  const int64_t t = t0 + tt;
-  if (t >= tokens) return;
-  float* o = dx + t * d_model + d0 + dg * 8;
-  f32x4 r0 = {acc[0], acc[1], acc[2], acc[3]}, r1 = {acc[4], acc[5], acc[6], acc[7]};
-  if (accumulate) {
-    const f32x4 p0 = *reinterpret_cast<const f32x4*>(o);
-    const f32x4 p1 = *reinterpret_cast<const f32x4*>(o + 4);
-    r0 = p0 + r0;
-    r1 = p1 + r1;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t t = t0 + tg * 4 + r;
+    if (t >= tokens) break;
+    float* o = dx + t * d_model + d0 + dg * 8;
+    f32x4 r0 = {acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
+    f32x4 r1 = {acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
+    if (accumulate) {
+      const f32x4 p0 = *reinterpret_cast<const f32x4*>(o);
+      const f32x4 p1 = *reinterpret_cast<const f32x4*>(o + 4);
+      r0 = p0 + r0;
+      r1 = p1 + r1;
+    }
+    *reinterpret_cast<f32x4*>(o) = r0;
+    *reinterpret_cast<f32x4*>(o + 4) = r1;
   }
-  *reinterpret_cast<f32x4*>(o) = r0;
-  *reinterpret_cast<f32x4*>(o + 4) = r1;
 }
 
 }  // namespace
@@ -319,7 +347,7 @@ extern "C" int hmoe_router_dx(const float* d_logits, const void* router_w, int w
   if (tokens == 0) return HMOE_OK;
   HMOE_REQUIRE(d_logits && router_w && dx, "router_dx: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 32)), static_cast<unsigned>(d_model / 64));
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 128)), static_cast<unsigned>(d_model / 64));
   if (w_dtype == HMOE_F32)
     hipLaunchKernelGGL(router_dx_kernel<float>, grid, dim3(256), 0, s, d_logits,
                        static_cast<const float*>(router_w), tokens, d_model, n_experts, dx, accumulate);
