@@ -14,8 +14,14 @@ fixed, as JAX does for integer-valued operations:
     gates    (moe.py:179-192) d_logits           hmoe_router_bwd
     router   (moe.py:178)     dx += d_l W^T      hmoe_router_dx
 
-The expert and router weight gradients are not built yet.  Every step runs in
-the library on the current stream; there is no CPU fallback.
+and the weight gradients (:func:`moe_backward_weights`):
+
+    experts  (moe.py:70-73)   dWd = h^T d_ys,    hmoe_grouped_wgrad_down
+                              dWg|dWu = xs^T dg|du  hmoe_grouped_wgrad_gate_up
+    router   (moe.py:178)     d_router = x^T d_l hmoe_router_dw
+
+Every step runs in the library on the current stream; there is no CPU
+fallback.
 """
 from __future__ import annotations
 
@@ -59,3 +65,16 @@ def moe_backward_data(x: torch.Tensor, router_w: torch.Tensor, fwd: dict,
     K.router_dx(d_logits, router_w, dx)
     return {"dx": dx, "d_gates": d_gates, "d_logits": d_logits, "d_ys": d_ys, "gu": gu,
             "dh": dh, "dgu": dgu, "d_xs": d_xs}
+
+
+def moe_backward_weights(x: torch.Tensor, fwd: dict, data: dict) -> dict:
+    """Weight gradients of the routed layer from the forward's ``plan`` and
+    ``h`` and :func:`moe_backward_data`'s result: ``dWg``, ``dWu`` f32
+    ``[N, D, F]``, ``dWd`` f32 ``[N, F, D]``, ``d_router`` f32 ``[D, N]``
+    (the dispatched rows ``xs`` are gathered once for the gate/up gradient)."""
+    plan = fwd["plan"]
+    xs = K.permute_rows(x, plan, torch.bfloat16)
+    dwg, dwu = K.grouped_wgrad_gate_up(xs, data["dgu"], plan.offsets)
+    dwd = K.grouped_wgrad_down(fwd["h"], data["d_ys"], plan.offsets)
+    d_router = K.router_dw(x, data["d_logits"])
+    return {"dWg": dwg, "dWu": dwu, "dWd": dwd, "d_router": d_router}

@@ -269,6 +269,82 @@ __global__ __launch_bounds__(256) void router_dx_kernel(const float* __restrict_
   }
 }
 
+// d_router[d, n] = sum_t x[t, d] * d_logits[t, n] (the VJP of x_f @ router,
+// moe.py:178, with respect to the router weight), float32, in two passes for
+// a fixed summation order: pass 1 sums chunks of kRdwChunk tokens (ascending)
+// into partials [chunk][D][N]; pass 2 sums the chunks in order.  Pass 1
+// workgroup tile: 64 d x 64 n; thread (dq, nq) = (tid / 16, tid % 16) owns
+// d = 4 dq .. +4 and n = 4 nq .. +4, tokens staged 64 at a time in LDS.
+constexpr int kRdwChunk = 1024;
+
+template <typename TX>
+__global__ __launch_bounds__(256) void router_dw_partial_kernel(const TX* __restrict__ x,
+                                                                const float* __restrict__ d_logits,
+                                                                int64_t tokens, int d_model,
+                                                                int n_experts,
+                                                                float* __restrict__ partial) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float sx[64][64];
+  __shared__ __attribute__((aligned(16))) float sl[64][64];
+  const int tid = threadIdx.x;
+  const int dq = tid >> 4, nq = tid & 15;
+  const int d0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+  const int64_t c = blockIdx.z;
+  const int64_t t_begin = c * kRdwChunk;
+  const int64_t t_end = t_begin + kRdwChunk < tokens ? t_begin + kRdwChunk : tokens;
+  float acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += 64) {
+    __syncthreads();
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int r = i >> 6, cc = i & 63;
+      const int64_t t = t0 + r;
+      float vx = 0.0f, vl = 0.0f;
+      if (t < t_end) {
+        if constexpr (sizeof(TX) == 4) vx = x[t * d_model + d0 + cc];
+        else vx = bf16_bits_to_f32(x[t * d_model + d0 + cc]);
+        if (n0 + cc < n_experts) vl = d_logits[t * n_experts + n0 + cc];
+      }
+      sx[r][cc] = vx;
+      sl[r][cc] = vl;
+    }
+    __syncthreads();
+    const int nt = t_end - t0 < 64 ? static_cast<int>(t_end - t0) : 64;
+    for (int r = 0; r < nt; ++r) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&sx[r][dq * 4]);
+      const f32x4 lv = *reinterpret_cast<const f32x4*>(&sl[r][nq * 4]);
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = acc[a][b] + xv[a] * lv[b];
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int d = d0 + dq * 4 + a;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int n = n0 + nq * 4 + b;
+      if (n < n_experts) partial[(c * d_model + d) * n_experts + n] = acc[a][b];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void router_dw_sum_kernel(const float* __restrict__ partial,
+                                                            int chunks, int64_t count,
+                                                            float* __restrict__ out) {
+#pragma clang fp contract(off)
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    float v = 0.0f;
+    for (int c = 0; c < chunks; ++c) v = v + partial[c * count + i];
+    out[i] = v;
+  }
+}
+
 }  // namespace
 }  // namespace hmoe
 
@@ -356,4 +432,40 @@ extern "C" int hmoe_router_dx(const float* d_logits, const void* router_w, int w
                        static_cast<const uint16_t*>(router_w), tokens, d_model, n_experts, dx,
                        accumulate);
   return check_launch("hmoe_router_dx");
+}
+
+extern "C" size_t hmoe_router_dw_workspace_bytes(int64_t tokens, int d_model, int n_experts) {
+  if (tokens <= 0 || d_model <= 0 || n_experts <= 0) return 0;
+  return static_cast<size_t>(hmoe::ceil_div(tokens, hmoe::kRdwChunk)) * d_model * n_experts *
+         sizeof(float);
+}
+
+extern "C" int hmoe_router_dw(const void* x, int x_dtype, const float* d_logits, int64_t tokens,
+                              int d_model, int n_experts, float* d_router, void* workspace,
+                              size_t workspace_bytes, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(tokens >= 1 && n_experts >= 1, "router_dw: need tokens >= 1 and n_experts >= 1");
+  HMOE_REQUIRE(d_model >= 64 && d_model % 64 == 0,
+               "router_dw: d_model must be a multiple of 64 (got %d)", d_model);
+  HMOE_REQUIRE(x_dtype == HMOE_F32 || x_dtype == HMOE_BF16, "router_dw: x dtype must be F32 or BF16");
+  HMOE_REQUIRE(x && d_logits && d_router && workspace, "router_dw: null pointer argument");
+  const size_t need = hmoe_router_dw_workspace_bytes(tokens, d_model, n_experts);
+  HMOE_REQUIRE_CODE(workspace_bytes >= need, HMOE_ERR_WORKSPACE,
+                    "router_dw: workspace of %zu bytes, need %zu", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int chunks = static_cast<int>(ceil_div(tokens, kRdwChunk));
+  float* partial = static_cast<float*>(workspace);
+  const dim3 grid(static_cast<unsigned>(d_model / 64), static_cast<unsigned>(ceil_div(n_experts, 64)),
+                  static_cast<unsigned>(chunks));
+  if (x_dtype == HMOE_F32)
+    hipLaunchKernelGGL(router_dw_partial_kernel<float>, grid, dim3(256), 0, s,
+                       static_cast<const float*>(x), d_logits, tokens, d_model, n_experts, partial);
+  else
+    hipLaunchKernelGGL(router_dw_partial_kernel<uint16_t>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), d_logits, tokens, d_model, n_experts,
+                       partial);
+  const int64_t count = static_cast<int64_t>(d_model) * n_experts;
+  hipLaunchKernelGGL(router_dw_sum_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(count, 256), 4096))),
+                     dim3(256), 0, s, partial, chunks, count, d_router);
+  return check_launch("hmoe_router_dw");
 }

@@ -828,6 +828,237 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   }
 }
 
+// ---- weight gradients: ragged-K grouped GEMM -----------------------------------
+// C_e[m][n] = sum over the rows r of expert e's segment [offsets[e],
+// offsets[e+1]) of A[r][m] * B[r][n]: dWd[e] = h^T d_ys and dWg|dWu[e] =
+// xs^T dg|du (the VJPs of moe.py:70-73 with respect to the expert weights).
+// Both operands are row-major with the reduction index as the row, so a K
+// step stages 64 rows x 256 columns of A and of B in LDS as they lie in
+// memory ([k][col], 512-byte rows, 32-byte segment s of row k at s ^ 2(k&3))
+// and the MFMA fragments come out of LDS through the transposing read
+// ds_read_b64_tr_b16: in a group of 16 lanes, lane j receives element j % 4 of
+// the 8 bytes addressed by lanes j/4 + 4q, q = 0..3.  Lane s of group G
+// addresses row k0 + s/4, columns c0 + 16 (G % 2) + 4 (s % 4), so lane L
+// receives rows k0 .. k0+3 of column c0 + L % 32; two such reads (k0 and
+// k0 + 4, k0 = 8 (L / 32) of the sub-step) give the 8 consecutive K values of
+// the 32x32x16 operand.  Tiles: every expert (an empty one too, whose
+// gradient is zero) x (M / 256) x (N / 256), persistent as in the forward.
+// Rows past the segment read zeros: the loads are raw buffer loads whose
+// range ends at the segment's last row (the row offset is in the
+// range-checked VGPR offset), so a tile runs max(2, ceil(rows / 64)) steps,
+// rounded up to even, with no masking.  The output is float32; SPLIT: B's
+// columns are in the gate/up order (blocks of 32 gate columns, then the 32 up
+// columns of the same h columns) and C goes to out0 (gate) and out1 (up) as
+// [e][m][F].
+template <bool SPLIT>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+    const int32_t* __restrict__ offsets, int n_experts, int M, int N, float* __restrict__ out0,
+    float* __restrict__ out1) {
+  typedef GemmElem<false> E;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tm = M / kBM, tn = N / kBN;
+  const int per_e = tm * tn;
+  const int total = n_experts * per_e;
+  const int xcd = blockIdx.x % kNumXcd;
+  const int per_xcd = gridDim.x / kNumXcd;
+  const int slot = blockIdx.x / kNumXcd;
+  const int lo = static_cast<int>((static_cast<int64_t>(total) * xcd) / kNumXcd);
+  const int hi = static_cast<int>((static_cast<int64_t>(total) * (xcd + 1)) / kNumXcd);
+  const int first = lo + slot;
+  if (first >= hi) return;  // uniform per workgroup
+  const int a_row_bytes = M * 2, b_row_bytes = N * 2;
+
+  struct Tile {
+    int e, m0, n0, kpad;
+    int64_t seg0;
+    int rows;
+  };
+  auto decode = [&](int t) __attribute__((always_inline)) {
+    Tile r;
+    r.e = __builtin_amdgcn_readfirstlane(t / per_e);
+    const int l = t - r.e * per_e;
+    r.m0 = (l / tn) * kBM;
+    r.n0 = (l - (l / tn) * tn) * kBN;
+    const int s0 = __builtin_amdgcn_readfirstlane(offsets[r.e]);
+    const int s1 = __builtin_amdgcn_readfirstlane(offsets[r.e + 1]);
+    r.seg0 = s0;
+    r.rows = s1 - s0;
+    const int ks = (r.rows + 63) / 64;
+    r.kpad = ks < 2 ? 2 : ks + (ks & 1);
+    return r;
+  };
+
+  // ---- global -> registers -> LDS ------------------------------------------
+  // Round i (0..7): this thread loads 16-byte chunk ld_c of row 8i + ld_r of
+  // the A and B tiles (32 chunks per 512-byte row).
+  const int ld_r = tid >> 5;
+  const int ld_c = tid & 31;
+  auto swz = [](int k, int byte) __attribute__((always_inline)) {
+    return (((byte >> 5) ^ (2 * (k & 3))) << 5) | (byte & 31);
+  };
+  __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, 0, kBufferWord3);
+  __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, 0, kBufferWord3);
+  Tile lt = decode(first);
+  int ld_t = first, ld_kb = 0;
+  bool ld_more = true;
+  auto set_load_tile = [&](int t) __attribute__((always_inline)) {
+    lt = decode(t);
+    const uint32_t nr = static_cast<uint32_t>(lt.rows);
+    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(A + lt.seg0 * M + lt.m0), 0, static_cast<int>(nr * a_row_bytes), kBufferWord3);
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(B + lt.seg0 * N + lt.n0), 0, static_cast<int>(nr * b_row_bytes), kBufferWord3);
+  };
+  auto issue_part = [&](u32x4* ra, u32x4* rb, int p) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * p + q;
+      const int k = ld_kb * 64 + 8 * i + ld_r;
+      ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            a_rsrc, k * a_row_bytes + ld_c * 16, 0, 0));
+      rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            b_rsrc, k * b_row_bytes + ld_c * 16, 0, 0));
+    }
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (ld_more && ++ld_kb == lt.kpad) {
+      if (ld_t + per_xcd < hi) {
+        ld_t += per_xcd;
+        ld_kb = 0;
+        set_load_tile(ld_t);
+      } else {
+        ld_kb = lt.kpad - 1;
+        ld_more = false;
+      }
+    }
+  };
+  auto park_part = [&](const u32x4* ra, const u32x4* rb, int stage, int p) __attribute__((always_inline)) {
+    uint8_t* base = smem + stage * kStageBytes;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * p + q;
+      const int k = 8 * i + ld_r;
+      const int off = k * 512 + swz(k, ld_c * 16);
+      *reinterpret_cast<u32x4*>(base + off) = ra[i];
+      *reinterpret_cast<u32x4*>(base + 32768 + off) = rb[i];
+    }
+  };
+  u32x4 ra[8], rb[8];
+
+  // ---- MFMA fragments (transposing LDS reads) --------------------------------
+  const int wm = wave >> 1, wn = wave & 1;
+  const int grp = lane >> 4, j16 = lane & 15;
+  const int fr_k = 8 * (grp >> 1) + (j16 >> 2);                  // + 16 s (+ 4)
+  const int fr_c = 16 * (grp & 1) + 4 * (j16 & 3);               // + 32-column block
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  auto tr_read = [&](const uint8_t* base, int k, int col) __attribute__((always_inline)) {
+    const int off = k * 512 + swz(k, col * 2);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(
+            (__attribute__((address_space(3))) uint8_t*)(base) + off));
+  };
+  typename E::frag_t fa[2][4], fb[2][4];
+  auto read_frags = [&](int buf, int stage, int s) __attribute__((always_inline)) {
+    const uint8_t* base = smem + stage * kStageBytes;
+    const int k = 16 * s + fr_k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ca = wm * 128 + 32 * i + fr_c;
+      const int cb = wn * 128 + 32 * i + fr_c;
+      const v4i16 a0 = tr_read(base, k, ca), a1 = tr_read(base, k + 4, ca);
+      const v4i16 b0 = tr_read(base + 32768, k, cb), b1 = tr_read(base + 32768, k + 4, cb);
+      fa[buf][i] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
+      fb[buf][i] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+  f32x16 acc[4][4];
+
+  auto step = [&](auto Pc) __attribute__((always_inline)) {
+    constexpr int P = decltype(Pc)::value;
+#pragma unroll
+    for (int s = 0; s < E::kSub; ++s) {
+      park_part(ra, rb, P ^ 1, s);
+      issue_part(ra, rb, s);
+      if (s + 1 < E::kSub) read_frags((s + 1) & 1, P, s + 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    advance();
+    barrier_lds();
+  };
+
+  set_load_tile(first);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) issue_part(ra, rb, p);
+  advance();
+#pragma unroll
+  for (int p = 0; p < 4; ++p) park_part(ra, rb, 0, p);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) issue_part(ra, rb, p);
+  advance();
+  __syncthreads();
+
+  for (int t = first; t < hi; t += per_xcd) {
+    const Tile ct = decode(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    read_frags(0, 0, 0);
+    for (int kb = 0; kb < ct.kpad; kb += 2) {
+      step(IntC<0>{});
+      read_frags(0, 1, 0);
+      step(IntC<1>{});
+      if (kb + 2 < ct.kpad) read_frags(0, 0, 0);
+    }
+    // Epilogue: acc[i][j] lane L element r is C[m][n] with m = wm*128 + 32i +
+    // L%32, n = wn*128 + 32j + (r/4)*8 + (L/32)*4 + r%4 (tile-relative).
+    const int frow = lane & 31;
+    const int col_lane = (lane >> 5) * 4;
+    const int F = N / 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = ct.m0 + wm * 128 + 32 * i + frow;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = ct.n0 + wn * 128 + 32 * j + g * 8 + col_lane;
+          const f32x4 v = {acc[i][j][g * 4], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                           acc[i][j][g * 4 + 3]};
+          float* dst;
+          if (SPLIT) {
+            const int f = (n >> 6) * 32 + (n & 31);
+            dst = ((n & 63) < 32 ? out0 : out1) + (static_cast<int64_t>(ct.e) * M + m) * F + f;
+          } else {
+            dst = out0 + (static_cast<int64_t>(ct.e) * M + m) * N + n;
+          }
+          __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 // Workgroups per launch: one per CU, a multiple of the XCD count.
 int persistent_grid(hipStream_t s, int* grid, int* dev_out) {
   int dev = 0;
@@ -873,6 +1104,8 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_wgrad<false>),
+      reinterpret_cast<const void*>(grouped_gemm_wgrad<true>),
   };
   bool ok = true;
   for (const void* k : kernels) ok = ok && set_lds_limit(k, bytes);
@@ -1104,4 +1337,66 @@ extern "C" int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale,
   return launch_grouped(false, true, h_q, w_packed, h_scale, w_scales, offsets, n_experts,
                         rows_cap, d_ff, d_model, ys, d_model, static_cast<hipStream_t>(stream),
                         "hmoe_grouped_down_fp8");
+}
+
+// ---- backward weight gradients (the VJP of moe.py:70-73 w.r.t. the weights) --
+
+namespace hmoe {
+namespace {
+int launch_wgrad(bool split, const void* A, const void* B, const int32_t* offsets, int n_experts,
+                 int M, int N, float* out0, float* out1, hipStream_t s, const char* what) {
+  int dev = 0;
+  int grid = 0;
+  if (int rc = persistent_grid(s, &grid, &dev)) return rc;
+  if (int rc = allow_dynamic_lds(dev)) return rc;
+  const size_t lds = 2 * kStageBytes;
+  const uint16_t* a = static_cast<const uint16_t*>(A);
+  const uint16_t* b = static_cast<const uint16_t*>(B);
+  if (split)
+    hipLaunchKernelGGL((grouped_gemm_wgrad<true>), dim3(grid), dim3(kThreads), lds, s, a, b,
+                       offsets, n_experts, M, N, out0, out1);
+  else
+    hipLaunchKernelGGL((grouped_gemm_wgrad<false>), dim3(grid), dim3(kThreads), lds, s, a, b,
+                       offsets, n_experts, M, N, out0, out1);
+  return check_launch(what);
+}
+}  // namespace
+}  // namespace hmoe
+
+extern "C" int hmoe_grouped_wgrad_down(const void* h, const void* d_ys, const int32_t* offsets,
+                                       int n_experts, int64_t rows_cap, int d_ff, int d_model,
+                                       float* dw_down, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_wgrad_down: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
+  HMOE_REQUIRE_CODE(d_ff % kBM == 0 && d_ff > 0 && d_model % kBN == 0 && d_model > 0,
+                    HMOE_ERR_UNSUPPORTED,
+                    "grouped_wgrad_down: d_ff and d_model must be multiples of 256 (got %d, %d)",
+                    d_ff, d_model);
+  HMOE_REQUIRE(rows_cap >= 0 && rows_cap * static_cast<int64_t>(d_model) * 2 < (int64_t(1) << 31) &&
+                   rows_cap * static_cast<int64_t>(d_ff) * 2 < (int64_t(1) << 31),
+               "grouped_wgrad_down: h and d_ys must be smaller than 2 GiB");
+  HMOE_REQUIRE(h && d_ys && offsets && dw_down, "grouped_wgrad_down: null pointer argument");
+  return launch_wgrad(false, h, d_ys, offsets, n_experts, d_ff, d_model, dw_down, nullptr,
+                      static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_down");
+}
+
+extern "C" int hmoe_grouped_wgrad_gate_up(const void* xs, const void* dgu, const int32_t* offsets,
+                                          int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                          float* dw_gate, float* dw_up, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_wgrad_gate_up: n_experts must be in [1, %d] (got %d)", kMaxExperts,
+               n_experts);
+  HMOE_REQUIRE_CODE(d_model % kBM == 0 && d_model > 0 && (2 * d_ff) % kBN == 0 && d_ff > 0,
+                    HMOE_ERR_UNSUPPORTED,
+                    "grouped_wgrad_gate_up: d_model must be a multiple of 256 and d_ff of 128 "
+                    "(got %d, %d)", d_model, d_ff);
+  HMOE_REQUIRE(rows_cap >= 0 && rows_cap * static_cast<int64_t>(d_model) * 2 < (int64_t(1) << 31) &&
+                   rows_cap * static_cast<int64_t>(d_ff) * 4 < (int64_t(1) << 31),
+               "grouped_wgrad_gate_up: xs and dgu must be smaller than 2 GiB");
+  HMOE_REQUIRE(xs && dgu && offsets && dw_gate && dw_up,
+               "grouped_wgrad_gate_up: null pointer argument");
+  return launch_wgrad(true, xs, dgu, offsets, n_experts, d_model, 2 * d_ff, dw_gate, dw_up,
+                      static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_gate_up");
 }

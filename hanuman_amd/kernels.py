@@ -519,3 +519,51 @@ def router_dx(d_logits: torch.Tensor, router_w: torch.Tensor, dx: torch.Tensor |
     call("hmoe_router_dx", _ptr(d_logits), _ptr(router_w), _dtype_code(router_w), T, D, N,
          _ptr(dx), 1 if acc else 0, _stream())
     return dx
+
+
+def grouped_wgrad_down(h: torch.Tensor, d_ys: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
+    """``dWd[e] = h^T d_ys`` over each expert's segment, f32 ``[N, F, D]``."""
+    _check(h, "h", 2)
+    _check(d_ys, "d_ys", 2)
+    _check(offsets, "offsets", 1)
+    R, F = h.shape
+    D = d_ys.shape[1]
+    if h.dtype != torch.bfloat16 or d_ys.dtype != torch.bfloat16 or d_ys.shape[0] != R:
+        raise ValueError("grouped_wgrad_down: h and d_ys must be bf16 with the same rows")
+    N = offsets.numel() - 1
+    dw = torch.empty((N, F, D), dtype=torch.float32, device=h.device)
+    call("hmoe_grouped_wgrad_down", _ptr(h), _ptr(d_ys), _ptr(offsets), N, R, F, D, _ptr(dw),
+         _stream())
+    return dw
+
+
+def grouped_wgrad_gate_up(xs: torch.Tensor, dgu: torch.Tensor, offsets: torch.Tensor):
+    """``(dWg, dWu)[e] = xs^T (dg, du)`` over each expert's segment, f32 ``[N, D, F]`` each."""
+    _check(xs, "xs", 2)
+    _check(dgu, "dgu", 2)
+    _check(offsets, "offsets", 1)
+    R, D = xs.shape
+    F = dgu.shape[1] // 2
+    if xs.dtype != torch.bfloat16 or dgu.dtype != torch.bfloat16 or dgu.shape[0] != R:
+        raise ValueError("grouped_wgrad_gate_up: xs and dgu must be bf16 with the same rows")
+    N = offsets.numel() - 1
+    dwg = torch.empty((N, D, F), dtype=torch.float32, device=xs.device)
+    dwu = torch.empty_like(dwg)
+    call("hmoe_grouped_wgrad_gate_up", _ptr(xs), _ptr(dgu), _ptr(offsets), N, R, D, F, _ptr(dwg),
+         _ptr(dwu), _stream())
+    return dwg, dwu
+
+
+def router_dw(x: torch.Tensor, d_logits: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``d_router = x^T d_logits`` f32 ``[D, N]`` (VJP of ``moe.py:178`` w.r.t. the router)."""
+    _check(x, "x", 2)
+    _check(d_logits, "d_logits", 2)
+    T, D = x.shape
+    N = d_logits.shape[1]
+    ws = int(_lib.lib().hmoe_router_dw_workspace_bytes(T, D, N))
+    if workspace is None or workspace.numel() < ws:
+        workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty((D, N), dtype=torch.float32, device=x.device)
+    call("hmoe_router_dw", _ptr(x), _dtype_code(x), _ptr(d_logits), T, D, N, _ptr(out),
+         _ptr(workspace), workspace.numel(), _stream())
+    return out

@@ -227,10 +227,9 @@ int hmoe_router_aux(const float* logits, const int32_t* top_idx, int batch, int 
                     int n_experts, int top_k, float* losses, float* expert_counts,
                     void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
 
-/* ---- backward, data gradients: the VJP that jax.value_and_grad
- *      (train.py:266) takes of MoE.__call__ (moe.py:170-246).  Routing
- *      decisions (top-k, drops, the plan) are held fixed: integer valued.
- *      Weight gradients of the expert GEMMs are not built yet. ----------- */
+/* ---- backward: the VJP that jax.value_and_grad (train.py:266) takes of
+ *      MoE.__call__ (moe.py:170-246).  Routing decisions (top-k, drops, the
+ *      plan) are held fixed: integer valued. ----------------------------- */
 
 /* VJP of the weighted combine (moe.py:80-85) for dy = d out [T,D] f32:
  * d_ys[slot_pos[t*K+k]] = bf16(dy[t] * bf16(gates[t,k])) (float32 product)
@@ -305,6 +304,31 @@ int hmoe_router_bwd(const float* logits, const int32_t* top_idx, const float* ga
  * accumulate != 0 adds into dx.  D % 64 == 0. */
 int hmoe_router_dx(const float* d_logits, const void* router_w, int w_dtype, int64_t tokens,
                    int d_model, int n_experts, float* dx, int accumulate, hmoe_stream_t stream);
+
+/* Expert weight gradients, float32, per expert e over its segment rows
+ * [offsets[e], offsets[e+1]) (an empty expert gets zeros):
+ *   dw_down [N,F,D] = h^T d_ys            (VJP of moe.py:73)
+ *   dw_gate, dw_up [N,D,F] = xs^T dg, xs^T du  (VJP of moe.py:70-71)
+ * h [rows_cap, F], d_ys [rows_cap, D], xs [rows_cap, D] (the dispatched rows,
+ * hmoe_permute_rows) and dgu [rows_cap, 2F] (hmoe_swiglu_bwd's column order)
+ * bf16.  Summation order over the rows is fixed (64-row steps, float32
+ * accumulation in the matrix cores).  F % 256 and D % 256 == 0 for
+ * dw_down; D % 256 and F % 128 == 0 for dw_gate/up. */
+int hmoe_grouped_wgrad_down(const void* h, const void* d_ys, const int32_t* offsets,
+                            int n_experts, int64_t rows_cap, int d_ff, int d_model,
+                            float* dw_down, hmoe_stream_t stream);
+int hmoe_grouped_wgrad_gate_up(const void* xs, const void* dgu, const int32_t* offsets,
+                               int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                               float* dw_gate, float* dw_up, hmoe_stream_t stream);
+
+/* d_router [D,N] f32 = x^T d_logits (the VJP of moe.py:178 with respect to
+ * the router weight), x [T,D] F32/BF16, d_logits [T,N] f32; float32 sums
+ * over chunks of 1024 tokens (ascending), then over the chunks in order.
+ * workspace >= hmoe_router_dw_workspace_bytes.  D % 64 == 0. */
+size_t hmoe_router_dw_workspace_bytes(int64_t tokens, int d_model, int n_experts);
+int hmoe_router_dw(const void* x, int x_dtype, const float* d_logits, int64_t tokens,
+                   int d_model, int n_experts, float* d_router, void* workspace,
+                   size_t workspace_bytes, hmoe_stream_t stream);
 
 #ifdef __cplusplus
 }

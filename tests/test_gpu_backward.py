@@ -19,7 +19,7 @@ import oracle as O
 from oracle import moe_backward as B
 from hanuman_amd import _lib
 from hanuman_amd import kernels as K
-from hanuman_amd.backward import BackwardOperands, moe_backward_data
+from hanuman_amd.backward import BackwardOperands, moe_backward_data, moe_backward_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -240,9 +240,63 @@ def test_layer_backward_matches_oracle(gpu, T, D, N, Kk, F, cf):
                           ref["d_ys"][:kept].view(np.uint32)), "d_ys"
     ulps = bf16_ulps(host(res["d_gates"]), ref["d_gates"])
     assert ulps.max() <= 1, "d_gates"
+    fwd["h"] = h
+    wres = moe_backward_weights(xd, fwd, res)
+    torch.cuda.synchronize()
     for name, got, want in (("d_xs", host(res["d_xs"])[:kept], ref["d_xs"][:kept]),
                             ("dx", host(res["dx"]), ref["dx"]),
-                            ("d_logits", host(res["d_logits"]), ref["d_logits"])):
+                            ("d_logits", host(res["d_logits"]), ref["d_logits"]),
+                            ("dWg", host(wres["dWg"]), ref["dWg"]),
+                            ("dWu", host(wres["dWu"]), ref["dWu"]),
+                            ("dWd", host(wres["dWd"]), ref["dWd"]),
+                            ("d_router", host(wres["d_router"]), ref["d_router"])):
         err = O.normwise_rel_err(np.asarray(got, np.float64), np.asarray(want, np.float64))
         print(f"  {name}: normwise {err:.2e}", flush=True)
         assert err < 2e-2, (name, err)
+
+
+@pytest.mark.parametrize("R,D,F,N", [(1500, 512, 256, 6), (700, 256, 384, 3)])
+def test_wgrad_gemms(gpu, R, D, F, N):
+    """Weight gradients per expert segment against float64 on the same bf16
+    operands; the last expert has no rows (its gradient must be zero) and the
+    segments end at arbitrary rows (partial 64-row steps)."""
+    rng = np.random.default_rng(R + F)
+    cuts = np.sort(rng.choice(np.arange(1, R - 4), N - 2, replace=False))
+    offsets = np.concatenate([[0], cuts, [R - 3, R - 3]]).astype(np.int32)   # rows past R-3 unused
+    off_d = torch.from_numpy(offsets).to(gpu)
+    h = O.bf16_round(rng.standard_normal((R, F)).astype(np.float32))
+    d_ys = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
+    xs = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
+    dgu = O.bf16_round(rng.standard_normal((R, 2 * F)).astype(np.float32))
+    dwd = host(K.grouped_wgrad_down(dev_bf16(h, gpu), dev_bf16(d_ys, gpu), off_d)) if F % 256 == 0 else None
+    dwg, dwu = (host(t) for t in K.grouped_wgrad_gate_up(dev_bf16(xs, gpu), dev_bf16(dgu, gpu), off_d))
+    col = np.arange(F)
+    gc = (col // 32) * 64 + col % 32
+    for e in range(N):
+        a, b = offsets[e], offsets[e + 1]
+        x64 = xs[a:b].astype(np.float64)
+        for name, got, ref in (("dWg", dwg[e], x64.T @ dgu[a:b, gc]), ("dWu", dwu[e], x64.T @ dgu[a:b, gc + 32])):
+            if b == a:
+                assert np.all(got == 0), (name, e)
+            else:
+                assert O.normwise_rel_err(got, ref) < 1e-5, (name, e, O.normwise_rel_err(got, ref))
+        if dwd is not None:
+            ref = h[a:b].astype(np.float64).T @ d_ys[a:b]
+            if b == a:
+                assert np.all(dwd[e] == 0)
+            else:
+                assert O.normwise_rel_err(dwd[e], ref) < 1e-5, ("dWd", e)
+
+
+@pytest.mark.parametrize("x_dtype", ["bf16", "f32"])
+def test_router_dw(gpu, x_dtype):
+    rng = np.random.default_rng(5)
+    T, D, N = 2500, 256, 72
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    if x_dtype == "bf16":
+        x = O.bf16_round(x)
+    dl = rng.standard_normal((T, N)).astype(np.float32)
+    xd = dev_bf16(x, gpu) if x_dtype == "bf16" else dev_f32(x, gpu)
+    got = host(K.router_dw(xd, dev_f32(dl, gpu)))
+    ref = x.astype(np.float64).T @ dl.astype(np.float64)
+    assert O.normwise_rel_err(got, ref) < 1e-5
