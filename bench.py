@@ -344,7 +344,8 @@ def main():
 
 
 def bench_backward(args, name, wl, layer):
-    """Times the data-gradient backward (hanuman_amd.backward) on `wl`."""
+    """Times the layer backward (hanuman_amd.backward): data gradients, then
+    the expert and router weight gradients, on `wl`."""
     import torch
     import hanuman_amd.kernels as K
     from hanuman_amd import _lib
@@ -365,8 +366,12 @@ def bench_backward(args, name, wl, layer):
     plan = fwd["plan"]
     N = wl.n_experts
     # with router logits given (no router weight) the VJP ends at d_logits
-    stages = ["combine_bwd", "gate_up_recompute", "dgrad_down", "swiglu_bwd", "dgrad_gate_up",
-              "gather_bwd", "router_bwd"] + (["router_dx"] if layer.router_w is not None else [])
+    has_router = layer.router_w is not None
+    stages = (["combine_bwd", "gate_up_recompute", "dgrad_down", "swiglu_bwd", "dgrad_gate_up",
+               "gather_bwd", "router_bwd"] + (["router_dx"] if has_router else [])
+              + ["permute_xs", "wgrad_gate_up", "wgrad_down"] + (["router_dw"] if has_router else []))
+    dw_ws = torch.empty(max(int(_lib.lib().hmoe_router_dw_workspace_bytes(wl.tokens, wl.d_model, N)), 1),
+                        dtype=torch.uint8, device=dev)
 
     def step(ev=None):
         marks = iter(ev) if ev is not None else None
@@ -390,10 +395,19 @@ def bench_backward(args, name, wl, layer):
         mark()
         dl = K.router_bwd(fwd["logits"], fwd["top_idx"], fwd["gates"], d_g, N, layer.mode)
         mark()
-        if layer.router_w is not None:
+        if has_router:
             K.router_dx(dl, layer.router_w, dx)
             mark()
-        return dx
+        xs = K.permute_rows(layer.x, plan, torch.bfloat16)
+        mark()
+        dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, plan.offsets)
+        mark()
+        dwd = K.grouped_wgrad_down(fwd["h"], d_ys, plan.offsets)
+        mark()
+        if has_router:
+            K.router_dw(layer.x, dl, dw_ws)
+            mark()
+        return dx, dwg, dwu, dwd
 
     t_warm = time.perf_counter()
     warm_steps = 0
@@ -429,6 +443,10 @@ def bench_backward(args, name, wl, layer):
         "gather_bwd": ("hbm", kept * D * 2 + T * D * 4 + R * 4, HBM_PEAK_GBS),
         "router_bwd": ("hbm", T * N * 4 * 2 + T * K_ * 12, HBM_PEAK_GBS),
         "router_dx": ("hbm", T * N * 4 + D * N * w_b + 2 * T * D * 4, HBM_PEAK_GBS),
+        "permute_xs": ("hbm", T * D * 2 + kept * D * 2 + R * 4, HBM_PEAK_GBS),
+        "wgrad_gate_up": ("mfma", 4 * kept * D * F, BF16_PEAK_TFLOPS),
+        "wgrad_down": ("mfma", 2 * kept * D * F, BF16_PEAK_TFLOPS),
+        "router_dw": ("hbm", T * D * 2 + T * N * 4 + D * N * 4, HBM_PEAK_GBS),
     }
     kernels = {}
     for st in stages:
@@ -446,16 +464,18 @@ def bench_backward(args, name, wl, layer):
     log(f"[bench] backward {ms_per_step:.4f} ms/step, {T / ms_per_step / 1e3:.3f} M tokens/s; stages "
         + ", ".join(f"{k} {v:.4f}" for k, v in stage_ms.items()))
     line = {
-        "metric": "MoE layer backward (data gradients) tokens/s (1 GPU)",
+        "metric": "MoE layer backward (data and weight gradients) tokens/s (1 GPU)",
         "value": round(T / (ms_per_step / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "warmup_steps_run": warm_steps,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded normal inputs, weights and output cotangent)",
-        "config": {"workload": name + " backward (data gradients)", "tokens": T, "d_model": D,
+        "config": {"workload": name + " backward (data and weight gradients)", "tokens": T, "d_model": D,
                    "n_experts": N, "top_k": K_, "d_ff": F, "capacity_factor": wl.capacity_factor,
                    "kept_rows": kept, "parallelism": "single GPU, all experts resident"},
         "roofline": roofline, "kernels": kernels, "cpu_baseline": None,
+        "data_gradients_ms": round(sum(stage_ms[st] for st in stages[:stages.index("permute_xs")]), 4),
+        "weight_gradients_ms": round(sum(stage_ms[st] for st in stages[stages.index("permute_xs"):]), 4),
     }
     print(json.dumps(line), flush=True)
 
