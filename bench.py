@@ -381,7 +381,7 @@ def bench_backward(args, name, wl, layer):
                 next(marks).record()
 
         mark()
-        d_ys, d_g = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"])
+        d_ys, d_g, _ = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"])
         mark()
         gu = K.grouped_gate_up_raw_gather(layer.x, plan, layer.w_gate_up)
         mark()

@@ -60,16 +60,19 @@ SIGNATURES = {
     "hmoe_grouped_down_fp8": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hmoe_aux_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "hmoe_router_aux": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
-    "hmoe_combine_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_combine_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _f32, _vp]),
     "hmoe_grouped_gate_up_raw_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32, _i32,
                                                _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_raw": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "hmoe_swiglu_bwd": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp]),
     "hmoe_pack_down_dgrad": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "hmoe_pack_gate_up_dgrad": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "hmoe_grouped_dgrad_down": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "hmoe_grouped_dgrad_gate_up": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
-    "hmoe_gather_bwd": (_i32, [_vp, _i32, _vp, _i64, _i32, _i32, _vp, _i32, _vp]),
+    "hmoe_gather_bwd": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp]),
     "hmoe_router_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _vp, _vp]),
+    "hmoe_aux_bwd_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "hmoe_router_aux_bwd": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz, _vp]),
     "hmoe_router_dx": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp]),
     "hmoe_grouped_wgrad_down": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
     "hmoe_grouped_wgrad_gate_up": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),

@@ -1,9 +1,11 @@
-"""Data-gradient backward of the MoE layer on the HIP library.
+"""Backward of the MoE layer on the HIP library.
 
 ``jax.value_and_grad`` (``train.py:266``) differentiates ``MoE.__call__``
-(``model/moe.py:170-246``); this is that VJP for the routed bf16 path, with
-the routing decisions (top-k indices, capacity drops, the dispatch plan) held
-fixed, as JAX does for integer-valued operations:
+(``model/moe.py:170-294``) inside the loss of ``train.py:191-200`` (output
+plus ``z_loss_weight * router_z_loss + balance_loss_weight * balance_loss``);
+this is that VJP, with the routing decisions (top-k indices, capacity drops,
+the dispatch plan, the expert counts) held fixed, as JAX does for
+integer-valued operations:
 
     combine  (moe.py:80-85)   d_ys, d_gates      hmoe_combine_bwd
     experts  (moe.py:70-73)   g, u recomputed    hmoe_grouped_gate_up_raw_gather
@@ -19,6 +21,12 @@ and the weight gradients (:func:`moe_backward_weights`):
     experts  (moe.py:70-73)   dWd = h^T d_ys,    hmoe_grouped_wgrad_down
                               dWg|dWu = xs^T dg|du  hmoe_grouped_wgrad_gate_up
     router   (moe.py:178)     d_router = x^T d_l hmoe_router_dw
+
+and, in :func:`moe_backward` (the whole module), the shared expert
+(``moe.py:161-168, 249-251``: the same grouped kernels with one segment of
+all tokens, its output cotangent ``bf16(dy / n_shared)`` from
+``hmoe_combine_bwd``) and the aux losses (``moe.py:253-283``,
+``hmoe_router_aux_bwd`` into ``d_logits``).
 
 Every step runs in the library on the current stream; there is no CPU
 fallback.
@@ -39,6 +47,26 @@ class BackwardOperands:
         self.w_down_dgrad = K.pack_down_dgrad(w_down)
 
 
+class SharedOperands:
+    """Packed operands of the shared expert(s) (``moe.py:152-159``): 2-D
+    masters for one shared expert, stacked ``[n, ...]`` for several.  Per
+    expert: the forward gate/up pack (for the g, u recompute) and the two
+    backward packs."""
+
+    def __init__(self, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                 n_shared: int, forward_packs=None):
+        if n_shared < 1:
+            raise ValueError("the shared-expert backward needs n_shared >= 1")
+        self.n_shared = n_shared
+        if n_shared == 1:
+            w_gate, w_up, w_down = (w.unsqueeze(0) for w in (w_gate, w_up, w_down))
+        self.experts = []
+        for i in range(n_shared):
+            wg, wu, wd = (w[i:i + 1].contiguous() for w in (w_gate, w_up, w_down))
+            fwd_gu = forward_packs[i][0] if forward_packs is not None else K.pack_gate_up(wg, wu)
+            self.experts.append((fwd_gu, K.pack_gate_up_dgrad(wg, wu), K.pack_down_dgrad(wd)))
+
+
 def moe_backward_data(x: torch.Tensor, router_w: torch.Tensor, fwd: dict,
                       w_gate_up: torch.Tensor, ops: BackwardOperands, dy: torch.Tensor,
                       mode: int = _lib.ROUTE_SOFTMAX,
@@ -54,7 +82,7 @@ def moe_backward_data(x: torch.Tensor, router_w: torch.Tensor, fwd: dict,
     """
     plan = fwd["plan"]
     N = plan.n_experts
-    d_ys, d_gates = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"])
+    d_ys, d_gates, _ = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"])
     gu = K.grouped_gate_up_raw_gather(x, plan, w_gate_up)
     dh = K.grouped_dgrad_down(d_ys, plan.offsets, ops.w_down_dgrad)
     dgu = K.swiglu_bwd(dh, gu, plan.offsets)
@@ -78,3 +106,85 @@ def moe_backward_weights(x: torch.Tensor, fwd: dict, data: dict) -> dict:
     dwd = K.grouped_wgrad_down(fwd["h"], data["d_ys"], plan.offsets)
     d_router = K.router_dw(x, data["d_logits"])
     return {"dWg": dwg, "dWu": dwu, "dWd": dwd, "d_router": d_router}
+
+
+def shared_backward(xc: torch.Tensor, d_shared: torch.Tensor, h_shared, ops: SharedOperands) -> dict:
+    """VJP of the shared expert(s) for the output cotangent ``d_shared``
+    (``bf16(dy / n_shared)`` from :func:`kernels.combine_bwd`): each SwiGLU
+    (``moe.py:23-29``) is one segment of all ``T`` rows on the grouped
+    kernels.  ``xc`` bf16 ``[T, D]``; ``h_shared`` the forward's ``h`` per
+    shared expert.  Returns ``dx`` (bf16 ``[T, D]`` for one shared expert,
+    float32 sum for several) and ``dWg``, ``dWu``, ``dWd`` in the parameter
+    shapes."""
+    T = xc.shape[0]
+    off = torch.tensor([0, T], dtype=torch.int32, device=xc.device)
+    dxs, dwg, dwu, dwd = [], [], [], []
+    for (fwd_gu, gu_dgrad, down_dgrad), h in zip(ops.experts, h_shared):
+        gu = K.grouped_gate_up_raw(xc, off, fwd_gu)
+        dh = K.grouped_dgrad_down(d_shared, off, down_dgrad)
+        dgu = K.swiglu_bwd(dh, gu, off)
+        dxs.append(K.grouped_dgrad_gate_up(dgu, off, gu_dgrad))
+        g_, u_ = K.grouped_wgrad_gate_up(xc, dgu, off)
+        dwg.append(g_)
+        dwu.append(u_)
+        dwd.append(K.grouped_wgrad_down(h, d_shared, off))
+    if ops.n_shared == 1:
+        return {"dx": dxs[0], "dWg": dwg[0][0], "dWu": dwu[0][0], "dWd": dwd[0][0]}
+    # several shared experts: their input gradients add in float32
+    dx = dxs[0].float()
+    for d in dxs[1:]:
+        dx += d.float()
+    return {"dx": dx, "dWg": torch.cat(dwg), "dWu": torch.cat(dwu), "dWd": torch.cat(dwd)}
+
+
+def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
+                 w_gate_up: torch.Tensor, ops: BackwardOperands, dy: torch.Tensor, *,
+                 mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0,
+                 shared: SharedOperands | None = None, h_shared=None,
+                 aux: tuple | None = None) -> dict:
+    """The whole module's VJP (``moe.py:170-294``): every input and weight
+    gradient for the cotangent ``dy`` (f32 ``[T, D]``) of ``out`` and, with
+    ``aux = (batch, seq, d_losses)``, the cotangents ``d_losses`` (f32 ``[3]``:
+    router_z_loss, balance_loss, mean_entropy) of the aux losses.
+
+    ``x`` ``[T, D]`` (bf16 or f32); ``fwd`` the forward's ``logits``,
+    ``top_idx``, ``gates``, ``plan``, ``h``, ``ys``; ``shared``/``h_shared``
+    the shared expert's operands and forward ``h`` (None: no shared expert).
+    Returns ``dx`` f32 ``[T, D]``, ``d_router`` f32 ``[D, N]`` (None without a
+    router weight), ``dWg``, ``dWu`` ``[N, D, F]``, ``dWd`` ``[N, F, D]`` and
+    ``dWg_shared``, ``dWu_shared``, ``dWd_shared`` when there is a shared
+    expert.
+    """
+    plan = fwd["plan"]
+    N = plan.n_experts
+    xc = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)   # x.astype(dtype), moe.py:198
+    n_sh = shared.n_shared if shared is not None else 0
+    d_ys, d_gates, d_sh = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"], n_sh)
+    gu = K.grouped_gate_up_raw_gather(xc, plan, w_gate_up)
+    dh = K.grouped_dgrad_down(d_ys, plan.offsets, ops.w_down_dgrad)
+    dgu = K.swiglu_bwd(dh, gu, plan.offsets)
+    del gu, dh
+    d_xs = K.grouped_dgrad_gate_up(dgu, plan.offsets, ops.w_gate_up_dgrad)
+    res = {}
+    residual = None
+    if shared is not None:
+        sh = shared_backward(xc, d_sh, h_shared, shared)
+        residual = sh["dx"]
+        res.update(dWg_shared=sh["dWg"], dWu_shared=sh["dWu"], dWd_shared=sh["dWd"])
+    dx = K.gather_bwd(d_xs, plan, residual=residual)
+    del d_xs, residual
+    d_logits = K.router_bwd(fwd["logits"], fwd["top_idx"], fwd["gates"], d_gates, N, mode,
+                            routed_scaling_factor)
+    if aux is not None:
+        batch, seq, d_losses = aux
+        K.router_aux_bwd(fwd["logits"], fwd["top_idx"], batch, seq, d_losses, d_logits)
+    if router_w is not None:
+        K.router_dx(d_logits, router_w, dx)
+    xs = K.permute_rows(x, plan, torch.bfloat16)
+    dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, plan.offsets)
+    del xs, dgu
+    dwd = K.grouped_wgrad_down(fwd["h"], d_ys, plan.offsets)
+    d_router = K.router_dw(x, d_logits) if router_w is not None else None
+    res.update(dx=dx, d_router=d_router, dWg=dwg, dWu=dwu, dWd=dwd, d_logits=d_logits,
+               d_gates=d_gates)
+    return res

@@ -19,12 +19,15 @@ constexpr int kMaxKBwd = 16;
 // One wave per token.  d_ys[pos(t,k)] = bf16(dy[t] * bf16(g[t,k])) (float32
 // product, one rounding); d_g[t,k] = bf16(f32(sum_d dy[t,d] * ys[pos,d])) with
 // the sum in float64 (every product of a float32 and a bf16 value is exact in
-// float64), 0 for dropped slots.
+// float64), 0 for dropped slots.  With d_shared, also the cotangent of the
+// shared expert's output (moe.py:249-251, each SwiGLU's f32(bf16) result):
+// d_shared[t] = bf16(dy[t] / shared_div).
 template <int KMAX>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(
     const float* __restrict__ dy, const uint16_t* __restrict__ ys,
     const int32_t* __restrict__ slot_pos, const float* __restrict__ gates, int64_t tokens,
-    int top_k, int d_model, uint16_t* __restrict__ d_ys, float* __restrict__ d_gates) {
+    int top_k, int d_model, uint16_t* __restrict__ d_ys, float* __restrict__ d_gates,
+    uint16_t* __restrict__ d_shared, float shared_div) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -73,6 +76,13 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
     for (int u = 0; u < kU; ++u) {
       const int c = c0 + 64 * u;
       if (c >= chunks) break;
+      if (d_shared != nullptr) {
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          o[q] = pack_bf16x2(d[u][2 * q] / shared_div, d[u][2 * q + 1] / shared_div);
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(d_shared + t * d_model + c * 8));
+      }
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
         if (k < top_k && pos[k] >= 0) {
@@ -350,7 +360,8 @@ __global__ __launch_bounds__(256) void router_dw_sum_kernel(const float* __restr
 
 extern "C" int hmoe_combine_bwd(const float* dy, const void* ys, const int32_t* slot_pos,
                                 const float* gates, int64_t tokens, int top_k, int d_model,
-                                void* d_ys, float* d_gates, hmoe_stream_t stream) {
+                                void* d_ys, float* d_gates, void* d_shared, float shared_div,
+                                hmoe_stream_t stream) {
   using namespace hmoe;
   HMOE_REQUIRE(tokens >= 0, "combine_bwd: tokens must be >= 0");
   HMOE_REQUIRE(top_k >= 1 && top_k <= kMaxKBwd, "combine_bwd: top_k must be in [1, %d] (got %d)",
@@ -359,18 +370,21 @@ extern "C" int hmoe_combine_bwd(const float* dy, const void* ys, const int32_t* 
                "combine_bwd: d_model must be a multiple of 8 (got %d)", d_model);
   if (tokens == 0) return HMOE_OK;
   HMOE_REQUIRE(dy && ys && slot_pos && gates && d_ys && d_gates, "combine_bwd: null pointer argument");
+  HMOE_REQUIRE(d_shared == nullptr || shared_div >= 1.0f,
+               "combine_bwd: shared_div must be the number of shared experts (>= 1)");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4)));
   const uint16_t* y = static_cast<const uint16_t*>(ys);
   uint16_t* o = static_cast<uint16_t*>(d_ys);
+  uint16_t* sh = static_cast<uint16_t*>(d_shared);
   if (top_k <= 2)
-    hipLaunchKernelGGL(combine_bwd_kernel<2>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates);
+    hipLaunchKernelGGL(combine_bwd_kernel<2>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
   else if (top_k <= 4)
-    hipLaunchKernelGGL(combine_bwd_kernel<4>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates);
+    hipLaunchKernelGGL(combine_bwd_kernel<4>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
   else if (top_k <= 8)
-    hipLaunchKernelGGL(combine_bwd_kernel<8>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates);
+    hipLaunchKernelGGL(combine_bwd_kernel<8>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
   else
-    hipLaunchKernelGGL(combine_bwd_kernel<16>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates);
+    hipLaunchKernelGGL(combine_bwd_kernel<16>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
   return check_launch("hmoe_combine_bwd");
 }
 

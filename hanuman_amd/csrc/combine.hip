@@ -205,10 +205,12 @@ extern "C" int hmoe_combine(const void* ys, int ys_dtype, const int32_t* slot_po
 
 // The VJP of the row gather xs[j] = x_flat[perm_src[j] / K] (moe.py:56):
 // dx[t] = sum_k d_xs[slot_pos[t*K+k]] over kept slots, k ascending in float32
-// -- the combine with unit weights.
+// -- the combine with unit weights; a residual (the shared expert's input
+// gradient) is added last.
 extern "C" int hmoe_gather_bwd(const void* d_xs, int d_xs_dtype, const int32_t* slot_pos,
-                               int64_t tokens, int top_k, int d_model, void* dx, int dx_dtype,
+                               const void* residual, int residual_dtype, int64_t tokens,
+                               int top_k, int d_model, void* dx, int dx_dtype,
                                hmoe_stream_t stream) {
-  return hmoe_combine(d_xs, d_xs_dtype, slot_pos, nullptr, nullptr, HMOE_F32, tokens, top_k,
-                      d_model, dx, dx_dtype, stream);
+  return hmoe_combine(d_xs, d_xs_dtype, slot_pos, nullptr, residual, residual_dtype, tokens,
+                      top_k, d_model, dx, dx_dtype, stream);
 }

@@ -1259,6 +1259,25 @@ extern "C" int hmoe_grouped_gate_up_raw_gather(const void* x, int64_t tokens, in
                         static_cast<int>(tokens));
 }
 
+extern "C" int hmoe_grouped_gate_up_raw(const void* xs, const int32_t* offsets, int n_experts,
+                                        int64_t rows_cap, int d_model, int d_ff,
+                                        const void* w_gate_up_packed, void* gu,
+                                        hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_raw: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "grouped_gate_up_raw: rows_cap must be >= 0");
+  HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_raw: d_model must be a multiple of %d (got %d)", kBK, d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_raw: d_ff must be a multiple of %d (got %d)", kBN / 2, d_ff);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(xs && offsets && w_gate_up_packed && gu, "grouped_gate_up_raw: null pointer argument");
+  return launch_grouped(false, false, xs, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, gu, 2 * d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_raw");
+}
+
 extern "C" int hmoe_grouped_dgrad_down(const void* d_ys, const int32_t* offsets, int n_experts,
                                        int64_t rows_cap, int d_model, int d_ff,
                                        const void* w_down_dgrad, void* dh, hmoe_stream_t stream) {

@@ -369,9 +369,13 @@ def router_aux(logits: torch.Tensor, top_idx: torch.Tensor, batch: int, seq: int
 # Data gradients of the layer (the VJP of moe.py:170-246 with the routing held
 # fixed); see hanuman_amd.backward for the composed pass.
 
-def combine_bwd(dy: torch.Tensor, ys: torch.Tensor, plan: Plan, gates: torch.Tensor):
-    """VJP of :func:`combine`: ``(d_ys bf16 [rows, D], d_gates f32 [T, K])``;
-    rows of ``d_ys`` no kept slot maps to are left as allocated."""
+def combine_bwd(dy: torch.Tensor, ys: torch.Tensor, plan: Plan, gates: torch.Tensor,
+                n_shared: int = 0):
+    """VJP of :func:`combine`: ``(d_ys bf16 [rows, D], d_gates f32 [T, K],
+    d_shared)``; rows of ``d_ys`` no kept slot maps to are left as allocated.
+    ``d_shared`` is ``bf16(dy / n_shared)`` ``[T, D]`` (the cotangent of each
+    shared expert's output, ``moe.py:249-251``) when ``n_shared > 0``, else
+    None."""
     _check(dy, "dy", 2)
     _check(ys, "ys", 2)
     _check(gates, "gates", 2)
@@ -383,9 +387,10 @@ def combine_bwd(dy: torch.Tensor, ys: torch.Tensor, plan: Plan, gates: torch.Ten
         raise ValueError("combine_bwd: inconsistent shapes or dtypes")
     d_ys = torch.empty_like(ys)
     d_g = torch.empty((T, K), dtype=torch.float32, device=dy.device)
+    d_sh = torch.empty((T, D), dtype=torch.bfloat16, device=dy.device) if n_shared > 0 else None
     call("hmoe_combine_bwd", _ptr(dy), _ptr(ys), _ptr(plan.slot_pos), _ptr(gates), T, K, D,
-         _ptr(d_ys), _ptr(d_g), _stream())
-    return d_ys, d_g
+         _ptr(d_ys), _ptr(d_g), _ptr(d_sh), float(max(n_shared, 1)), _stream())
+    return d_ys, d_g, d_sh
 
 
 def grouped_gate_up_raw_gather(x: torch.Tensor, plan: Plan, w_gate_up: torch.Tensor) -> torch.Tensor:
@@ -402,6 +407,24 @@ def grouped_gate_up_raw_gather(x: torch.Tensor, plan: Plan, w_gate_up: torch.Ten
     gu = torch.empty((plan.rows_cap, F2), dtype=torch.bfloat16, device=x.device)
     call("hmoe_grouped_gate_up_raw_gather", _ptr(x), T, plan.top_k, _ptr(plan.perm_src),
          _ptr(plan.offsets), N, plan.rows_cap, D, F2 // 2, _ptr(w_gate_up), _ptr(gu), _stream())
+    return gu
+
+
+def grouped_gate_up_raw(xs: torch.Tensor, offsets: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+    """g and u of rows given in order (the shared expert, ``moe.py:23-29``),
+    bf16 ``[rows, 2F]`` in the packed gate/up column order."""
+    _check(xs, "xs", 2)
+    _check(offsets, "offsets", 1)
+    _check(w_gate_up, "w_gate_up", 3)
+    if xs.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16:
+        raise TypeError("grouped_gate_up_raw takes bf16 operands")
+    R, D = xs.shape
+    N, F2, D2 = w_gate_up.shape
+    if D2 != D or offsets.numel() != N + 1:
+        raise ValueError("grouped_gate_up_raw: inconsistent shapes")
+    gu = torch.empty((R, F2), dtype=torch.bfloat16, device=xs.device)
+    call("hmoe_grouped_gate_up_raw", _ptr(xs), _ptr(offsets), N, R, D, F2 // 2, _ptr(w_gate_up),
+         _ptr(gu), _stream())
     return gu
 
 
@@ -479,14 +502,22 @@ def grouped_dgrad_gate_up(dgu: torch.Tensor, offsets: torch.Tensor, w_gate_up_dg
     return d_xs
 
 
-def gather_bwd(d_xs: torch.Tensor, plan: Plan, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """VJP of the row gather (``moe.py:56``): ``dx[t] = sum_k d_xs[slot_pos[t,k]]``."""
+def gather_bwd(d_xs: torch.Tensor, plan: Plan, out_dtype: torch.dtype = torch.float32,
+               residual: torch.Tensor | None = None) -> torch.Tensor:
+    """VJP of the row gather (``moe.py:56``): ``dx[t] = sum_k d_xs[slot_pos[t,k]]``
+    (+ ``residual[t]``, the shared expert's input gradient, added last)."""
     _check(d_xs, "d_xs", 2)
     T = plan.slot_pos.numel() // plan.top_k
     D = d_xs.shape[1]
+    res_dt = _lib.F32
+    if residual is not None:
+        _check(residual, "residual", 2)
+        if tuple(residual.shape) != (T, D):
+            raise ValueError("gather_bwd: residual must be [T, D]")
+        res_dt = _dtype_code(residual)
     dx = torch.empty((T, D), dtype=out_dtype, device=d_xs.device)
-    call("hmoe_gather_bwd", _ptr(d_xs), _dtype_code(d_xs), _ptr(plan.slot_pos), T, plan.top_k, D,
-         _ptr(dx), _DT[out_dtype], _stream())
+    call("hmoe_gather_bwd", _ptr(d_xs), _dtype_code(d_xs), _ptr(plan.slot_pos), _ptr(residual),
+         res_dt, T, plan.top_k, D, _ptr(dx), _DT[out_dtype], _stream())
     return dx
 
 
@@ -503,6 +534,35 @@ def router_bwd(logits: torch.Tensor | None, top_idx: torch.Tensor, gates: torch.
     call("hmoe_router_bwd", _ptr(logits), _ptr(top_idx), _ptr(gates), _ptr(d_gates), T,
          n_experts, K, mode, routed_scaling_factor, _ptr(dl), _stream())
     return dl
+
+
+def router_aux_bwd(logits: torch.Tensor, top_idx: torch.Tensor, batch: int, seq: int,
+                   d_losses: torch.Tensor, d_logits: torch.Tensor | None = None,
+                   workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """VJP of the aux losses (``moe.py:253-283``) with respect to the logits
+    for ``d_losses`` f32 ``[3]`` (cotangents of router_z_loss, balance_loss,
+    mean_entropy): added into ``d_logits`` when given, else a new f32
+    ``[T, N]``.  The per-sequence expert counts of ``top_idx`` are held fixed."""
+    _check(logits, "logits", 2)
+    _check(top_idx, "top_idx", 2)
+    _check(d_losses, "d_losses", 1)
+    T, N = logits.shape
+    if T != batch * seq or top_idx.shape[0] != T or d_losses.numel() != 3 \
+            or d_losses.dtype != torch.float32:
+        raise ValueError("router_aux_bwd: logits/top_idx must hold batch*seq tokens, d_losses f32 [3]")
+    acc = d_logits is not None
+    if acc:
+        _check(d_logits, "d_logits", 2)
+        if tuple(d_logits.shape) != (T, N) or d_logits.dtype != torch.float32:
+            raise ValueError("router_aux_bwd: d_logits must be f32 [T, N]")
+    else:
+        d_logits = torch.empty((T, N), dtype=torch.float32, device=logits.device)
+    ws = int(_lib.lib().hmoe_aux_bwd_workspace_bytes(batch, seq, N))
+    if workspace is None or workspace.numel() < ws:
+        workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=logits.device)
+    call("hmoe_router_aux_bwd", _ptr(logits), _ptr(top_idx), batch, seq, N, top_idx.shape[1],
+         _ptr(d_losses), _ptr(d_logits), int(acc), _ptr(workspace), workspace.numel(), _stream())
+    return d_logits
 
 
 def router_dx(d_logits: torch.Tensor, router_w: torch.Tensor, dx: torch.Tensor | None = None) -> torch.Tensor:

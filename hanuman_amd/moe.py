@@ -204,9 +204,10 @@ class MoE:
         return self._shared_pack.get((wg, wu, wd), build)
 
     # ---- forward -----------------------------------------------------------
-    def _shared_ffn(self, x_flat: torch.Tensor) -> torch.Tensor:
+    def _shared_ffn(self, x_flat: torch.Tensor, hs: list | None = None) -> torch.Tensor:
         """Shared expert(s) (``moe.py:161-168``): bf16 output of one expert, or
-        the float32 mean over ``n_shared_experts``."""
+        the float32 mean over ``n_shared_experts``.  ``hs`` collects each
+        expert's ``h`` for the backward."""
         if self.n_shared_experts == 0:
             return 0.0 / self.n_shared_experts  # ZeroDivisionError, as the reference
         T = x_flat.shape[0]
@@ -214,6 +215,8 @@ class MoE:
         outs = []
         for wgu, wd in self._packed_shared():
             h = K.grouped_gate_up(x_flat, off, wgu)
+            if hs is not None:
+                hs.append(h)
             outs.append(K.grouped_down(h, off, wd))
         if len(outs) == 1:
             return outs[0]
@@ -222,8 +225,36 @@ class MoE:
             acc += o.float()
         return acc / self.n_shared_experts
 
+    def _params(self):
+        return (self.router.value, self.expert_w_gate.value, self.expert_w_up.value,
+                self.expert_w_down.value, self.shared_w_gate.value, self.shared_w_up.value,
+                self.shared_w_down.value)
+
     def __call__(self, x: torch.Tensor):
-        """``x [B,S,D]`` -> (``out [B,S,D]`` float32, aux dict)."""
+        """``x [B,S,D]`` -> (``out [B,S,D]`` float32, aux dict).
+
+        When autograd is on and ``x`` or a parameter requires grad, the call
+        is recorded as one autograd node whose backward is the library's VJP
+        of the whole module (:func:`hanuman_amd.backward.moe_backward`):
+        ``out``, ``router_z_loss``, ``balance_loss`` and ``mean_entropy``
+        are differentiable, ``expert_counts`` is not (``train.py:191-200``
+        differentiates the same outputs)."""
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self._params())):
+            out, z, bal, ent, counts = _MoEFunction.apply(self, x, *self._params())
+            return out, {"router_z_loss": z, "balance_loss": bal, "mean_entropy": ent,
+                         "expert_counts": counts}
+        out, losses, counts, _ = self._forward(x, save=False)
+        aux = {
+            "router_z_loss": losses[0],
+            "balance_loss": losses[1],
+            "mean_entropy": losses[2],
+            "expert_counts": counts,
+        }
+        return out, aux
+
+    def _forward(self, x: torch.Tensor, save: bool):
+        """The forward; returns ``(out [B,S,D], losses [3], counts [N], saved)``
+        with ``saved`` the backward's residuals when ``save``."""
         _require_bf16_compute(self.dtype)
         if x.dim() != 3:
             raise ValueError(f"x must be [B, S, d_model] (got {tuple(x.shape)})")
@@ -246,13 +277,70 @@ class MoE:
             h = K.grouped_gate_up(K.permute_rows(x2, plan, self.dtype), plan.offsets, wgu)
         ys = K.grouped_down(h, plan.offsets, wd)
         xc = x2 if x2.dtype == self.dtype else x2.to(self.dtype)
-        shared = self._shared_ffn(xc)
+        hs = [] if save else None
+        shared = self._shared_ffn(xc, hs)
         out = K.combine(ys, plan, gates, shared, torch.float32)
         losses, counts = K.router_aux(logits, top_idx, B, S)
-        aux = {
-            "router_z_loss": losses[0],
-            "balance_loss": losses[1],
-            "mean_entropy": losses[2],
-            "expert_counts": counts,
-        }
-        return out.reshape(B, S, D), aux
+        saved = None
+        if save:
+            saved = {"x": x2, "logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan,
+                     "h": h, "ys": ys, "h_shared": hs, "mode": mode, "rsf": rsf,
+                     "batch": B, "seq": S}
+        return out.reshape(B, S, D), losses, counts, saved
+
+    def _backward_operands(self):
+        """Packed backward operands of the routed and shared experts, cached
+        like the forward's packs (rebuilt when a master changes)."""
+        if not hasattr(self, "_bwd_pack"):
+            self._bwd_pack = _PackCache()
+        wg, wu, wd = self.expert_w_gate.value, self.expert_w_up.value, self.expert_w_down.value
+        swg, swu, swd = self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value
+        from .backward import BackwardOperands, SharedOperands
+
+        def build():
+            return (BackwardOperands(wg, wu, wd),
+                    SharedOperands(swg, swu, swd, self.n_shared_experts, self._packed_shared()))
+        return self._bwd_pack.get((wg, wu, wd, swg, swu, swd), build)
+
+
+class _MoEFunction(torch.autograd.Function):
+    """``MoE.__call__`` as one autograd node: forward on the library, backward
+    the library's VJP of the whole module (routing held fixed)."""
+
+    @staticmethod
+    def forward(ctx, layer, x, router, wg, wu, wd, swg, swu, swd):
+        out, losses, counts, saved = layer._forward(x, save=True)
+        ctx.layer = layer
+        ctx.saved = saved
+        ctx.x_shape, ctx.x_dtype = x.shape, x.dtype
+        ctx.shared_shapes = (swg.shape, swu.shape, swd.shape)
+        ctx.mark_non_differentiable(counts)
+        z, bal, ent = (v.clone() for v in losses.unbind())
+        return out, z, bal, ent, counts
+
+    @staticmethod
+    def backward(ctx, d_out, d_z, d_bal, d_ent, d_counts):
+        from .backward import moe_backward
+        layer, sv = ctx.layer, ctx.saved
+        ctx.saved = None
+        x2 = sv["x"]
+        T, D = x2.shape
+        dev = x2.device
+        dy = (d_out.reshape(T, D).float().contiguous() if d_out is not None
+              else torch.zeros((T, D), dtype=torch.float32, device=dev))
+        zero = torch.zeros((), dtype=torch.float32, device=dev)
+        d_losses = torch.stack([(g.float() if g is not None else zero)
+                                for g in (d_z, d_bal, d_ent)]).contiguous()
+        ops, shared = layer._backward_operands()
+        wgu, _ = layer._packed_routed()
+        router_w = layer.router.value.float().contiguous()
+        g = moe_backward(x2, router_w, {k: sv[k] for k in ("logits", "top_idx", "gates", "plan",
+                                                           "h", "ys")},
+                         wgu, ops, dy, mode=sv["mode"], routed_scaling_factor=sv["rsf"],
+                         shared=shared, h_shared=sv["h_shared"],
+                         aux=(sv["batch"], sv["seq"], d_losses))
+        dx = g["dx"].reshape(ctx.x_shape).to(ctx.x_dtype)
+        sg, su, sd = ctx.shared_shapes
+        return (None, dx, g["d_router"], g["dWg"], g["dWu"], g["dWd"],
+                g["dWg_shared"].reshape(sg), g["dWu_shared"].reshape(su),
+                g["dWd_shared"].reshape(sd))

@@ -228,18 +228,21 @@ int hmoe_router_aux(const float* logits, const int32_t* top_idx, int batch, int 
                     void* workspace, size_t workspace_bytes, hmoe_stream_t stream);
 
 /* ---- backward: the VJP that jax.value_and_grad (train.py:266) takes of
- *      MoE.__call__ (moe.py:170-246).  Routing decisions (top-k, drops, the
- *      plan) are held fixed: integer valued. ----------------------------- */
+ *      MoE.__call__ (moe.py:170-294) for the loss of train.py:191-200.
+ *      Routing decisions (top-k, drops, the plan, the expert counts) are
+ *      held fixed: integer valued. --------------------------------------- */
 
 /* VJP of the weighted combine (moe.py:80-85) for dy = d out [T,D] f32:
  * d_ys[slot_pos[t*K+k]] = bf16(dy[t] * bf16(gates[t,k])) (float32 product)
  * for kept slots (other rows of d_ys are not written), d_gates[t,k] =
  * bf16(f32(sum_d dy[t,d] * ys[pos,d])) with the sum in float64, 0 for dropped
  * slots.  ys and d_ys [rows, D] bf16, d_gates [T,K] f32.  D % 8 == 0,
- * K <= 16. */
+ * K <= 16.  d_shared (NULL: not written) [T,D] bf16 = bf16(dy / shared_div):
+ * the cotangent of each shared expert's output (moe.py:161-168, 249-251),
+ * shared_div = n_shared_experts. */
 int hmoe_combine_bwd(const float* dy, const void* ys, const int32_t* slot_pos,
                      const float* gates, int64_t tokens, int top_k, int d_model, void* d_ys,
-                     float* d_gates, hmoe_stream_t stream);
+                     float* d_gates, void* d_shared, float shared_div, hmoe_stream_t stream);
 
 /* Recomputes the gate/up GEMM outputs g and u (moe.py:70-71) on the
  * dispatched rows of x, as bf16 [rows_cap, 2F] in the packed operand's
@@ -251,6 +254,11 @@ int hmoe_grouped_gate_up_raw_gather(const void* x, int64_t tokens, int top_k,
                                     int n_experts, int64_t rows_cap, int d_model, int d_ff,
                                     const void* w_gate_up_packed, void* gu,
                                     hmoe_stream_t stream);
+/* The same on rows given in order (xs [rows_cap, D] bf16, as
+ * hmoe_grouped_gate_up): the shared expert's g and u (moe.py:23-29). */
+int hmoe_grouped_gate_up_raw(const void* xs, const int32_t* offsets, int n_experts,
+                             int64_t rows_cap, int d_model, int d_ff,
+                             const void* w_gate_up_packed, void* gu, hmoe_stream_t stream);
 
 /* VJP of h = silu(g) * u (moe.py:72): dg = dh * u * silu'(g), du = dh *
  * silu(g), float32 arithmetic, one bf16 rounding each.  dh [rows, F], gu and
@@ -285,9 +293,12 @@ int hmoe_grouped_dgrad_gate_up(const void* dgu, const int32_t* offsets, int n_ex
                                const void* w_gate_up_dgrad, void* d_xs, hmoe_stream_t stream);
 
 /* VJP of the row gather (moe.py:56): dx[t] = sum_k d_xs[slot_pos[t*K+k]]
- * over kept slots, float32, k ascending (hmoe_combine with unit weights). */
-int hmoe_gather_bwd(const void* d_xs, int d_xs_dtype, const int32_t* slot_pos, int64_t tokens,
-                    int top_k, int d_model, void* dx, int dx_dtype, hmoe_stream_t stream);
+ * over kept slots, float32, k ascending (hmoe_combine with unit weights),
+ * then + residual[t] (NULL: none; F32/BF16 [T,D]: the shared expert's input
+ * gradient). */
+int hmoe_gather_bwd(const void* d_xs, int d_xs_dtype, const int32_t* slot_pos,
+                    const void* residual, int residual_dtype, int64_t tokens, int top_k,
+                    int d_model, void* dx, int dx_dtype, hmoe_stream_t stream);
 
 /* VJP of the gates with respect to the logits (moe.py:179-192; mode as in
  * hmoe_router): d_logits [T,N] f32, zero off the selected experts.
@@ -298,6 +309,19 @@ int hmoe_gather_bwd(const void* d_xs, int d_xs_dtype, const int32_t* slot_pos, i
 int hmoe_router_bwd(const float* logits, const int32_t* top_idx, const float* gates,
                     const float* d_gates, int64_t tokens, int n_experts, int top_k, int mode,
                     float routed_scaling_factor, float* d_logits, hmoe_stream_t stream);
+
+/* VJP of the aux losses (moe.py:253-283) with respect to the logits, for
+ * d_losses[3] = cotangents of {router_z_loss, balance_loss, mean_entropy}
+ * (device memory; train.py:198-200 weighs the first two): d_logits [B*S, N]
+ * f32 (+)= (accumulate != 0) d_z * 2 lse/T * softmax(l) + the balance and
+ * entropy terms through p = sigmoid(l) / (sum sigmoid(l) + 1e-9), with the
+ * per-sequence counts of top_idx held fixed.  N <= 256.
+ * workspace >= hmoe_aux_bwd_workspace_bytes. */
+size_t hmoe_aux_bwd_workspace_bytes(int batch, int seq, int n_experts);
+int hmoe_router_aux_bwd(const float* logits, const int32_t* top_idx, int batch, int seq,
+                        int n_experts, int top_k, const float* d_losses, float* d_logits,
+                        int accumulate, void* workspace, size_t workspace_bytes,
+                        hmoe_stream_t stream);
 
 /* dx [T,D] f32 (+)= d_logits [T,N] @ router_w^T (router_w [D,N] F32/BF16):
  * the VJP of l = f32(x) @ router (moe.py:175,178) with respect to x.

@@ -32,8 +32,8 @@ from .moe_oracle import F32, F64, bf16_round
 
 __all__ = [
     "silu64", "dsilu64", "combine_bwd", "swiglu_bwd", "expert_ffn_bwd", "gather_bwd",
-    "route_softmax_bwd", "route_sigmoid_bwd", "router_bwd", "moe_backward",
-    "routed_forward64",
+    "route_softmax_bwd", "route_sigmoid_bwd", "router_bwd", "aux_bwd", "shared_bwd",
+    "moe_backward", "routed_forward64", "aux_forward64", "shared_forward64",
 ]
 
 
@@ -219,6 +219,112 @@ def router_bwd(x, router_w, d_logits):
 
 
 # --------------------------------------------------------------------------
+# aux losses (moe.py:253-283) and the shared expert (moe.py:161-168, 249-251)
+# --------------------------------------------------------------------------
+
+def aux_forward64(logits, top_idx, B: int, S: int):
+    """``(router_z_loss, balance_loss, mean_entropy)`` in float64 with the
+    per-sequence expert counts taken from ``top_idx`` (``moe.py:253-283``;
+    the same arithmetic as ``moe_oracle.aux_losses``, scores recomputed from
+    the logits): the function :func:`aux_bwd` differentiates."""
+    l = np.asarray(logits, F64)
+    N = l.shape[-1]
+    l = l.reshape(B, S, N)
+    K = np.asarray(top_idx).shape[-1]
+    m = l.max(axis=-1, keepdims=True)
+    lse = (m + np.log(np.exp(l - m).sum(axis=-1, keepdims=True)))[..., 0]
+    idx = np.asarray(top_idx).reshape(B, S * K)
+    counts = np.stack([np.bincount(idx[b], minlength=N) for b in range(B)]).astype(F64)
+    s = 1.0 / (1.0 + np.exp(-l))
+    p = s / (s.sum(axis=-1, keepdims=True) + 1e-9)
+    bal = np.mean(N * np.sum(counts / (S * K) * p.mean(axis=1), axis=-1))
+    ent = np.mean(-np.sum(p * np.log(p + 1e-9), axis=-1))
+    return float(np.mean(lse ** 2)), float(bal), float(ent)
+
+
+def aux_bwd(logits, top_idx, B: int, S: int, d_z: float, d_bal: float, d_ent: float = 0.0):
+    """VJP of the aux losses with respect to the router logits, for the
+    cotangents ``d_z``, ``d_bal``, ``d_ent`` of ``router_z_loss``,
+    ``balance_loss`` and ``mean_entropy`` (``moe.py:253-283``).  The expert
+    counts come from the top-k indices and carry no derivative.  With
+    ``T = B*S``, ``q = softmax(l)``, ``s = sigmoid(l)``, ``Z = sum s + 1e-9``,
+    ``p = s / Z`` and ``f[b,n] = counts[b,n] / (S*K)``:
+
+    * z-loss: ``dl += d_z * 2 lse / T * q``;
+    * ``dp = d_bal * N f[b] / (B*S) - d_ent * (log(p + 1e-9) + p / (p + 1e-9)) / T``;
+    * through ``p = s / Z``: ``ds = dp / Z - sum(dp s) / Z^2``, ``dl += ds s (1 - s)``.
+
+    Returns ``d_logits [T, N]`` float64.
+    """
+    l = np.asarray(logits, F64)
+    N = l.shape[-1]
+    T = B * S
+    l = l.reshape(B, S, N)
+    K = np.asarray(top_idx).shape[-1]
+    m = l.max(axis=-1, keepdims=True)
+    e = np.exp(l - m)
+    se = e.sum(axis=-1, keepdims=True)
+    lse = m + np.log(se)
+    dl = d_z * 2.0 * lse / T * (e / se)
+    idx = np.asarray(top_idx).reshape(B, S * K)
+    counts = np.stack([np.bincount(idx[b], minlength=N) for b in range(B)]).astype(F64)
+    s = 1.0 / (1.0 + np.exp(-l))
+    Z = s.sum(axis=-1, keepdims=True) + 1e-9
+    p = s / Z
+    dp = d_bal * N * (counts / (S * K))[:, None, :] / (B * S)
+    dp = dp - d_ent * (np.log(p + 1e-9) + p / (p + 1e-9)) / T
+    ds = dp / Z - (dp * s).sum(axis=-1, keepdims=True) / Z ** 2
+    dl = dl + ds * s * (1.0 - s)
+    return dl.reshape(T, N)
+
+
+def shared_forward64(x, w_gate, w_up, w_down, n_shared: int):
+    """``_shared_ffn`` (``moe.py:161-168``) in float64: one SwiGLU for 2-D
+    weights, the mean of ``n_shared`` SwiGLUs for 3-D ones."""
+    x = np.asarray(x, F64)
+    if n_shared == 1:
+        w_gate, w_up, w_down = (np.asarray(w, F64)[None] for w in (w_gate, w_up, w_down))
+    out = 0.0
+    for i in range(n_shared):
+        g = x @ np.asarray(w_gate[i], F64)
+        u = x @ np.asarray(w_up[i], F64)
+        out = out + (silu64(g) * u) @ np.asarray(w_down[i], F64)
+    return out / n_shared
+
+
+def shared_bwd(x, w_gate, w_up, w_down, n_shared: int, dy, precision: str = "bf16") -> dict:
+    """VJP of the shared expert(s) (``moe.py:161-168``, added with weight 1 at
+    ``:249-251``) for the float32 cotangent ``dy`` of the layer output.
+
+    Each SwiGLU returns ``f32(bf16 out)`` (``moe.py:23-29``), so its output
+    cotangent is ``bf16(dy / n_shared)``; the rest is :func:`expert_ffn_bwd`
+    with one segment holding every token.  Returns ``dx [T, D]`` and
+    ``dWg``, ``dWu``, ``dWd`` in the parameter shapes (2-D for one shared
+    expert, stacked for several), plus ``d_out`` (the per-expert cotangent).
+    """
+    x = np.asarray(x)
+    T = x.shape[0]
+    dy = np.asarray(dy, F32 if precision == "bf16" else F64)
+    d_out = _r(dy / dy.dtype.type(n_shared), precision)
+    stack = n_shared > 1
+    ws = [(w_gate[i], w_up[i], w_down[i]) for i in range(n_shared)] if stack \
+        else [(w_gate, w_up, w_down)]
+    dx = np.zeros(x.shape, F64)
+    grads = {"dWg": [], "dWu": [], "dWd": []}
+    for wg_, wu_, wd_ in ws:
+        r = expert_ffn_bwd(x, np.array([0, T]), np.asarray(wg_)[None], np.asarray(wu_)[None],
+                           np.asarray(wd_)[None], d_out, precision)
+        dx = dx + r["d_xs"]
+        for k in grads:
+            grads[k].append(r[k][0])
+    dt = F32 if precision == "bf16" else F64
+    res = {k: (np.stack(v) if stack else v[0]).astype(dt) for k, v in grads.items()}
+    res["dx"] = dx.astype(dt)
+    res["d_out"] = d_out
+    return res
+
+
+# --------------------------------------------------------------------------
 # composed routed layer
 # --------------------------------------------------------------------------
 
@@ -260,15 +366,19 @@ def routed_forward64(x, router_w, wg, wu, wd, top_idx, slot_pos, perm_src, offse
 
 
 def moe_backward(x, params: dict, dy, fwd: dict, *, routing: str = "softmax",
-                 rsf: float = 1.0, precision: str = "bf16") -> dict:
-    """VJP of the routed MoE layer (``moe.py:170-246``, shared expert and aux
-    losses excluded) for the cotangent ``dy`` of ``out``.
+                 rsf: float = 1.0, precision: str = "bf16", n_shared: int = 0,
+                 batch_shape=None, d_aux=None) -> dict:
+    """VJP of the MoE layer (``moe.py:170-294``) for the cotangent ``dy`` of
+    ``out`` and, optionally, ``d_aux = (d_z, d_bal, d_ent)`` of the aux losses
+    (with ``batch_shape = (B, S)``; ``:253-283``).
 
     ``fwd`` is :func:`moe_oracle.moe_forward`'s result (logits, top_idx,
-    gates, plan, xs, ys).  Returns ``dx [T, D]`` (experts + router),
-    ``d_router [D, N]``, ``dWg``, ``dWu [N, D, F]``, ``dWd [N, F, D]`` and the
-    intermediates ``d_ys``, ``d_gates``, ``d_logits``, ``d_xs``, ``dx_experts``,
-    ``dx_router``.
+    gates, plan, xs, ys).  ``n_shared > 0`` adds the shared expert's VJP
+    (``params["shared_w_*"]``).  Returns ``dx [T, D]`` (experts + router +
+    shared), ``d_router [D, N]``, ``dWg``, ``dWu [N, D, F]``, ``dWd [N, F, D]``,
+    ``dWg_shared``/``dWu_shared``/``dWd_shared`` when there is a shared expert,
+    and the intermediates ``d_ys``, ``d_gates``, ``d_logits``, ``d_xs``,
+    ``dx_experts``, ``dx_router``.
     """
     x = np.asarray(x, F32)
     T = x.shape[0]
@@ -283,9 +393,22 @@ def moe_backward(x, params: dict, dy, fwd: dict, *, routing: str = "softmax",
         dl = route_softmax_bwd(fwd["logits"], fwd["top_idx"], fwd["gates"], d_g)
     else:
         dl = route_sigmoid_bwd(fwd["logits"], fwd["top_idx"], d_g, rsf)
+    if d_aux is not None:
+        B, S = batch_shape
+        dl = dl + aux_bwd(fwd["logits"], fwd["top_idx"], B, S, *d_aux)
     d_router, dx_r = router_bwd(x, params["router"], dl)
     dt = F32 if precision == "bf16" else F64
-    return {"dx": (np.asarray(dx_e, F64) + dx_r).astype(dt), "d_router": d_router.astype(dt),
-            "dWg": ex["dWg"], "dWu": ex["dWu"], "dWd": ex["dWd"], "d_ys": d_ys,
-            "d_gates": d_g, "d_logits": dl.astype(dt), "d_xs": ex["d_xs"],
-            "dx_experts": dx_e, "dx_router": dx_r.astype(dt), "expert": ex}
+    dx = np.asarray(dx_e, F64) + dx_r
+    res = {}
+    if n_shared > 0:
+        xc = bf16_round(x) if precision == "bf16" else x
+        sh = shared_bwd(xc, params["shared_w_gate"], params["shared_w_up"],
+                        params["shared_w_down"], n_shared, dy, precision)
+        dx = dx + sh["dx"]
+        res = {"dWg_shared": sh["dWg"], "dWu_shared": sh["dWu"], "dWd_shared": sh["dWd"],
+               "dx_shared": sh["dx"], "d_shared_out": sh["d_out"]}
+    res.update({"dx": dx.astype(dt), "d_router": d_router.astype(dt),
+                "dWg": ex["dWg"], "dWu": ex["dWu"], "dWd": ex["dWd"], "d_ys": d_ys,
+                "d_gates": d_g, "d_logits": dl.astype(dt), "d_xs": ex["d_xs"],
+                "dx_experts": dx_e, "dx_router": dx_r.astype(dt), "expert": ex})
+    return res

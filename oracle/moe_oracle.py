@@ -543,9 +543,10 @@ def shared_expert(x_flat, w_gate, w_up, w_down, n_shared: int, precision: str = 
             x64 = x.astype(F64)
             return ((silu(x64 @ np.asarray(wg, F64)) * (x64 @ np.asarray(wu, F64)))
                     @ np.asarray(wd, F64)).astype(F32)
-        g = bf16_round(silu(bf16_round(x @ bf16_round(wg))))
+        # the routed experts' rounding points (expert_ffn "bf16")
+        g = bf16_round(x @ bf16_round(wg))
         u = bf16_round(x @ bf16_round(wu))
-        h = bf16_round(g * u)
+        h = bf16_round(silu(g).astype(F32) * u)
         return bf16_round(h @ bf16_round(wd))
 
     if n_shared == 1:

@@ -1,5 +1,4 @@
-"""Parity of the HIP backward (data gradients) against the backward oracle
-(needs an MI355X).
+"""Parity of the HIP backward against the backward oracle (needs an MI355X).
 
 The combine VJP's bf16 cotangent rows and the gather VJP are compared bit for
 bit (their rounding points are fixed: one float32 product, one bf16
@@ -20,6 +19,7 @@ from oracle import moe_backward as B
 from hanuman_amd import _lib
 from hanuman_amd import kernels as K
 from hanuman_amd.backward import BackwardOperands, moe_backward_data, moe_backward_weights
+from hanuman_amd.moe import MoE
 
 pytestmark = pytest.mark.gpu
 
@@ -61,8 +61,16 @@ def test_combine_bwd(gpu, T, D, N, Kk, cf):
     ys = O.bf16_round(rng.standard_normal((R, D)).astype(np.float32))
     gates = rng.uniform(0.0, 1.0, (T, Kk)).astype(np.float32)
     dy = rng.standard_normal((T, D)).astype(np.float32)
-    d_ys, d_g = K.combine_bwd(dev_f32(dy, gpu), dev_bf16(ys, gpu), plan, dev_f32(gates, gpu))
+    n_sh = 0 if Kk == 1 else (1 if Kk == 4 else 3)
+    d_ys, d_g, d_sh = K.combine_bwd(dev_f32(dy, gpu), dev_bf16(ys, gpu), plan, dev_f32(gates, gpu),
+                                    n_shared=n_sh)
     torch.cuda.synchronize()
+    if n_sh == 0:
+        assert d_sh is None
+    else:
+        # the shared expert's output cotangent, bf16(dy / n_shared), bit for bit
+        ref_sh = O.bf16_round((dy / np.float32(n_sh)).astype(np.float32))
+        assert np.array_equal(host(d_sh).view(np.uint32), ref_sh.view(np.uint32)), "d_shared"
     r_ys, r_g = B.combine_bwd(dy, ys, ref_plan["slot_pos"], gates, T, Kk, "bf16")
     kept = int(ref_plan["offsets"][-1])
     got = host(d_ys)[:kept]
@@ -168,6 +176,10 @@ def test_gather_bwd_bit_exact(gpu, T, D, N, Kk, cf):
     dx = host(K.gather_bwd(dev_bf16(d_xs, gpu), plan))
     ref = B.gather_bwd(d_xs, ref_plan["slot_pos"], T, Kk, "bf16")
     assert np.array_equal(dx.view(np.uint32), ref.view(np.uint32))
+    # with the shared expert's input gradient added last (float32)
+    res = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    dx2 = host(K.gather_bwd(dev_bf16(d_xs, gpu), plan, residual=dev_bf16(res, gpu)))
+    assert np.array_equal(dx2.view(np.uint32), (ref + res).astype(np.float32).view(np.uint32))
 
 
 @pytest.mark.parametrize("mode", ["softmax", "sigmoid"])
@@ -300,3 +312,98 @@ def test_router_dw(gpu, x_dtype):
     got = host(K.router_dw(xd, dev_f32(dl, gpu)))
     ref = x.astype(np.float64).T @ dl.astype(np.float64)
     assert O.normwise_rel_err(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("Bq,Sq,N,Kk", [(2, 300, 64, 8), (3, 70, 200, 6), (1, 64, 8, 2)])
+def test_router_aux_bwd(gpu, Bq, Sq, N, Kk):
+    rng = np.random.default_rng(Bq * Sq + N)
+    T = Bq * Sq
+    logits = (1.5 * rng.standard_normal((T, N))).astype(np.float32)
+    idx = O.topk_desc(logits, Kk)
+    d_losses = np.array([0.7, -1.3, 0.4], np.float32)
+    ref = B.aux_bwd(logits, idx, Bq, Sq, *[float(v) for v in d_losses])
+    lg, ix, dl = dev_f32(logits, gpu), torch.from_numpy(idx).to(gpu), dev_f32(d_losses, gpu)
+    got = host(K.router_aux_bwd(lg, ix, Bq, Sq, dl))
+    tol = dict(rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+    np.testing.assert_allclose(got, ref, **tol)
+    base = rng.standard_normal((T, N)).astype(np.float32)
+    acc = host(K.router_aux_bwd(lg, ix, Bq, Sq, dl, dev_f32(base, gpu)))
+    np.testing.assert_allclose(acc, base + ref, **tol)
+
+
+def test_gate_up_raw_matches_gather(gpu):
+    """The non-gather recompute on the dispatched rows equals the gathering
+    one bit for bit (same tiles, same accumulation order)."""
+    rng = np.random.default_rng(21)
+    T, D, N, Kk, F = 600, 512, 8, 2, 256
+    x, w, wg, wu, wd, logits, idx, gates, ref_plan, plan = expert_problem(gpu, rng, T, D, N, Kk, F, 1.25)
+    xd = dev_bf16(x, gpu)
+    wgu = K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    a = K.grouped_gate_up_raw_gather(xd, plan, wgu)
+    b = K.grouped_gate_up_raw(K.permute_rows(xd, plan), plan.offsets, wgu)
+    torch.cuda.synchronize()
+    kept = int(ref_plan["offsets"][-1])
+    assert torch.equal(a[:kept], b[:kept])
+
+
+@pytest.mark.parametrize("n_shared,cf", [(1, None), (2, 1.0)])
+def test_module_autograd_matches_oracle(gpu, n_shared, cf):
+    """MoE.__call__ under torch autograd: loss = <dy, out> + c_z z_loss +
+    c_b balance_loss (train.py:191-200), backward through the library's VJP
+    of the whole module, every gradient against the bf16-mode oracle fed
+    with the forward's own routing."""
+    Bq, Sq, D, F, N, Kk = 2, 160, 256, 256, 8, 2
+    m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.bfloat16, rngs=1, device=gpu,
+            capacity_factor=cf)
+    m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))
+    names = ("router", "expert_w_gate", "expert_w_up", "expert_w_down",
+             "shared_w_gate", "shared_w_up", "shared_w_down")
+    for n in names:
+        getattr(m, n).value.requires_grad_(True)
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(Bq, Sq, D, generator=gen, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(Bq, Sq, D, generator=gen, device=gpu)
+    c_z, c_b = 0.37, 0.81
+    print(f"module autograd n_shared={n_shared} cf={cf}", flush=True)
+    out, aux = m(x)
+    loss = (out * dy).sum() + c_z * aux["router_z_loss"] + c_b * aux["balance_loss"]
+    loss.backward()
+    torch.cuda.synchronize()
+    assert out.grad_fn is not None and x.grad is not None and x.grad.dtype == torch.bfloat16
+    with torch.no_grad():
+        _, _, _, sv = m._forward(x.detach(), save=True)
+    T = Bq * Sq
+    idx = host(sv["top_idx"])
+    cap = O.capacity_of(T, Kk, N, cf)
+    ref_plan = O.dispatch_plan(idx, N, cap)
+    xn = host(x.detach()).reshape(T, D)
+    p = {n: getattr(m, n).value.detach().float().cpu().numpy() for n in names}
+    ref_fwd = {"logits": host(sv["logits"]), "top_idx": idx, "gates": host(sv["gates"]),
+               "plan": ref_plan, "xs": O.permute_rows(xn, ref_plan["perm_src"], Kk),
+               "ys": host(sv["ys"])}
+    ref = B.moe_backward(xn, p, host(dy).reshape(T, D), ref_fwd, routing="sigmoid", rsf=2.5,
+                         precision="bf16", n_shared=n_shared, batch_shape=(Bq, Sq),
+                         d_aux=(c_z, c_b, 0.0))
+    pairs = [("dx", x.grad, ref["dx"]), ("d_router", m.router.value.grad, ref["d_router"]),
+             ("dWg", m.expert_w_gate.value.grad, ref["dWg"]),
+             ("dWu", m.expert_w_up.value.grad, ref["dWu"]),
+             ("dWd", m.expert_w_down.value.grad, ref["dWd"]),
+             ("dWg_shared", m.shared_w_gate.value.grad, ref["dWg_shared"]),
+             ("dWu_shared", m.shared_w_up.value.grad, ref["dWu_shared"]),
+             ("dWd_shared", m.shared_w_down.value.grad, ref["dWd_shared"])]
+    for name, got, want in pairs:
+        got = host(got).reshape(np.shape(want))
+        err = O.normwise_rel_err(got, want)
+        print(f"  {name}: normwise {err:.2e}", flush=True)
+        assert err < 2e-2, (name, err)
+    # the aux terms alone reach the router: a loss of only the aux losses
+    for n in names:
+        getattr(m, n).value.grad = None
+    out, aux = m(x.detach())
+    (c_z * aux["router_z_loss"] + c_b * aux["balance_loss"]).backward()
+    torch.cuda.synchronize()
+    ref_aux = B.router_bwd(xn, p["router"], B.aux_bwd(host(sv["logits"]), idx, Bq, Sq, c_z, c_b))[0]
+    err = O.normwise_rel_err(host(m.router.value.grad), ref_aux)
+    print(f"  d_router (aux only): normwise {err:.2e}", flush=True)
+    assert err < 1e-4
+    assert float(m.expert_w_gate.value.grad.abs().max()) == 0.0

@@ -209,3 +209,131 @@ def test_bf16_mode_tracks_fp64():
     g64 = B.moe_backward(x, params, dy, fwd, routing="softmax", precision="fp64")
     for k in ("dx", "d_router", "dWg", "dWu", "dWd", "d_gates"):
         assert O.normwise_rel_err(np.asarray(g16[k], np.float64), np.asarray(g64[k], np.float64)) < 2e-2, k
+
+
+def test_aux_bwd():
+    """All three aux terms, two sequences, counts from fixed top-k indices."""
+    rng = np.random.default_rng(8)
+    Bq, Sq, N, K = 2, 6, 7, 3
+    logits = 1.5 * rng.standard_normal((Bq * Sq, N))
+    idx = O.topk_desc(logits.astype(np.float32), K)
+    d_z, d_bal, d_ent = 0.7, -1.3, 0.4
+    dl = B.aux_bwd(logits, idx, Bq, Sq, d_z, d_bal, d_ent)
+
+    def f(p):
+        z, bal, ent = B.aux_forward64(p, idx, Bq, Sq)
+        return d_z * z + d_bal * bal + d_ent * ent
+
+    for _ in range(3):
+        v = rng.standard_normal(logits.shape)
+        close((dl * v).sum(), fd(f, logits, v))
+    # each term alone (a dropped term shows here even if the others cancel it)
+    for dz_, db_, de_ in ((1.0, 0.0, 0.0), (0.0, 1.0, 0.0), (0.0, 0.0, 1.0)):
+        dl1 = B.aux_bwd(logits, idx, Bq, Sq, dz_, db_, de_)
+        v = rng.standard_normal(logits.shape)
+
+        def f1(p):
+            z, bal, ent = B.aux_forward64(p, idx, Bq, Sq)
+            return dz_ * z + db_ * bal + de_ * ent
+
+        close((dl1 * v).sum(), fd(f1, logits, v))
+
+
+def test_aux_forward64_matches_forward_oracle():
+    rng = np.random.default_rng(9)
+    Bq, Sq, N, K = 3, 5, 6, 2
+    logits = rng.standard_normal((Bq * Sq, N)).astype(np.float32)
+    idx = O.topk_desc(logits, K)
+    scores = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    ref = O.aux_losses(logits, scores, idx, Bq, Sq, N)
+    z, bal, ent = B.aux_forward64(logits, idx, Bq, Sq)
+    np.testing.assert_allclose([z, bal, ent],
+                               [ref["router_z_loss"], ref["balance_loss"], ref["mean_entropy"]],
+                               rtol=1e-12)
+
+
+@pytest.mark.parametrize("n_shared", [1, 3])
+def test_shared_bwd(n_shared):
+    rng = np.random.default_rng(10 + n_shared)
+    T, D, F = 7, 12, 10
+    x = rng.standard_normal((T, D))
+    shape = (lambda *s: s) if n_shared == 1 else (lambda *s: (n_shared,) + s)
+    wg = 0.3 * rng.standard_normal(shape(D, F))
+    wu = 0.3 * rng.standard_normal(shape(D, F))
+    wd = 0.3 * rng.standard_normal(shape(F, D))
+    dy = rng.standard_normal((T, D))
+    r = B.shared_bwd(x, wg, wu, wd, n_shared, dy, "fp64")
+    base = [x, wg, wu, wd]
+    for name, pos in (("dx", 0), ("dWg", 1), ("dWu", 2), ("dWd", 3)):
+        assert r[name].shape == base[pos].shape
+        v = rng.standard_normal(base[pos].shape)
+
+        def f(p, pos=pos):
+            a = list(base)
+            a[pos] = p
+            return (dy * B.shared_forward64(*a, n_shared)).sum()
+
+        close((r[name] * v).sum(), fd(f, base[pos], v))
+
+
+def test_shared_forward64_matches_forward_oracle():
+    rng = np.random.default_rng(12)
+    T, D, F = 5, 8, 6
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    w = [0.3 * rng.standard_normal(s) for s in ((2, D, F), (2, D, F), (2, F, D))]
+    np.testing.assert_allclose(B.shared_forward64(x, *w, 2),
+                               O.shared_expert(x, *w, 2, precision="fp32"), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n_shared", [1, 2])
+def test_moe_backward_module_with_shared_and_aux(n_shared):
+    """The whole module (routed + shared + aux losses, reference sigmoid
+    routing, two sequences) against finite differences of its float64
+    forward with the routing held fixed."""
+    rng, x, w, wg, wu, wd, idx, plan = tiny_problem(13, T=12, cf=0.8)
+    T, K = idx.shape
+    D, F = x.shape[1], wg.shape[2]
+    Bq, Sq = 2, 6
+    rsf = 2.5
+    shp = (lambda *s: s) if n_shared == 1 else (lambda *s: (n_shared,) + s)
+    swg = 0.3 * rng.standard_normal(shp(D, F))
+    swu = 0.3 * rng.standard_normal(shp(D, F))
+    swd = 0.3 * rng.standard_normal(shp(F, D))
+    args = dict(top_idx=idx, slot_pos=plan["slot_pos"], perm_src=plan["perm_src"],
+                offsets=plan["offsets"], routing="sigmoid", rsf=rsf)
+    dy = rng.standard_normal((T, D))
+    d_aux = (0.3, 0.8, -0.5)
+    logits = x @ w
+    sel = np.take_along_axis(logits, idx, axis=1)
+    s = 1.0 / (1.0 + np.exp(-sel))
+    gates = rsf * s / (s.sum(axis=1, keepdims=True) + 1e-9)
+    xs = O.permute_rows(x, plan["perm_src"], K)
+    ys = np.zeros((xs.shape[0], D))
+    off = plan["offsets"]
+    for ex in range(len(off) - 1):
+        a, b = off[ex], off[ex + 1]
+        ys[a:b] = (B.silu64(xs[a:b] @ wg[ex]) * (xs[a:b] @ wu[ex])) @ wd[ex]
+    fwd = {"logits": logits, "top_idx": idx, "gates": gates, "plan": plan, "xs": xs, "ys": ys}
+    params = {"router": w, "expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd,
+              "shared_w_gate": swg, "shared_w_up": swu, "shared_w_down": swd}
+    g = B.moe_backward(x, params, dy, fwd, routing="sigmoid", rsf=rsf, precision="fp64",
+                       n_shared=n_shared, batch_shape=(Bq, Sq), d_aux=d_aux)
+
+    def L(x_, w_, wg_, wu_, wd_, swg_, swu_, swd_):
+        out = B.routed_forward64(x_, w_, wg_, wu_, wd_, **args) \
+            + B.shared_forward64(x_, swg_, swu_, swd_, n_shared)
+        z, bal, ent = B.aux_forward64(x_ @ w_, idx, Bq, Sq)
+        return (dy * out).sum() + d_aux[0] * z + d_aux[1] * bal + d_aux[2] * ent
+
+    base = [x, w, wg, wu, wd, swg, swu, swd]
+    names = ("dx", "d_router", "dWg", "dWu", "dWd", "dWg_shared", "dWu_shared", "dWd_shared")
+    for pos, name in enumerate(names):
+        assert g[name].shape == base[pos].shape, name
+        v = rng.standard_normal(base[pos].shape)
+
+        def f(p, pos=pos):
+            a = list(base)
+            a[pos] = p
+            return L(*a)
+
+        close((g[name] * v).sum(), fd(f, base[pos], v), rtol=1e-5)
