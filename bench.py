@@ -367,7 +367,7 @@ def bench_backward(args, name, wl, layer):
     N = wl.n_experts
     # with router logits given (no router weight) the VJP ends at d_logits
     has_router = layer.router_w is not None
-    stages = (["combine_bwd", "gate_up_recompute", "dgrad_down", "swiglu_bwd", "dgrad_gate_up",
+    stages = (["combine_bwd", "dgrad_down", "recompute_swiglu_bwd", "dgrad_gate_up",
                "gather_bwd", "router_bwd"] + (["router_dx"] if has_router else [])
               + ["permute_xs", "wgrad_gate_up", "wgrad_down"] + (["router_dw"] if has_router else []))
     dw_ws = torch.empty(max(int(_lib.lib().hmoe_router_dw_workspace_bytes(wl.tokens, wl.d_model, N)), 1),
@@ -383,11 +383,9 @@ def bench_backward(args, name, wl, layer):
         mark()
         d_ys, d_g, _ = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"])
         mark()
-        gu = K.grouped_gate_up_raw_gather(layer.x, plan, layer.w_gate_up)
-        mark()
         dh = K.grouped_dgrad_down(d_ys, plan.offsets, ops.w_down_dgrad)
         mark()
-        dgu = K.swiglu_bwd(dh, gu, plan.offsets)
+        dgu = K.grouped_gate_up_swiglu_bwd_gather(layer.x, plan, layer.w_gate_up, dh)
         mark()
         d_xs = K.grouped_dgrad_gate_up(dgu, plan.offsets, ops.w_gate_up_dgrad)
         mark()
@@ -436,9 +434,8 @@ def bench_backward(args, name, wl, layer):
     w_b = 2 if wl.router_w_dtype == "bf16" else 4
     work = {
         "combine_bwd": ("hbm", T * D * 4 + 2 * kept * D * 2 + R * 8, HBM_PEAK_GBS),
-        "gate_up_recompute": ("mfma", 4 * kept * D * F, BF16_PEAK_TFLOPS),
         "dgrad_down": ("mfma", 2 * kept * D * F, BF16_PEAK_TFLOPS),
-        "swiglu_bwd": ("hbm", kept * (F * 2 + 2 * F * 2 * 2), HBM_PEAK_GBS),
+        "recompute_swiglu_bwd": ("mfma", 4 * kept * D * F, BF16_PEAK_TFLOPS),
         "dgrad_gate_up": ("mfma", 4 * kept * D * F, BF16_PEAK_TFLOPS),
         "gather_bwd": ("hbm", kept * D * 2 + T * D * 4 + R * 4, HBM_PEAK_GBS),
         "router_bwd": ("hbm", T * N * 4 * 2 + T * K_ * 12, HBM_PEAK_GBS),

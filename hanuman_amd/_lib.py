@@ -64,6 +64,9 @@ SIGNATURES = {
     "hmoe_grouped_gate_up_raw_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32, _i32,
                                                _vp, _vp, _vp]),
     "hmoe_grouped_gate_up_raw": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_swiglu_bwd_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32,
+                                                      _i32, _vp, _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_swiglu_bwd": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hmoe_swiglu_bwd": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp]),
     "hmoe_pack_down_dgrad": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "hmoe_pack_gate_up_dgrad": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),

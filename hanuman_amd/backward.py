@@ -22,7 +22,10 @@ and the weight gradients (:func:`moe_backward_weights`):
                               dWg|dWu = xs^T dg|du  hmoe_grouped_wgrad_gate_up
     router   (moe.py:178)     d_router = x^T d_l hmoe_router_dw
 
-and, in :func:`moe_backward` (the whole module), the shared expert
+(:func:`moe_backward_data` keeps these steps apart and returns their
+intermediates; :func:`moe_backward` runs the recompute and the SwiGLU VJP as
+one GEMM, ``hmoe_grouped_gate_up_swiglu_bwd_gather``, so that g and u never
+reach HBM) and, in :func:`moe_backward` (the whole module), the shared expert
 (``moe.py:161-168, 249-251``: the same grouped kernels with one segment of
 all tokens, its output cotangent ``bf16(dy / n_shared)`` from
 ``hmoe_combine_bwd``) and the aux losses (``moe.py:253-283``,
@@ -120,9 +123,8 @@ def shared_backward(xc: torch.Tensor, d_shared: torch.Tensor, h_shared, ops: Sha
     off = torch.tensor([0, T], dtype=torch.int32, device=xc.device)
     dxs, dwg, dwu, dwd = [], [], [], []
     for (fwd_gu, gu_dgrad, down_dgrad), h in zip(ops.experts, h_shared):
-        gu = K.grouped_gate_up_raw(xc, off, fwd_gu)
         dh = K.grouped_dgrad_down(d_shared, off, down_dgrad)
-        dgu = K.swiglu_bwd(dh, gu, off)
+        dgu = K.grouped_gate_up_swiglu_bwd(xc, off, fwd_gu, dh)
         dxs.append(K.grouped_dgrad_gate_up(dgu, off, gu_dgrad))
         g_, u_ = K.grouped_wgrad_gate_up(xc, dgu, off)
         dwg.append(g_)
@@ -160,10 +162,9 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
     xc = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)   # x.astype(dtype), moe.py:198
     n_sh = shared.n_shared if shared is not None else 0
     d_ys, d_gates, d_sh = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"], n_sh)
-    gu = K.grouped_gate_up_raw_gather(xc, plan, w_gate_up)
     dh = K.grouped_dgrad_down(d_ys, plan.offsets, ops.w_down_dgrad)
-    dgu = K.swiglu_bwd(dh, gu, plan.offsets)
-    del gu, dh
+    dgu = K.grouped_gate_up_swiglu_bwd_gather(xc, plan, w_gate_up, dh)
+    del dh
     d_xs = K.grouped_dgrad_gate_up(dgu, plan.offsets, ops.w_gate_up_dgrad)
     res = {}
     residual = None

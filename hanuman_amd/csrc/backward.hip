@@ -145,9 +145,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
         const float d = __uint_as_float(h ? (hv[q] & 0xffff0000u) : (hv[q] << 16));
         const float gg = __uint_as_float(h ? (gv[q] & 0xffff0000u) : (gv[q] << 16));
         const float uu = __uint_as_float(h ? (uv[q] & 0xffff0000u) : (uv[q] << 16));
-        const float s = 1.0f / (1.0f + expf(-gg));
-        dgq[h] = d * uu * (s * (1.0f + gg * (1.0f - s)));
-        duq[h] = d * (gg * s);
+        swiglu_vjp(d, gg, uu, dgq[h], duq[h]);
       }
       og[q] = pack_bf16x2(dgq[0], dgq[1]);
       ou[q] = pack_bf16x2(duq[0], duq[1]);

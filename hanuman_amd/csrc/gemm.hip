@@ -371,6 +371,90 @@ __device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4],
   barrier_lds();
 }
 
+// The recompute of the backward with the SwiGLU VJP fused (C = dgu, ldc = 2F):
+// the accumulators are g and u, rounded to bf16 as the forward's outputs are,
+// the tile's dh [256 rows][128 h columns] comes from global memory straight
+// into registers (each lane the 4 h columns of its accumulator groups, 8-byte
+// range-checked buffer loads issued before any arithmetic; rows past the
+// segment read zeros), and dg, du (swiglu_vjp) go out in g and u's places
+// through the same two 128-row LDS passes as store_tile_lds.
+__device__ __forceinline__ void store_tile_lds_dswiglu(const f32x16 (&acc)[4][4], uint8_t* lds,
+                                                       uint16_t* __restrict__ C, int64_t ldc,
+                                                       const uint16_t* __restrict__ dh,
+                                                       int64_t row0, int64_t row_end, int n0,
+                                                       int wm, int wn, int lane, int tid) {
+  const int frow = lane & 31;
+  const int half = lane >> 5;
+  const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
+  const int f = static_cast<int>(ldc / 2);
+  const __amdgpu_buffer_rsrc_t dh_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(dh + row0 * f), 0, static_cast<int>(nrows * f * 2), kBufferWord3);
+  const int hc = (n0 + wn * 128) / 2 + half * 4;
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  // dh of pass q's accumulator rows (i = 2q, 2q+1); pass 1's loads go out
+  // right after pass 0's LDS writes, so they fly while pass 0 is stored.
+  u32x2_t dv[2][2][4];
+  auto load_dh = [&](int q) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          dv[ii][p][g] = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                           dh_rsrc, ((wm * 128 + (2 * q + ii) * 32 + frow) * f + hc + p * 32 + g * 8) * 2,
+                           0, 0));
+  };
+  load_dh(0);
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
+  const int row_bytes = static_cast<int>(ldc * 2);
+  const int c = tid & 31;
+  const int voff = ((tid >> 5) * static_cast<int>(ldc) + n0 + c * 8) * 2;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * q + ii;
+      const int l = wm * 64 + ii * 32 + frow;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float dg[4], du[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t w = dv[ii][p][g][r >> 1];
+            const float d = __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+            const uint32_t gu = pack_bf16x2_rne(acc[i][2 * p][g * 4 + r], acc[i][2 * p + 1][g * 4 + r]);
+            swiglu_vjp(d, __uint_as_float(gu << 16), __uint_as_float(gu & 0xffff0000u), dg[r], du[r]);
+          }
+          uint2 pg, pu;
+          pg.x = pack_bf16x2_rne(dg[0], dg[1]);
+          pg.y = pack_bf16x2_rne(dg[2], dg[3]);
+          pu.x = pack_bf16x2_rne(du[0], du[1]);
+          pu.y = pack_bf16x2_rne(du[2], du[3]);
+          const int cg = wn * 16 + 2 * p * 4 + g;
+          const int cu = cg + 4;
+          *reinterpret_cast<uint2*>(lds + l * 512 + ((cg ^ (l & 31)) * 16) + half * 8) = pg;
+          *reinterpret_cast<uint2*>(lds + l * 512 + ((cu ^ (l & 31)) * 16) + half * 8) = pu;
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (q == 0) load_dh(1);
+    barrier_lds();
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int l = m * 8 + (tid >> 5);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(lds + l * 512 + ((c ^ (l & 31)) * 16));
+      const int trow0 = (m >> 3) * 128 + q * 64 + (m & 7) * 8;
+      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, __builtin_amdgcn_readfirstlane(trow0 * row_bytes), 0);
+    }
+    barrier_lds();
+  }
+}
+
 // Main loop with direct global -> LDS loads (used for the e4m3 operands,
 // whose 32-byte MFMA fragments leave no registers for load staging): the next
 // K step's A and B tiles (2 x 32 KB) go straight into the other LDS stage with
@@ -575,13 +659,16 @@ struct IntC {
 // alternate statically.  GATHER: A is the token matrix x and row r of the
 // dispatched operand is x[gather_src[r] / gather_k] (gather_src = perm_src,
 // -1 past the kept rows), so the row permutation is done by the GEMM's own
-// loads and the dispatched copy of x is never written.
-template <bool SWIGLU, bool ODD, bool GATHER>
+// loads and the dispatched copy of x is never written.  DSWIGLU (backward,
+// without SWIGLU): the epilogue is store_tile_lds_dswiglu with dh.
+template <bool SWIGLU, bool ODD, bool GATHER, bool DSWIGLU = false>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
     uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n,
-    const int32_t* __restrict__ gather_src, int gather_k, int gather_rows) {
+    const int32_t* __restrict__ gather_src, int gather_k, int gather_rows,
+    const uint16_t* __restrict__ dh) {
+  static_assert(!(SWIGLU && DSWIGLU), "the SwiGLU VJP epilogue takes the raw g, u tile");
   typedef GemmElem<false> E;
   constexpr int kParts = 4 / E::kSub;  // load parts per MFMA sub-step
   // The two stages live in dynamic LDS: stage g & 1 holds global K step g.
@@ -818,7 +905,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     // stage 1 is idle here: the tile's last step (odd) read it, step 0 of the
     // next tile writes it only after the epilogue's last barrier
-    if constexpr (SWIGLU)
+    if constexpr (DSWIGLU)
+      store_tile_lds_dswiglu(acc, smem + kStageBytes, C, ldc, dh, row0, row_end, n0, wm, wn, lane,
+                             tid);
+    else if constexpr (SWIGLU)
       store_tile_lds_swiglu<false>(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane,
                                    tid, nullptr);
     else
@@ -1102,6 +1192,10 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_regs<true, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<false, false, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, false, false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, true, false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, false, true, true>),
+      reinterpret_cast<const void*>(grouped_gemm_regs<false, true, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_dma<false, true>),
       reinterpret_cast<const void*>(grouped_gemm_wgrad<false>),
@@ -1120,8 +1214,10 @@ int allow_dynamic_lds(int dev) {
 int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const float* a_scale,
                    const float* b_scale, const int32_t* offsets, int n_experts, int64_t rows_cap,
                    int kdim, int ncols, void* C, int64_t ldc, hipStream_t s, const char* what,
-                   const int32_t* gather_src = nullptr, int gather_k = 1, int gather_rows = 1) {
+                   const int32_t* gather_src = nullptr, int gather_k = 1, int gather_rows = 1,
+                   const uint16_t* dswiglu_dh = nullptr) {
   const int n_tiles_n = ncols / kBN;
+  HMOE_REQUIRE(dswiglu_dh == nullptr || (!swiglu && !fp8), "%s: SwiGLU VJP epilogue needs the raw bf16 GEMM", what);
   const int64_t max_tiles = (ceil_div(rows_cap, kBM) + n_experts) * n_tiles_n;
   HMOE_REQUIRE(max_tiles < (int64_t(1) << 31), "%s: too many tiles", what);
   HMOE_REQUIRE(rows_cap < (int64_t(1) << 31), "%s: rows_cap must fit in int32", what);
@@ -1145,11 +1241,16 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
       hipLaunchKernelGGL((grouped_gemm_dma<false, true>), dim3(grid), dim3(kThreads), lds, s, a, b,
                          a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n);
   } else {
-#define HMOE_LAUNCH_REGS(SW, OD, GA)                                                              \
-  hipLaunchKernelGGL((grouped_gemm_regs<SW, OD, GA>), dim3(grid), dim3(kThreads), lds, s, a, b,  \
-                     offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n, gather_src,     \
-                     gather_k, gather_rows)
-    if (gather_src != nullptr) {
+#define HMOE_LAUNCH_REGS(SW, OD, GA, ...)                                                         \
+  hipLaunchKernelGGL((grouped_gemm_regs<SW, OD, GA, ##__VA_ARGS__>), dim3(grid), dim3(kThreads),   \
+                     lds, s, a, b, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n,  \
+                     gather_src, gather_k, gather_rows, dswiglu_dh)
+    if (dswiglu_dh != nullptr) {
+      if (gather_src != nullptr && odd) HMOE_LAUNCH_REGS(false, true, true, true);
+      else if (gather_src != nullptr) HMOE_LAUNCH_REGS(false, false, true, true);
+      else if (odd) HMOE_LAUNCH_REGS(false, true, false, true);
+      else HMOE_LAUNCH_REGS(false, false, false, true);
+    } else if (gather_src != nullptr) {
       if (swiglu && odd) HMOE_LAUNCH_REGS(true, true, true);
       else if (swiglu) HMOE_LAUNCH_REGS(true, false, true);
       else if (odd) HMOE_LAUNCH_REGS(false, true, true);
@@ -1276,6 +1377,57 @@ extern "C" int hmoe_grouped_gate_up_raw(const void* xs, const int32_t* offsets, 
   return launch_grouped(false, false, xs, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
                         rows_cap, d_model, 2 * d_ff, gu, 2 * d_ff, static_cast<hipStream_t>(stream),
                         "hmoe_grouped_gate_up_raw");
+}
+
+extern "C" int hmoe_grouped_gate_up_swiglu_bwd_gather(
+    const void* x, int64_t tokens, int top_k, const int32_t* perm_src, const int32_t* offsets,
+    int n_experts, int64_t rows_cap, int d_model, int d_ff, const void* w_gate_up_packed,
+    const void* dh, void* dgu, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_swiglu_bwd_gather: n_experts must be in [1, %d] (got %d)",
+               kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
+               "grouped_gate_up_swiglu_bwd_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_swiglu_bwd_gather: d_model must be a multiple of %d (got %d)",
+                    kBK, d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_swiglu_bwd_gather: d_ff must be a multiple of %d (got %d)",
+                    kBN / 2, d_ff);
+  HMOE_REQUIRE(tokens * d_model * 2 < (int64_t(1) << 31),
+               "grouped_gate_up_swiglu_bwd_gather: x must be smaller than 2 GiB");
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && perm_src && offsets && w_gate_up_packed && dh && dgu,
+               "grouped_gate_up_swiglu_bwd_gather: null pointer argument");
+  return launch_grouped(false, false, x, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, dgu, 2 * d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_swiglu_bwd_gather", perm_src, top_k,
+                        static_cast<int>(tokens), static_cast<const uint16_t*>(dh));
+}
+
+extern "C" int hmoe_grouped_gate_up_swiglu_bwd(const void* xs, const int32_t* offsets,
+                                               int n_experts, int64_t rows_cap, int d_model,
+                                               int d_ff, const void* w_gate_up_packed,
+                                               const void* dh, void* dgu, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_swiglu_bwd: n_experts must be in [1, %d] (got %d)", kMaxExperts,
+               n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "grouped_gate_up_swiglu_bwd: rows_cap must be >= 0");
+  HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_swiglu_bwd: d_model must be a multiple of %d (got %d)", kBK,
+                    d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_swiglu_bwd: d_ff must be a multiple of %d (got %d)", kBN / 2,
+                    d_ff);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(xs && offsets && w_gate_up_packed && dh && dgu,
+               "grouped_gate_up_swiglu_bwd: null pointer argument");
+  return launch_grouped(false, false, xs, w_gate_up_packed, nullptr, nullptr, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, dgu, 2 * d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_swiglu_bwd", nullptr, 1, 1,
+                        static_cast<const uint16_t*>(dh));
 }
 
 extern "C" int hmoe_grouped_dgrad_down(const void* d_ys, const int32_t* offsets, int n_experts,

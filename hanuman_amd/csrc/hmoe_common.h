@@ -60,6 +60,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
          (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
 }
 
+// VJP of h = silu(g) * u at one element: dg = dh * u * silu'(g),
+// du = dh * silu(g), silu'(g) = s (1 + g (1 - s)), s = 1 / (1 + e^-g) with the
+// hardware exponential and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each,
+// far below the bf16 rounding that follows); float32, contraction off, so that
+// every kernel that inlines it gives the same bits.
+__device__ __forceinline__ void swiglu_vjp(float d, float g, float u, float& dg, float& du) {
+#pragma clang fp contract(off)
+  const float s = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+  dg = d * u * (s * (1.0f + g * (1.0f - s)));
+  du = d * (g * s);
+}
+
 // ------------------------------------------------------- deterministic exp --
 // Cody-Waite range reduction (Cody & Waite 1980) and a degree-7 Taylor
 // polynomial in Horner form, float32, each step one correctly rounded

@@ -410,6 +410,49 @@ def grouped_gate_up_raw_gather(x: torch.Tensor, plan: Plan, w_gate_up: torch.Ten
     return gu
 
 
+def grouped_gate_up_swiglu_bwd_gather(x: torch.Tensor, plan: Plan, w_gate_up: torch.Tensor,
+                                      dh: torch.Tensor) -> torch.Tensor:
+    """The g, u recompute (``moe.py:70-71``) with the SwiGLU VJP (``:72``) in
+    its epilogue: ``dgu`` bf16 ``[rows_cap, 2F]`` in the gate/up column order
+    from ``dh`` ``[rows_cap, F]``; g and u never reach HBM.  Bit-identical to
+    :func:`grouped_gate_up_raw_gather` followed by :func:`swiglu_bwd`."""
+    _check(x, "x", 2)
+    _check(w_gate_up, "w_gate_up", 3)
+    _check(dh, "dh", 2)
+    if x.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16 or dh.dtype != torch.bfloat16:
+        raise TypeError("grouped_gate_up_swiglu_bwd_gather takes bf16 operands")
+    T, D = x.shape
+    N, F2, D2 = w_gate_up.shape
+    if (D2 != D or plan.n_experts != N or plan.slot_pos.numel() != T * plan.top_k
+            or tuple(dh.shape) != (plan.rows_cap, F2 // 2)):
+        raise ValueError("grouped_gate_up_swiglu_bwd_gather: inconsistent shapes")
+    dgu = torch.empty((plan.rows_cap, F2), dtype=torch.bfloat16, device=x.device)
+    call("hmoe_grouped_gate_up_swiglu_bwd_gather", _ptr(x), T, plan.top_k, _ptr(plan.perm_src),
+         _ptr(plan.offsets), N, plan.rows_cap, D, F2 // 2, _ptr(w_gate_up), _ptr(dh), _ptr(dgu),
+         _stream())
+    return dgu
+
+
+def grouped_gate_up_swiglu_bwd(xs: torch.Tensor, offsets: torch.Tensor, w_gate_up: torch.Tensor,
+                               dh: torch.Tensor) -> torch.Tensor:
+    """:func:`grouped_gate_up_swiglu_bwd_gather` on rows given in order (the
+    shared expert)."""
+    _check(xs, "xs", 2)
+    _check(offsets, "offsets", 1)
+    _check(w_gate_up, "w_gate_up", 3)
+    _check(dh, "dh", 2)
+    if xs.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16 or dh.dtype != torch.bfloat16:
+        raise TypeError("grouped_gate_up_swiglu_bwd takes bf16 operands")
+    R, D = xs.shape
+    N, F2, D2 = w_gate_up.shape
+    if D2 != D or offsets.numel() != N + 1 or tuple(dh.shape) != (R, F2 // 2):
+        raise ValueError("grouped_gate_up_swiglu_bwd: inconsistent shapes")
+    dgu = torch.empty((R, F2), dtype=torch.bfloat16, device=xs.device)
+    call("hmoe_grouped_gate_up_swiglu_bwd", _ptr(xs), _ptr(offsets), N, R, D, F2 // 2,
+         _ptr(w_gate_up), _ptr(dh), _ptr(dgu), _stream())
+    return dgu
+
+
 def grouped_gate_up_raw(xs: torch.Tensor, offsets: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
     """g and u of rows given in order (the shared expert, ``moe.py:23-29``),
     bf16 ``[rows, 2F]`` in the packed gate/up column order."""

@@ -260,6 +260,21 @@ int hmoe_grouped_gate_up_raw(const void* xs, const int32_t* offsets, int n_exper
                              int64_t rows_cap, int d_model, int d_ff,
                              const void* w_gate_up_packed, void* gu, hmoe_stream_t stream);
 
+/* The recompute with the SwiGLU VJP in the GEMM's epilogue: g and u are
+ * rounded to bf16 in registers and dgu = hmoe_swiglu_bwd(dh, g, u) is written
+ * directly (bit-identical to the raw recompute followed by hmoe_swiglu_bwd;
+ * g and u never reach memory).  dh [rows_cap, F] bf16, dgu [rows_cap, 2F]
+ * bf16; operands and limits as the raw entries above. */
+int hmoe_grouped_gate_up_swiglu_bwd_gather(const void* x, int64_t tokens, int top_k,
+                                           const int32_t* perm_src, const int32_t* offsets,
+                                           int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                           const void* w_gate_up_packed, const void* dh, void* dgu,
+                                           hmoe_stream_t stream);
+int hmoe_grouped_gate_up_swiglu_bwd(const void* xs, const int32_t* offsets, int n_experts,
+                                    int64_t rows_cap, int d_model, int d_ff,
+                                    const void* w_gate_up_packed, const void* dh, void* dgu,
+                                    hmoe_stream_t stream);
+
 /* VJP of h = silu(g) * u (moe.py:72): dg = dh * u * silu'(g), du = dh *
  * silu(g), float32 arithmetic, one bf16 rounding each.  dh [rows, F], gu and
  * dgu [rows, 2F] bf16 in the column order of hmoe_grouped_gate_up_raw_gather.

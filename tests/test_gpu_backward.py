@@ -331,6 +331,26 @@ def test_router_aux_bwd(gpu, Bq, Sq, N, Kk):
     np.testing.assert_allclose(acc, base + ref, **tol)
 
 
+@pytest.mark.parametrize("T,D,N,Kk,F,cf", [(600, 512, 8, 2, 256, 1.25), (777, 192, 16, 4, 128, 0.8)])
+def test_fused_swiglu_bwd_matches_unfused(gpu, T, D, N, Kk, F, cf):
+    """The recompute with the SwiGLU VJP in its epilogue equals the raw
+    recompute followed by hmoe_swiglu_bwd bit for bit, gathering from x and
+    on rows given in order."""
+    rng = np.random.default_rng(T + F)
+    x, w, wg, wu, wd, logits, idx, gates, ref_plan, plan = expert_problem(gpu, rng, T, D, N, Kk, F, cf)
+    xd = dev_bf16(x, gpu)
+    wgu = K.pack_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    dh = dev_bf16(rng.standard_normal((plan.rows_cap, F)).astype(np.float32), gpu)
+    ref = K.swiglu_bwd(dh, K.grouped_gate_up_raw_gather(xd, plan, wgu), plan.offsets)
+    fused = K.grouped_gate_up_swiglu_bwd_gather(xd, plan, wgu, dh)
+    xs = K.permute_rows(xd, plan)
+    fused2 = K.grouped_gate_up_swiglu_bwd(xs, plan.offsets, wgu, dh)
+    torch.cuda.synchronize()
+    kept = int(ref_plan["offsets"][-1])
+    assert torch.equal(fused[:kept], ref[:kept])
+    assert torch.equal(fused2[:kept], ref[:kept])
+
+
 def test_gate_up_raw_matches_gather(gpu):
     """The non-gather recompute on the dispatched rows equals the gathering
     one bit for bit (same tiles, same accumulation order)."""
