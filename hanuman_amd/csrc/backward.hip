@@ -205,85 +205,117 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
   }
 }
 
+// The two router products run on the float32 matrix cores,
+// v_mfma_f32_32x32x2_f32: D[m][n] += A[m][k] B[k][n] over k = 2 per
+// instruction, lane L supplying A[L % 32][L / 32] and B[L / 32][L % 32] and
+// holding D[m][L % 32] for m = 8 (r / 4) + 4 (L / 32) + r % 4, r = 0..15.
+// Products are exact in float32 and accumulate in float32.  Operands are
+// staged in LDS with row strides chosen so that the 64 lanes of an operand
+// read hit 64 different banks.
+__device__ __forceinline__ f32x16 mfma_f32_32x32x2(float a, float b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
 // dx[t, d] (+)= sum_n d_logits[t, n] * W[d, n]  (the VJP of x_f @ router,
-// moe.py:178, with respect to x).  Workgroup tile: 128 tokens x 64 columns;
-// thread (tg, dg) = (tid / 8, tid % 8) owns tokens tg*4 .. +4 and columns
-// dg*8 .. +8 (32 accumulators).  n runs in chunks of 32 through LDS, both
-// operands stored n-major there, ascending.
+// moe.py:178, with respect to x).  Workgroup tile: 128 tokens x 64 columns
+// of d; wave w owns tokens 32 w .. +32 and both 32-column blocks (A = W rows,
+// B = d_logits rows, so a lane holds one token and runs of 4 consecutive d).
+// n runs in chunks of 64 (zero padded), both operands [row][n] in LDS.
+constexpr int kRdxStride = 66;  // 2 (L % 32) + L / 32 covers the 64 banks
+
 template <typename TW>
 __global__ __launch_bounds__(256) void router_dx_kernel(const float* __restrict__ d_logits,
                                                         const TW* __restrict__ w, int64_t tokens,
                                                         int d_model, int n_experts,
                                                         float* __restrict__ dx, int accumulate) {
-#pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float sdl[32][128];
-  __shared__ __attribute__((aligned(16))) float sw[32][64];
+  __shared__ float sl[128 * kRdxStride];
+  __shared__ float sw[64 * kRdxStride];
   const int tid = threadIdx.x;
-  const int tg = tid >> 3, dg = tid & 7;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 128;
   const int d0 = blockIdx.y * 64;
-  float acc[4][8];
+  f32x16 acc[2];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[a][i] = 0.0f;
-  for (int n0 = 0; n0 < n_experts; n0 += 32) {
-    __syncthreads();
-    for (int i = tid; i < 128 * 32; i += 256) {
-      const int r = i >> 5, c = i & 31;
-      const int64_t t = t0 + r;
-      sdl[c][r] = (t < tokens && n0 + c < n_experts) ? d_logits[t * n_experts + n0 + c] : 0.0f;
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  const int c = tid & 63;
+  const int64_t t = t0 + wave * 32 + l32;
+  float* o = dx + t * d_model + d0 + hi * 4;
+  // the rows this lane adds into, fetched before anything waits on memory
+  f32x4 prev[2][4];
+  if (accumulate && t < tokens) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) prev[j][q] = *reinterpret_cast<const f32x4*>(o + j * 32 + q * 8);
+  }
+  for (int n0 = 0; n0 < n_experts; n0 += 64) {
+    const bool nok = n0 + c < n_experts;
+    // every load of the chunk is issued before the first LDS write; loads
+    // are unconditional (addresses clamped in range), padding is selected
+    // to zero afterwards, so no load waits inside a branch
+    const int nc = nok ? n0 + c : n_experts - 1;
+    float vl[32], vw[16];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int64_t tr = t0 + (tid >> 6) + 4 * i;
+      vl[i] = d_logits[(tr < tokens ? tr : tokens - 1) * n_experts + nc];
     }
-    for (int i = tid; i < 64 * 32; i += 256) {
-      const int dd = i >> 5, c = i & 31;
-      float v = 0.0f;
-      if (n0 + c < n_experts) {
-        const int64_t idx = static_cast<int64_t>(d0 + dd) * n_experts + n0 + c;
-        if constexpr (sizeof(TW) == 4) v = w[idx];
-        else v = bf16_bits_to_f32(w[idx]);
-      }
-      sw[c][dd] = v;
+    TW rw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      rw[i] = w[static_cast<int64_t>(d0 + (tid >> 6) + 4 * i) * n_experts + nc];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int64_t tr = t0 + (tid >> 6) + 4 * i;
+      vl[i] = (nok && tr < tokens) ? vl[i] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float v;
+      if constexpr (sizeof(TW) == 4) v = rw[i];
+      else v = bf16_bits_to_f32(rw[i]);
+      vw[i] = nok ? v : 0.0f;
     }
     __syncthreads();
-    const int nn = n_experts - n0 < 32 ? n_experts - n0 : 32;
-    for (int c = 0; c < nn; ++c) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(&sdl[c][tg * 4]);
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(&sw[c][dg * 8]);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(&sw[c][dg * 8 + 4]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+    for (int i = 0; i < 32; ++i) sl[((tid >> 6) + 4 * i) * kRdxStride + c] = vl[i];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[r][i] = acc[r][i] + a[r] * w0[i];
-          acc[r][4 + i] = acc[r][4 + i] + a[r] * w1[i];
-        }
+    for (int i = 0; i < 16; ++i) sw[((tid >> 6) + 4 * i) * kRdxStride + c] = vw[i];
+    __syncthreads();
+    const float* pb = sl + (wave * 32 + l32) * kRdxStride + hi;
+    const float* pa0 = sw + l32 * kRdxStride + hi;
+    const float* pa1 = pa0 + 32 * kRdxStride;
+#pragma unroll 8
+    for (int kk = 0; kk < 64; kk += 2) {
+      const float b = pb[kk];
+      acc[0] = mfma_f32_32x32x2(pa0[kk], b, acc[0]);
+      acc[1] = mfma_f32_32x32x2(pa1[kk], b, acc[1]);
     }
   }
+  if (t >= tokens) return;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t t = t0 + tg * 4 + r;
-    if (t >= tokens) break;
-    float* o = dx + t * d_model + d0 + dg * 8;
-    f32x4 r0 = {acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
-    f32x4 r1 = {acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
-    if (accumulate) {
-      const f32x4 p0 = *reinterpret_cast<const f32x4*>(o);
-      const f32x4 p1 = *reinterpret_cast<const f32x4*>(o + 4);
-      r0 = p0 + r0;
-      r1 = p1 + r1;
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 v = {acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
+      if (accumulate) v = prev[j][q] + v;
+      *reinterpret_cast<f32x4*>(o + j * 32 + q * 8) = v;
     }
-    *reinterpret_cast<f32x4*>(o) = r0;
-    *reinterpret_cast<f32x4*>(o + 4) = r1;
-  }
 }
 
 // d_router[d, n] = sum_t x[t, d] * d_logits[t, n] (the VJP of x_f @ router,
 // moe.py:178, with respect to the router weight), float32, in two passes for
-// a fixed summation order: pass 1 sums chunks of kRdwChunk tokens (ascending)
-// into partials [chunk][D][N]; pass 2 sums the chunks in order.  Pass 1
-// workgroup tile: 64 d x 64 n; thread (dq, nq) = (tid / 16, tid % 16) owns
-// d = 4 dq .. +4 and n = 4 nq .. +4, tokens staged 64 at a time in LDS.
-constexpr int kRdwChunk = 1024;
+// a fixed summation order: pass 1 sums chunks of kRdwChunk tokens into
+// partials [chunk][D][N]; pass 2 sums the chunks in order.  Pass 1
+// workgroup tile: 128 d x 64 n of one chunk; wave w owns d 32 w .. +32 and
+// both 32-column n blocks (A = x^T, B = d_logits); tokens staged 64 at a time
+// in LDS as [token][d] and [token][n].
+constexpr int kRdwChunk = 512;
+constexpr int kRdwStrideX = 160;  // row offset 32 banks apart: the two k rows never collide
+constexpr int kRdwStrideL = 96;
 
 template <typename TX>
 __global__ __launch_bounds__(256) void router_dw_partial_kernel(const TX* __restrict__ x,
@@ -291,52 +323,77 @@ __global__ __launch_bounds__(256) void router_dw_partial_kernel(const TX* __rest
                                                                 int64_t tokens, int d_model,
                                                                 int n_experts,
                                                                 float* __restrict__ partial) {
-#pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float sx[64][64];
-  __shared__ __attribute__((aligned(16))) float sl[64][64];
+  __shared__ float sx[64 * kRdwStrideX];
+  __shared__ float sl[64 * kRdwStrideL];
   const int tid = threadIdx.x;
-  const int dq = tid >> 4, nq = tid & 15;
-  const int d0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int d0 = blockIdx.x * 128, n0 = blockIdx.y * 64;
   const int64_t c = blockIdx.z;
   const int64_t t_begin = c * kRdwChunk;
   const int64_t t_end = t_begin + kRdwChunk < tokens ? t_begin + kRdwChunk : tokens;
-  float acc[4][4];
+  f32x16 acc[2];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += 64) {
-    __syncthreads();
-    for (int i = tid; i < 64 * 64; i += 256) {
-      const int r = i >> 6, cc = i & 63;
-      const int64_t t = t0 + r;
-      float vx = 0.0f, vl = 0.0f;
-      if (t < t_end) {
-        if constexpr (sizeof(TX) == 4) vx = x[t * d_model + d0 + cc];
-        else vx = bf16_bits_to_f32(x[t * d_model + d0 + cc]);
-        if (n0 + cc < n_experts) vl = d_logits[t * n_experts + n0 + cc];
-      }
-      sx[r][cc] = vx;
-      sl[r][cc] = vl;
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  const int cx = tid & 127, cl = tid & 63;
+  const bool nok = n0 + cl < n_experts;
+  // 64-token steps, software pipelined: step s+1's operands are loaded into
+  // registers while step s's MFMAs run.
+  // Loads are unconditional (row and column clamped in range) and the
+  // padding is zeroed when the registers go to LDS, so no load waits inside
+  // a branch.
+  const int nc = nok ? n0 + cl : n_experts - 1;
+  TX vx[32];
+  float vl[16];
+  int64_t fetched = t_begin;
+  auto fetch = [&](int64_t tt) __attribute__((always_inline)) {
+    fetched = tt;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int64_t t = tt + (tid >> 7) + 2 * i;
+      vx[i] = x[(t < t_end ? t : t_end - 1) * d_model + d0 + cx];
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t t = tt + (tid >> 6) + 4 * i;
+      vl[i] = d_logits[(t < t_end ? t : t_end - 1) * n_experts + nc];
+    }
+  };
+  fetch(t_begin);
+  for (int64_t tt = t_begin; tt < t_end; tt += 64) {
     __syncthreads();
-    const int nt = t_end - t0 < 64 ? static_cast<int>(t_end - t0) : 64;
-    for (int r = 0; r < nt; ++r) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(&sx[r][dq * 4]);
-      const f32x4 lv = *reinterpret_cast<const f32x4*>(&sl[r][nq * 4]);
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+    for (int i = 0; i < 32; ++i) {
+      float v;
+      if constexpr (sizeof(TX) == 4) v = vx[i];
+      else v = bf16_bits_to_f32(vx[i]);
+      sx[((tid >> 7) + 2 * i) * kRdwStrideX + cx] = fetched + (tid >> 7) + 2 * i < t_end ? v : 0.0f;
+    }
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = acc[a][b] + xv[a] * lv[b];
+    for (int i = 0; i < 16; ++i)
+      sl[((tid >> 6) + 4 * i) * kRdwStrideL + cl] =
+          (nok && fetched + (tid >> 6) + 4 * i < t_end) ? vl[i] : 0.0f;
+    __syncthreads();
+    if (tt + 64 < t_end) fetch(tt + 64);
+    const float* pa = sx + hi * kRdwStrideX + wave * 32 + l32;
+    const float* pb = sl + hi * kRdwStrideL + l32;
+#pragma unroll 8
+    for (int kk = 0; kk < 64; kk += 2) {
+      const float a = pa[kk * kRdwStrideX];
+      acc[0] = mfma_f32_32x32x2(a, pb[kk * kRdwStrideL], acc[0]);
+      acc[1] = mfma_f32_32x32x2(a, pb[kk * kRdwStrideL + 32], acc[1]);
     }
   }
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int d = d0 + dq * 4 + a;
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + j * 32 + l32;
+    if (n >= n_experts) continue;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int n = n0 + nq * 4 + b;
-      if (n < n_experts) partial[(c * d_model + d) * n_experts + n] = acc[a][b];
+    for (int r = 0; r < 16; ++r) {
+      const int d = d0 + wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+      partial[(c * d_model + d) * n_experts + n] = acc[j][r];
     }
   }
 }
@@ -457,8 +514,8 @@ extern "C" int hmoe_router_dw(const void* x, int x_dtype, const float* d_logits,
                               size_t workspace_bytes, hmoe_stream_t stream) {
   using namespace hmoe;
   HMOE_REQUIRE(tokens >= 1 && n_experts >= 1, "router_dw: need tokens >= 1 and n_experts >= 1");
-  HMOE_REQUIRE(d_model >= 64 && d_model % 64 == 0,
-               "router_dw: d_model must be a multiple of 64 (got %d)", d_model);
+  HMOE_REQUIRE(d_model >= 128 && d_model % 128 == 0,
+               "router_dw: d_model must be a multiple of 128 (got %d)", d_model);
   HMOE_REQUIRE(x_dtype == HMOE_F32 || x_dtype == HMOE_BF16, "router_dw: x dtype must be F32 or BF16");
   HMOE_REQUIRE(x && d_logits && d_router && workspace, "router_dw: null pointer argument");
   const size_t need = hmoe_router_dw_workspace_bytes(tokens, d_model, n_experts);
@@ -467,7 +524,7 @@ extern "C" int hmoe_router_dw(const void* x, int x_dtype, const float* d_logits,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int chunks = static_cast<int>(ceil_div(tokens, kRdwChunk));
   float* partial = static_cast<float*>(workspace);
-  const dim3 grid(static_cast<unsigned>(d_model / 64), static_cast<unsigned>(ceil_div(n_experts, 64)),
+  const dim3 grid(static_cast<unsigned>(d_model / 128), static_cast<unsigned>(ceil_div(n_experts, 64)),
                   static_cast<unsigned>(chunks));
   if (x_dtype == HMOE_F32)
     hipLaunchKernelGGL(router_dw_partial_kernel<float>, grid, dim3(256), 0, s,

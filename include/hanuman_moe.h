@@ -339,8 +339,8 @@ int hmoe_router_aux_bwd(const float* logits, const int32_t* top_idx, int batch, 
                         hmoe_stream_t stream);
 
 /* dx [T,D] f32 (+)= d_logits [T,N] @ router_w^T (router_w [D,N] F32/BF16):
- * the VJP of l = f32(x) @ router (moe.py:175,178) with respect to x.
- * accumulate != 0 adds into dx.  D % 64 == 0. */
+ * the VJP of l = f32(x) @ router (moe.py:175,178) with respect to x, on the
+ * float32 matrix cores.  accumulate != 0 adds into dx.  D % 64 == 0. */
 int hmoe_router_dx(const float* d_logits, const void* router_w, int w_dtype, int64_t tokens,
                    int d_model, int n_experts, float* dx, int accumulate, hmoe_stream_t stream);
 
@@ -362,8 +362,8 @@ int hmoe_grouped_wgrad_gate_up(const void* xs, const void* dgu, const int32_t* o
 
 /* d_router [D,N] f32 = x^T d_logits (the VJP of moe.py:178 with respect to
  * the router weight), x [T,D] F32/BF16, d_logits [T,N] f32; float32 sums
- * over chunks of 1024 tokens (ascending), then over the chunks in order.
- * workspace >= hmoe_router_dw_workspace_bytes.  D % 64 == 0. */
+ * over chunks of 512 tokens (float32 matrix cores), then over the chunks in
+ * order.  workspace >= hmoe_router_dw_workspace_bytes.  D % 128 == 0. */
 size_t hmoe_router_dw_workspace_bytes(int64_t tokens, int d_model, int n_experts);
 int hmoe_router_dw(const void* x, int x_dtype, const float* d_logits, int64_t tokens,
                    int d_model, int n_experts, float* d_router, void* workspace,

@@ -204,10 +204,13 @@ def test_router_bwd(gpu, mode, T, N, Kk):
     np.testing.assert_allclose(dl, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("N", [72, 64, 40, 20])
 @pytest.mark.parametrize("w_dtype", ["f32", "bf16"])
-def test_router_dx(gpu, w_dtype):
-    rng = np.random.default_rng(11)
-    T, D, N = 777, 512, 72
+def test_router_dx(gpu, w_dtype, N):
+    """Expert counts around the 64-wide LDS chunks (one partial chunk,
+    exactly one, a part of one, two with the second partial)."""
+    rng = np.random.default_rng(11 + N)
+    T, D = 777, 512
     dl = rng.standard_normal((T, N)).astype(np.float32)
     w = (0.02 * rng.standard_normal((D, N))).astype(np.float32)
     if w_dtype == "bf16":
