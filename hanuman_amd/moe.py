@@ -188,6 +188,46 @@ class MoE:
                  "shared_w_gate", "shared_w_up", "shared_w_down")
         return {n: getattr(self, n) for n in names}
 
+    def state(self) -> dict:
+        """The parameters as a pure dict of float32 NumPy arrays under the
+        reference's attribute names (the MoE subtree of the nnx state that
+        ``train.py:326-334`` checkpoints)."""
+        return {n: p.value.detach().float().cpu().numpy() for n, p in self.named_params().items()}
+
+    def load_state(self, tree) -> None:
+        """Loads parameters from a mapping in the reference's layout: each
+        name of :meth:`named_params` maps to an array (NumPy, torch or
+        anything ``np.asarray`` takes) or to an nnx-style ``{"value": array}``
+        node.  Every name must be present with the parameter's shape; values
+        are copied in place (float32), so packed operands rebuild on the next
+        call."""
+        for name, param in self.named_params().items():
+            if name not in tree:
+                raise KeyError(f"checkpoint has no {name!r}")
+            leaf = tree[name]
+            if isinstance(leaf, dict):
+                if "value" not in leaf:
+                    raise KeyError(f"checkpoint node {name!r} has no 'value'")
+                leaf = leaf["value"]
+            arr = leaf if isinstance(leaf, torch.Tensor) else torch.from_numpy(
+                np.ascontiguousarray(np.asarray(leaf, dtype=np.float32)))
+            if tuple(arr.shape) != tuple(param.value.shape):
+                raise ValueError(f"{name}: checkpoint shape {tuple(arr.shape)} != "
+                                 f"parameter shape {tuple(param.value.shape)}")
+            with torch.no_grad():
+                param.value.copy_(arr.to(device=param.value.device, dtype=param.value.dtype))
+
+    def save_safetensors(self, path) -> None:
+        """Writes :meth:`state` to a safetensors file (reference names)."""
+        from safetensors.numpy import save_file
+        save_file(self.state(), str(path))
+
+    def load_safetensors(self, path) -> None:
+        """Loads a file written by :meth:`save_safetensors` (or any
+        safetensors file with the reference names and shapes)."""
+        from safetensors.numpy import load_file
+        self.load_state(load_file(str(path)))
+
     def _packed_routed(self):
         wg, wu, wd = self.expert_w_gate.value, self.expert_w_up.value, self.expert_w_down.value
         return self._routed_pack.get((wg, wu, wd), lambda: (K.pack_gate_up(wg, wu), K.pack_down(wd)))

@@ -74,3 +74,26 @@ def test_moe_rejects_what_is_not_built():
     m = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu")
     with pytest.raises(ValueError, match="GPU"):   # no CPU path: kernels need device tensors
         m(torch.zeros(1, 4, 64, dtype=torch.bfloat16))
+
+
+def test_moe_state_round_trip(tmp_path):
+    """Reference-named parameter tree in and out: a safetensors file, nnx
+    {"value": array} nodes, shape and name checks."""
+    a = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu")
+    b = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=1, device="cpu")
+    assert not np.array_equal(a.state()["router"], b.state()["router"])
+    a.save_safetensors(tmp_path / "moe.safetensors")
+    b.load_safetensors(tmp_path / "moe.safetensors")
+    for k, v in a.state().items():
+        assert np.array_equal(v, b.state()[k]), k
+    c = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=2, device="cpu")
+    c.load_state({k: {"value": v} for k, v in a.state().items()})
+    assert all(np.array_equal(v, c.state()[k]) for k, v in a.state().items())
+    bad = a.state()
+    bad["expert_w_up"] = bad["expert_w_up"][:, :, :16]
+    with pytest.raises(ValueError, match="expert_w_up"):
+        c.load_state(bad)
+    missing = a.state()
+    del missing["bias"]
+    with pytest.raises(KeyError, match="bias"):
+        c.load_state(missing)
