@@ -281,7 +281,7 @@ def main():
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
         kname = ("grouped_gemm_dma<true, true>" if fp8
                  else f"grouped_gemm_regs<true, {'true' if odd else 'false'}, "
-                      f"{'true' if fused else 'false'}>")
+                      f"{'true' if fused else 'false'}, false>")
         flop, peak = work["gate_up"][1], work["gate_up"][2]
         ach = flop / (stage_ms["gate_up"] / 1e3) / 1e12
         roofline = {"kernel": kname, "bound": "mfma", "achieved": round(ach, 1), "peak": peak,
@@ -454,7 +454,7 @@ def bench_backward(args, name, wl, layer):
                        "unit": "GB/s" if kind == "hbm" else "TFLOP/s", "peak": peak,
                        "frac": round(ach / peak, 4), ("bytes" if kind == "hbm" else "flop"): amount}
     dom = "dgrad_gate_up"
-    roofline = {"kernel": "grouped_gemm_regs<false, false, false> (dgrad gate/up)", "bound": "mfma",
+    roofline = {"kernel": "grouped_gemm_regs<false, false, false, false> (dgrad gate/up)", "bound": "mfma",
                 "achieved": kernels[dom]["achieved"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": kernels[dom]["frac"], "traffic": None, "flop_per_launch": work[dom][1],
                 "ms": kernels[dom]["ms"]}
