@@ -16,13 +16,15 @@ namespace {
 constexpr int kMaxKBwd = 16;
 
 // ---- combine VJP ------------------------------------------------------------
-// One wave per token.  d_ys[pos(t,k)] = bf16(dy[t] * bf16(g[t,k])) (float32
-// product, one rounding); d_g[t,k] = bf16(f32(sum_d dy[t,d] * ys[pos,d])) with
-// the sum in float64 (every product of a float32 and a bf16 value is exact in
-// float64), 0 for dropped slots.  With d_shared, also the cotangent of the
-// shared expert's output (moe.py:249-251, each SwiGLU's f32(bf16) result):
-// d_shared[t] = bf16(dy[t] / shared_div).
-template <int KMAX>
+// One wave per (token, slot).  d_ys[pos(t,k)] = bf16(dy[t] * bf16(g[t,k]))
+// (float32 product, one rounding); d_g[t,k] = bf16(f32(sum_d dy[t,d] *
+// ys[pos,d])) with the sum in float64 (every product of a float32 and a bf16
+// value is exact in float64): each lane sums its 8-column chunks in column
+// order, then the wave adds the lanes in a fixed tree.  Dropped slots get
+// d_g = 0 and no row.  The K waves of a token read its dy row from L2 after
+// the first; a wave holds few registers, so many waves keep loads in flight.
+// The k = 0 wave also writes d_shared[t] = bf16(dy[t] / shared_div), the
+// cotangent of the shared expert's output (moe.py:249-251).
 __global__ __launch_bounds__(256) void combine_bwd_kernel(
     const float* __restrict__ dy, const uint16_t* __restrict__ ys,
     const int32_t* __restrict__ slot_pos, const float* __restrict__ gates, int64_t tokens,
@@ -30,87 +32,69 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
     uint16_t* __restrict__ d_shared, float shared_div) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= tokens) return;
-  int32_t my_pos = -1;
-  float my_g = 0.0f;
-  if (lane < top_k) {
-    my_pos = slot_pos[t * top_k + lane];
-    my_g = bf16_bits_to_f32(f32_to_bf16_bits(gates[t * top_k + lane]));
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (w >= tokens * top_k) return;
+  const int64_t t = w / top_k;
+  const int k = static_cast<int>(w - t * top_k);
+  const int32_t pos = slot_pos[w];
+  const bool shared = d_shared != nullptr && k == 0;
+  if (pos < 0 && !shared) {
+    if (lane == 0) d_gates[w] = 0.0f;
+    return;
   }
-  int32_t pos[KMAX];
-  float g[KMAX];
-  double part[KMAX];
-#pragma unroll
-  for (int k = 0; k < KMAX; ++k) {
-    pos[k] = __shfl(my_pos, k, 64);
-    g[k] = __shfl(my_g, k, 64);
-    part[k] = 0.0;
-  }
+  const float g = bf16_bits_to_f32(f32_to_bf16_bits(gates[w]));
   const int chunks = d_model / 8;
   const float* dy_row = dy + t * d_model;
-  // Two chunks per lane per iteration: 2 (K + 2) loads in flight.
-  constexpr int kU = KMAX <= 8 ? 2 : 1;
+  const uint16_t* y_row = ys + static_cast<int64_t>(pos < 0 ? 0 : pos) * d_model;
+  uint16_t* o_row = d_ys + static_cast<int64_t>(pos < 0 ? 0 : pos) * d_model;
+  double part = 0.0;
+  constexpr int kU = 4;  // chunks in flight per lane
   for (int c0 = lane; c0 < chunks; c0 += 64 * kU) {
-    float d[kU][8];
-    u32x4 yv[kU][KMAX];
+    f32x4 da[kU], db[kU];
+    u32x4 yv[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int c = c0 + 64 * u;
       if (c < chunks) {
-        const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy_row + c * 8));
-        const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy_row + c * 8 + 4));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          d[u][i] = a[i];
-          d[u][4 + i] = b[i];
-        }
-#pragma unroll
-        for (int k = 0; k < KMAX; ++k)
-          if (k < top_k && pos[k] >= 0)
-            yv[u][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                ys + static_cast<int64_t>(pos[k]) * d_model + c * 8));
+        // cached: the token's other slots read the same row
+        da[u] = *reinterpret_cast<const f32x4*>(dy_row + c * 8);
+        db[u] = *reinterpret_cast<const f32x4*>(dy_row + c * 8 + 4);
+        if (pos >= 0) yv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(y_row + c * 8));
       }
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int c = c0 + 64 * u;
       if (c >= chunks) break;
-      if (d_shared != nullptr) {
+      float d[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        d[i] = da[u][i];
+        d[4 + i] = db[u][i];
+      }
+      if (shared) {
         u32x4 o;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          o[q] = pack_bf16x2(d[u][2 * q] / shared_div, d[u][2 * q + 1] / shared_div);
+        for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(d[2 * q] / shared_div, d[2 * q + 1] / shared_div);
         __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(d_shared + t * d_model + c * 8));
       }
+      if (pos >= 0) {
+        u32x4 o;
 #pragma unroll
-      for (int k = 0; k < KMAX; ++k) {
-        if (k < top_k && pos[k] >= 0) {
-          u32x4 o;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            o[q] = pack_bf16x2(d[u][2 * q] * g[k], d[u][2 * q + 1] * g[k]);
-            const uint32_t w = yv[u][k][q];
-            part[k] += static_cast<double>(d[u][2 * q]) *
-                       static_cast<double>(__uint_as_float(w << 16));
-            part[k] += static_cast<double>(d[u][2 * q + 1]) *
-                       static_cast<double>(__uint_as_float(w & 0xffff0000u));
-          }
-          __builtin_nontemporal_store(
-              o, reinterpret_cast<u32x4*>(d_ys + static_cast<int64_t>(pos[k]) * d_model + c * 8));
+        for (int q = 0; q < 4; ++q) {
+          o[q] = pack_bf16x2(d[2 * q] * g, d[2 * q + 1] * g);
+          const uint32_t wv = yv[u][q];
+          part += static_cast<double>(d[2 * q]) * static_cast<double>(__uint_as_float(wv << 16));
+          part += static_cast<double>(d[2 * q + 1]) *
+                  static_cast<double>(__uint_as_float(wv & 0xffff0000u));
         }
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(o_row + c * 8));
       }
     }
   }
-  float mine = 0.0f;
 #pragma unroll
-  for (int k = 0; k < KMAX; ++k) {
-    double v = part[k];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    if (lane == k) mine = bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(v)));
-  }
-  if (lane < top_k) d_gates[t * top_k + lane] = my_pos >= 0 ? mine : 0.0f;
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+  if (lane == 0) d_gates[w] = pos >= 0 ? bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(part))) : 0.0f;
 }
 
 // ---- SwiGLU VJP -------------------------------------------------------------
@@ -428,18 +412,11 @@ extern "C" int hmoe_combine_bwd(const float* dy, const void* ys, const int32_t* 
   HMOE_REQUIRE(d_shared == nullptr || shared_div >= 1.0f,
                "combine_bwd: shared_div must be the number of shared experts (>= 1)");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4)));
-  const uint16_t* y = static_cast<const uint16_t*>(ys);
-  uint16_t* o = static_cast<uint16_t*>(d_ys);
-  uint16_t* sh = static_cast<uint16_t*>(d_shared);
-  if (top_k <= 2)
-    hipLaunchKernelGGL(combine_bwd_kernel<2>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
-  else if (top_k <= 4)
-    hipLaunchKernelGGL(combine_bwd_kernel<4>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
-  else if (top_k <= 8)
-    hipLaunchKernelGGL(combine_bwd_kernel<8>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
-  else
-    hipLaunchKernelGGL(combine_bwd_kernel<16>, grid, dim3(256), 0, s, dy, y, slot_pos, gates, tokens, top_k, d_model, o, d_gates, sh, shared_div);
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens * top_k, 4)));
+  hipLaunchKernelGGL(combine_bwd_kernel, grid, dim3(256), 0, s, dy,
+                     static_cast<const uint16_t*>(ys), slot_pos, gates, tokens, top_k, d_model,
+                     static_cast<uint16_t*>(d_ys), d_gates, static_cast<uint16_t*>(d_shared),
+                     shared_div);
   return check_launch("hmoe_combine_bwd");
 }
 
