@@ -369,8 +369,9 @@ def test_gate_up_raw_matches_gather(gpu):
     assert torch.equal(a[:kept], b[:kept])
 
 
-@pytest.mark.parametrize("n_shared,cf", [(1, None), (2, 1.0)])
-def test_module_autograd_matches_oracle(gpu, n_shared, cf):
+@pytest.mark.parametrize("n_shared,cf,x_dtype", [(1, None, "bf16"), (2, 1.0, "bf16"),
+                                                 (1, 1.0, "f32")])
+def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype):
     """MoE.__call__ under torch autograd: loss = <dy, out> + c_z z_loss +
     c_b balance_loss (train.py:191-200), backward through the library's VJP
     of the whole module, every gradient against the bf16-mode oracle fed
@@ -384,15 +385,18 @@ def test_module_autograd_matches_oracle(gpu, n_shared, cf):
     for n in names:
         getattr(m, n).value.requires_grad_(True)
     gen = torch.Generator(device=gpu).manual_seed(5)
-    x = torch.randn(Bq, Sq, D, generator=gen, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    x = torch.randn(Bq, Sq, D, generator=gen, device=gpu)
+    if x_dtype == "bf16":
+        x = x.to(torch.bfloat16)
+    x.requires_grad_(True)
     dy = torch.randn(Bq, Sq, D, generator=gen, device=gpu)
     c_z, c_b = 0.37, 0.81
-    print(f"module autograd n_shared={n_shared} cf={cf}", flush=True)
+    print(f"module autograd n_shared={n_shared} cf={cf} x {x_dtype}", flush=True)
     out, aux = m(x)
     loss = (out * dy).sum() + c_z * aux["router_z_loss"] + c_b * aux["balance_loss"]
     loss.backward()
     torch.cuda.synchronize()
-    assert out.grad_fn is not None and x.grad is not None and x.grad.dtype == torch.bfloat16
+    assert out.grad_fn is not None and x.grad is not None and x.grad.dtype == x.dtype
     with torch.no_grad():
         _, _, _, sv = m._forward(x.detach(), save=True)
     T = Bq * Sq
@@ -401,8 +405,9 @@ def test_module_autograd_matches_oracle(gpu, n_shared, cf):
     ref_plan = O.dispatch_plan(idx, N, cap)
     xn = host(x.detach()).reshape(T, D)
     p = {n: getattr(m, n).value.detach().float().cpu().numpy() for n in names}
+    # the experts see x in bf16 (moe.py:198); the router sees it as given
     ref_fwd = {"logits": host(sv["logits"]), "top_idx": idx, "gates": host(sv["gates"]),
-               "plan": ref_plan, "xs": O.permute_rows(xn, ref_plan["perm_src"], Kk),
+               "plan": ref_plan, "xs": O.permute_rows(O.bf16_round(xn), ref_plan["perm_src"], Kk),
                "ys": host(sv["ys"])}
     ref = B.moe_backward(xn, p, host(dy).reshape(T, D), ref_fwd, routing="sigmoid", rsf=2.5,
                          precision="bf16", n_shared=n_shared, batch_shape=(Bq, Sq),
