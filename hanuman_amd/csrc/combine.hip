@@ -1,5 +1,6 @@
 // Weighted combine (model/moe.py:80-85): un-permute the expert outputs through
-// slot_pos and sum the K slots with bf16-rounded gates in float32.
+// slot_pos and sum the K slots in float32 with the gates cast to the rows'
+// dtype (bf16-rounded for bf16 rows, as they are for float32 rows).
 //
 // One wave per token.  Lane k < K loads slot k's row index and gate; the wave
 // then streams the D columns in 8-element (16-byte bf16) chunks, issuing the
@@ -94,7 +95,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const TY* __restrict__ ys,
   float my_g = 0.0f;
   if (lane < top_k) {
     my_pos = slot_pos[t * top_k + lane];
-    my_g = gates != nullptr ? bf16_bits_to_f32(f32_to_bf16_bits(gates[t * top_k + lane])) : 1.0f;
+    // the gates are cast to the rows' dtype (weights.astype(out.dtype), moe.py:84)
+    const float g = gates != nullptr ? gates[t * top_k + lane] : 1.0f;
+    my_g = sizeof(TY) == 2 ? bf16_bits_to_f32(f32_to_bf16_bits(g)) : g;
   }
   int32_t pos[KMAX];
   float g[KMAX];

@@ -289,6 +289,41 @@ def grouped_down(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor,
     return ys
 
 
+def grouped_gate_up_f32(xs: torch.Tensor, offsets: torch.Tensor, w_gate: torch.Tensor,
+                        w_up: torch.Tensor) -> torch.Tensor:
+    """Float32 ``h = silu(xs Wg[e]) * (xs Wu[e])`` per expert segment
+    (``moe.py:70-72`` with dtype float32), masters ``[N, D, F]`` as they are."""
+    for t, n in ((xs, "xs"), (offsets, "offsets"), (w_gate, "w_gate"), (w_up, "w_up")):
+        _check(t, n)
+    if xs.dtype != torch.float32 or w_gate.dtype != torch.float32 or w_up.dtype != torch.float32:
+        raise TypeError("grouped_gate_up_f32 takes float32 operands")
+    R, D = xs.shape
+    N, D2, F = w_gate.shape
+    if D2 != D or tuple(w_up.shape) != (N, D, F) or offsets.numel() != N + 1:
+        raise ValueError("grouped_gate_up_f32: inconsistent shapes")
+    h = torch.empty((R, F), dtype=torch.float32, device=xs.device)
+    call("hmoe_grouped_gate_up_f32", _ptr(xs), _ptr(offsets), N, R, D, F, _ptr(w_gate), _ptr(w_up),
+         _ptr(h), _stream())
+    return h
+
+
+def grouped_down_f32(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor) -> torch.Tensor:
+    """Float32 ``ys = h Wd[e]`` per expert segment (``moe.py:73``), master
+    ``[N, F, D]`` as it is."""
+    for t, n in ((h, "h"), (offsets, "offsets"), (w_down, "w_down")):
+        _check(t, n)
+    if h.dtype != torch.float32 or w_down.dtype != torch.float32:
+        raise TypeError("grouped_down_f32 takes float32 operands")
+    R, F = h.shape
+    N, F2, D = w_down.shape
+    if F2 != F or offsets.numel() != N + 1:
+        raise ValueError("grouped_down_f32: inconsistent shapes")
+    ys = torch.empty((R, D), dtype=torch.float32, device=h.device)
+    call("hmoe_grouped_down_f32", _ptr(h), _ptr(offsets), N, R, F, D, _ptr(w_down), _ptr(ys),
+         _stream())
+    return ys
+
+
 def grouped_gate_up_fp8(xs_q: torch.Tensor, xs_scale: torch.Tensor, offsets: torch.Tensor,
                         w_packed: torch.Tensor, w_scales: torch.Tensor) -> torch.Tensor:
     """bf16 ``h`` of the fp8 gate/up GEMM (dequantised, SwiGLU applied)."""

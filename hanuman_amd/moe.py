@@ -60,10 +60,19 @@ def _generator(rngs, device) -> torch.Generator:
 
 
 def _require_bf16_compute(dtype: torch.dtype):
-    if dtype != torch.bfloat16:
+    if dtype not in (torch.bfloat16, torch.float32):
         raise NotImplementedError(
-            "the grouped expert GEMM computes in bfloat16 (fp32 accumulation); "
+            "the grouped expert GEMMs compute in bfloat16 (fp32 accumulation) or float32; "
             f"compute dtype {dtype} is not built")
+
+
+def _f32_swiglu_one(x32: torch.Tensor, wg, wu, wd) -> torch.Tensor:
+    """One float32 SwiGLU (``moe.py:23-29`` with dtype float32): one segment
+    of all rows on the float32 grouped GEMMs, masters as they are."""
+    off = _offsets_one_group(x32.shape[0], x32.device)
+    h = K.grouped_gate_up_f32(x32, off, wg.float().unsqueeze(0).contiguous(),
+                              wu.float().unsqueeze(0).contiguous())
+    return K.grouped_down_f32(h, off, wd.float().unsqueeze(0).contiguous())
 
 
 class _PackCache:
@@ -95,6 +104,8 @@ def swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: to
     """
     dt = _torch_dtype(dtype)
     _require_bf16_compute(dt)
+    if dt == torch.float32:
+        return _f32_swiglu_one(x.float().contiguous(), w_gate, w_up, w_down)
     xb = x.to(dt).contiguous()
     T = xb.shape[0]
     off = _offsets_one_group(T, x.device)
@@ -118,6 +129,12 @@ def ragged_dispatch(x_flat: torch.Tensor, top_idx: torch.Tensor, weights: torch.
     T, Kk = top_idx.shape
     N = w_gate.shape[0]
     plan = K.dispatch_plan(top_idx.to(torch.int32).contiguous(), N, T * Kk)
+    if dt == torch.float32:
+        xs = K.permute_rows(x_flat.contiguous(), plan, torch.float32)
+        h = K.grouped_gate_up_f32(xs, plan.offsets, w_gate.float().contiguous(),
+                                  w_up.float().contiguous())
+        ys = K.grouped_down_f32(h, plan.offsets, w_down.float().contiguous())
+        return K.combine(ys, plan, weights.float().contiguous(), None, torch.float32)
     wgu = K.pack_gate_up(w_gate, w_up)
     if x_flat.dtype == torch.bfloat16:
         # the gate/up GEMM gathers its rows from x (moe.py:56 fused)
@@ -253,6 +270,14 @@ class MoE:
         T = x_flat.shape[0]
         off = _offsets_one_group(T, x_flat.device)
         outs = []
+        if self.dtype == torch.float32:
+            wg, wu, wdn = self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value
+            if self.n_shared_experts == 1:
+                return _f32_swiglu_one(x_flat, wg, wu, wdn)
+            acc = torch.zeros((T, wdn.shape[-1]), dtype=torch.float32, device=x_flat.device)
+            for i in range(self.n_shared_experts):
+                acc += _f32_swiglu_one(x_flat, wg[i], wu[i], wdn[i])
+            return acc / self.n_shared_experts
         for wgu, wd in self._packed_shared():
             h = K.grouped_gate_up(x_flat, off, wgu)
             if hs is not None:
@@ -280,6 +305,8 @@ class MoE:
         are differentiable, ``expert_counts`` is not (``train.py:191-200``
         differentiates the same outputs)."""
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self._params())):
+            if self.dtype != torch.bfloat16:
+                raise NotImplementedError("the backward is built for the bfloat16 compute dtype")
             out, z, bal, ent, counts = _MoEFunction.apply(self, x, *self._params())
             return out, {"router_z_loss": z, "balance_loss": bal, "mean_entropy": ent,
                          "expert_counts": counts}
@@ -309,6 +336,16 @@ class MoE:
                                           bias, Kk, mode, rsf)
         cap = K.capacity(T, Kk, N, self.capacity_factor)
         plan = K.dispatch_plan(top_idx, N, cap)
+        if self.dtype == torch.float32:
+            # float32 compute dtype: the experts on the float32 matrix cores
+            xs = K.permute_rows(x2, plan, torch.float32)
+            h = K.grouped_gate_up_f32(xs, plan.offsets, self.expert_w_gate.value.float().contiguous(),
+                                      self.expert_w_up.value.float().contiguous())
+            ys = K.grouped_down_f32(h, plan.offsets, self.expert_w_down.value.float().contiguous())
+            shared = self._shared_ffn(x2.float().contiguous())
+            out = K.combine(ys, plan, gates, shared, torch.float32)
+            losses, counts = K.router_aux(logits, top_idx, B, S)
+            return out.reshape(B, S, D), losses, counts, None
         wgu, wd = self._packed_routed()
         if x2.dtype == torch.bfloat16:
             # the gate/up GEMM gathers its rows from x (moe.py:56 fused)

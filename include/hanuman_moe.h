@@ -203,10 +203,25 @@ int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale, const int32_
                           const uint8_t* w_packed, const float* w_scales, void* ys,
                           hmoe_stream_t stream);
 
+/* Float32 compute dtype (moe.py:70-74 with dtype = float32): the grouped
+ * GEMMs on the float32 matrix cores with the masters as they are.
+ * gate/up: h [rows_cap, F] = silu(xs W_gate[e]) * (xs W_up[e]) in float32,
+ * xs [rows_cap, D] f32, w_gate / w_up [N, D, F] f32; D % 16 == 0,
+ * F % 64 == 0.  down: ys [rows_cap, D] = h W_down[e], w_down [N, F, D] f32;
+ * F % 16 == 0, D % 64 == 0.  Rows past offsets[N] are not written. */
+int hmoe_grouped_gate_up_f32(const float* xs, const int32_t* offsets, int n_experts,
+                             int64_t rows_cap, int d_model, int d_ff, const float* w_gate,
+                             const float* w_up, float* h, hmoe_stream_t stream);
+int hmoe_grouped_down_f32(const float* h, const int32_t* offsets, int n_experts,
+                          int64_t rows_cap, int d_ff, int d_model, const float* w_down, float* ys,
+                          hmoe_stream_t stream);
+
 /* ---- combine: moe.py:80-85 (replaces `ys[inv]` and the weighted einsum) - */
 
-/* out[t] = sum_k bf16(gates[t,k]) * ys[slot_pos[t*K+k]] (+ residual[t]),
- * float32 accumulation over k ascending, dropped slots skipped.
+/* out[t] = sum_k g'[t,k] * ys[slot_pos[t*K+k]] (+ residual[t]), g' the gates
+ * cast to ys's dtype (bf16(gates) for BF16 rows, gates for F32 rows:
+ * weights.astype(out.dtype), moe.py:84), float32 accumulation over k
+ * ascending, dropped slots skipped.
  * ys [rows, D] (BF16/F32); gates [T,K] f32, or NULL for unit weights;
  * residual [T,D] (F32/BF16) or NULL: the shared expert's output, added last
  * (moe.py:249-251); out [T,D] (F32/BF16). */

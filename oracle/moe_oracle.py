@@ -488,17 +488,22 @@ def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s):
 # combine (moe.py:80-85)
 # --------------------------------------------------------------------------
 
-def combine(ys, slot_pos, gates, T: int, K: int, residual=None) -> np.ndarray:
-    """``y[t] = sum_k bf16(g[t,k]) * ys[slot_pos[t*K+k]]`` in float32.
+def combine(ys, slot_pos, gates, T: int, K: int, residual=None, ys_dtype: str = "bf16") -> np.ndarray:
+    """``y[t] = sum_k g'[t,k] * ys[slot_pos[t*K+k]]`` in float32, ``g'`` the
+    gates cast to the rows' dtype: ``bf16(g)`` for bf16 rows, ``g`` for
+    float32 rows (``ys_dtype="f32"``, the float32 compute dtype).
 
     ``inv = argsort(order)``; ``out = ys[inv]``; ``einsum('tkd,tk->td',
-    out, weights.astype(bf16), preferred_element_type=f32)`` (``moe.py:80-85``).
-    ``k`` ascending from +0.0; slots with ``slot_pos < 0`` (dropped) are
-    skipped.  ``residual`` (float32 [T,D]) is added last.
+    out, weights.astype(out.dtype), preferred_element_type=f32)``
+    (``moe.py:80-85``).  ``k`` ascending from +0.0; slots with
+    ``slot_pos < 0`` (dropped) are skipped.  ``residual`` (float32 [T,D]) is
+    added last.
     """
     ys = np.asarray(ys, dtype=F32)
     slot_pos = np.asarray(slot_pos).reshape(T, K)
-    g16 = bf16_round(np.asarray(gates, dtype=F32).reshape(T, K))
+    g16 = np.asarray(gates, dtype=F32).reshape(T, K)
+    if ys_dtype == "bf16":
+        g16 = bf16_round(g16)
     D = ys.shape[1]
     acc = np.zeros((T, D), dtype=F32)
     for k in range(K):
@@ -679,7 +684,8 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
     if n_shared > 0:
         residual = shared_expert(x_c, params["shared_w_gate"], params["shared_w_up"],
                                  params["shared_w_down"], n_shared, precision=precision)
-    out = combine(ys, plan["slot_pos"], gates, T, K, residual=residual)
+    out = combine(ys, plan["slot_pos"], gates, T, K, residual=residual,
+                  ys_dtype="f32" if (dtype == "f32" and expert == "swiglu") else "bf16")
     if out_dtype == "bf16":
         out = bf16_round(out)
     res = {"logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan,

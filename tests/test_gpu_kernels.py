@@ -191,26 +191,29 @@ def test_permute_rows_bit_exact(gpu, xdt):
 
 # ----------------------------------------------------------------- combine --
 
-@pytest.mark.parametrize("residual", [None, "bf16", "f32"])
+@pytest.mark.parametrize("residual,ys_dtype", [(None, "bf16"), ("bf16", "bf16"), ("f32", "bf16"),
+                                              (None, "f32")])
 @pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
-def test_combine_bit_exact(gpu, residual, out_dtype):
+def test_combine_bit_exact(gpu, residual, out_dtype, ys_dtype):
     rng = np.random.default_rng(40)
     T, D, N, Kk = 2000, 1024, 32, 4
     top = O.topk_desc(rng.standard_normal((T, N), dtype=np.float32), Kk)
     C = O.capacity_of(T, Kk, N, 1.0)
     ref = O.dispatch_plan(top, N, C)
     rows = int(ref["offsets"][-1])
-    ys = O.bf16_round(rng.standard_normal((O.rows_cap_of(T, Kk, N, C), D)).astype(np.float32))
+    ys = rng.standard_normal((O.rows_cap_of(T, Kk, N, C), D)).astype(np.float32)
+    if ys_dtype == "bf16":
+        ys = O.bf16_round(ys)
     g = rng.random((T, Kk)).astype(np.float32)
     res = None
     if residual == "bf16":
         res = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
     elif residual == "f32":
         res = rng.standard_normal((T, D)).astype(np.float32)
-    out_ref = O.combine(ys[:max(rows, 1)], ref["slot_pos"], g, T, Kk, residual=res)
+    out_ref = O.combine(ys[:max(rows, 1)], ref["slot_pos"], g, T, Kk, residual=res, ys_dtype=ys_dtype)
     plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, C)
     rt = None if res is None else (dev_bf16(res, gpu) if residual == "bf16" else dev_f32(res, gpu))
-    out = K.combine(dev_bf16(ys, gpu), plan, dev_f32(g, gpu), rt,
+    out = K.combine(dev_bf16(ys, gpu) if ys_dtype == "bf16" else dev_f32(ys, gpu), plan, dev_f32(g, gpu), rt,
                     torch.float32 if out_dtype == "f32" else torch.bfloat16)
     torch.cuda.synchronize()
     if out_dtype == "bf16":

@@ -236,3 +236,27 @@ def test_fp8_workload_full_size(gpu):
     err = O.normwise_rel_err(host(res["out"])[tokens], ref)
     print(f"fp8 full size: sampled-token normwise err {err:.3e}", flush=True)
     assert err < FP8_TOL
+
+
+@pytest.mark.parametrize("n_shared,routing,cf", [(1, "sigmoid", None), (2, "softmax", 1.25)])
+def test_moe_module_float32_compute(gpu, n_shared, routing, cf):
+    """dtype float32 (the tiny configuration's fp32): experts and shared
+    expert on the float32 matrix cores, gates kept float32 in the combine
+    (moe.py:84 casts them to the rows' dtype); against the oracle's float64
+    arithmetic on the same values."""
+    B, S, D, F, N, Kk = 4, 128, 256, 512, 8, 2
+    m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.float32, rngs=2, device=gpu,
+            routing=routing, capacity_factor=cf)
+    if routing == "sigmoid":
+        m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))
+    x = torch.randn(B, S, D, generator=torch.Generator(device=gpu).manual_seed(4), device=gpu)
+    out, aux = m(x)
+    torch.cuda.synchronize()
+    p = _params_np(m)
+    xn = x.cpu().numpy().reshape(B * S, D)
+    ref = O.moe_forward(xn, p, top_k=Kk, routing=routing, routed_scaling_factor=2.5,
+                        capacity_factor=cf, n_shared=n_shared, dtype="f32", precision="fp32",
+                        batch_shape=(B, S))
+    err = O.normwise_rel_err(host(out).reshape(B * S, D), ref["out"])
+    print(f"float32 MoE n_shared={n_shared} {routing}: normwise rel err {err:.3e}", flush=True)
+    assert out.dtype == torch.float32 and err < 1e-5

@@ -68,8 +68,13 @@ def test_moe_rejects_what_is_not_built():
     with pytest.raises(NotImplementedError):
         MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu",
             mesh=type("M", (), {"devices": np.zeros(8)})())
+    with pytest.raises(TypeError):
+        MoE(64, 32, 8, 2, 1, 0.01, 2.5, "float16", rngs=0, device="cpu")
     m = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "float32", rngs=0, device="cpu")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="GPU"):   # float32 compute is built; CPU tensors are not
+        m(torch.zeros(1, 4, 64))
+    m.router.value.requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="backward"):
         m(torch.zeros(1, 4, 64))
     m = MoE(64, 32, 8, 2, 1, 0.01, 2.5, "bfloat16", rngs=0, device="cpu")
     with pytest.raises(ValueError, match="GPU"):   # no CPU path: kernels need device tensors
