@@ -45,6 +45,7 @@ def log(*a):
 
 
 FP64_PEAK_TFLOPS = 78.6       # MI355X dense fp64 MFMA
+FP32_PEAK_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 
 
 def algorithmic(wl, kept_rows: int) -> dict:
@@ -52,11 +53,12 @@ def algorithmic(wl, kept_rows: int) -> dict:
     T, D, N, K, F = wl.tokens, wl.d_model, wl.n_experts, wl.top_k, wl.d_ff
     R = T * K
     fp8 = wl.expert_dtype == "fp8"
-    ex = 1 if fp8 else 2  # dispatched activation bytes
+    f32 = wl.expert_dtype == "f32"
+    ex = 1 if fp8 else (4 if f32 else 2)  # dispatched activation bytes
     x_in = 4 if wl.x_dtype == "f32" else 2
     out_b = 4 if wl.out_dtype == "f32" else 2
     w_b = 2 if wl.router_w_dtype == "bf16" else 4
-    mfma_peak = FP8_PEAK_TFLOPS if fp8 else BF16_PEAK_TFLOPS
+    mfma_peak = FP8_PEAK_TFLOPS if fp8 else (FP32_PEAK_TFLOPS if f32 else BF16_PEAK_TFLOPS)
     w = {}
     if wl.router_from_logits:
         w["router"] = ("hbm", T * N * 4 + T * K * 8, HBM_PEAK_GBS)
@@ -207,9 +209,14 @@ def main():
             ys = K.grouped_down(h, plan.offsets, layer.w_down)
             mark()
         else:
-            xs = K.permute_rows(layer.x, plan, torch.bfloat16)
+            xs = K.permute_rows(layer.x, plan, torch.float32 if layer.f32 else torch.bfloat16)
             mark()
-            if wl.expert == "swiglu":
+            if wl.expert == "swiglu" and layer.f32:
+                h = K.grouped_gate_up_f32(xs, plan.offsets, layer.w_gate, layer.w_up)
+                mark()
+                ys = K.grouped_down_f32(h, plan.offsets, layer.w_down_f32)
+                mark()
+            elif wl.expert == "swiglu":
                 h = K.grouped_gate_up(xs, plan.offsets, layer.w_gate_up)
                 mark()
                 ys = K.grouped_down(h, plan.offsets, layer.w_down)
@@ -280,6 +287,7 @@ def main():
         # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
         kname = ("grouped_gemm_dma<true, true>" if fp8
+                 else "grouped_gemm_f32_kernel<true>" if wl.expert_dtype == "f32"
                  else f"grouped_gemm_regs<true, {'true' if odd else 'false'}, "
                       f"{'true' if fused else 'false'}, false>")
         flop, peak = work["gate_up"][1], work["gate_up"][2]
@@ -325,7 +333,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8-e4m3" if fp8 else "bf16",
+        "dtype": "fp8-e4m3" if fp8 else ("f32" if wl.expert_dtype == "f32" else "bf16"),
         "data": "synthetic (seeded normal inputs and weights, fixed draw order)",
         "config": {"workload": name, "tokens": wl.tokens, "d_model": wl.d_model,
                    "n_experts": wl.n_experts, "top_k": wl.top_k, "d_ff": wl.d_ff,

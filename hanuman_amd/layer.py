@@ -20,10 +20,11 @@ _TORCH_DT = {"bf16": torch.bfloat16, "f32": torch.float32}
 class DeviceLayer:
     def __init__(self, inp: Inputs, device: str | torch.device = "cuda"):
         wl: Workload = inp.wl
-        if wl.expert_dtype not in ("bf16", "fp8"):
+        if wl.expert_dtype not in ("bf16", "fp8", "f32"):
             raise NotImplementedError(f"{wl.name}: expert dtype {wl.expert_dtype} is not built")
         self.wl = wl
         self.fp8 = wl.expert_dtype == "fp8"
+        self.f32 = wl.expert_dtype == "f32"
         dev = torch.device(device)
         self.device = dev
         self.x = torch.from_numpy(inp.x).to(dev, _TORCH_DT[wl.x_dtype]).contiguous()
@@ -39,7 +40,13 @@ class DeviceLayer:
         self.w_down = None
         self.w_gate_up_scale = None
         self.w_down_scale = None
-        if wl.expert == "swiglu":
+        self.w_gate = self.w_up = self.w_down_f32 = None
+        if wl.expert == "swiglu" and self.f32:
+            # float32 compute: the masters as they are
+            self.w_gate = torch.from_numpy(inp.w_gate).to(dev).contiguous()
+            self.w_up = torch.from_numpy(inp.w_up).to(dev).contiguous()
+            self.w_down_f32 = torch.from_numpy(inp.w_down).to(dev).contiguous()
+        elif wl.expert == "swiglu":
             wg = torch.from_numpy(inp.w_gate).to(dev)
             wu = torch.from_numpy(inp.w_up).to(dev)
             if self.fp8:
@@ -86,6 +93,10 @@ class DeviceLayer:
         if self.fp8:
             xs, xs_s, h, h_q, h_s, ys = self.experts_fp8(plan)
             extra = {"xs_scale": xs_s, "h_q": h_q, "h_scale": h_s}
+        elif self.f32:
+            xs = K.permute_rows(self.x, plan, torch.float32)
+            h = K.grouped_gate_up_f32(xs, plan.offsets, self.w_gate, self.w_up)
+            ys = K.grouped_down_f32(h, plan.offsets, self.w_down_f32)
         elif self.fused_dispatch:
             xs = None
             h = K.grouped_gate_up_gather(self.x, plan, self.w_gate_up)

@@ -30,7 +30,7 @@ class Workload:
     expert: str = "swiglu"    # "swiglu" | "identity"
     zipf_bias: bool = False   # per-expert logit bias 3 * rank^-1.1
     router_w_dtype: str = "f32"
-    expert_dtype: str = "bf16"  # "bf16" | "fp8"
+    expert_dtype: str = "bf16"  # "bf16" | "fp8" | "f32" (float32 compute)
     out_dtype: str = "f32"
     batch: int = 1
     weight_std: float = 0.02
@@ -60,7 +60,7 @@ class Workload:
 
 WORKLOADS = {
     "tiny_fp32": Workload("tiny_fp32", tokens=2048, d_model=256, n_experts=8, top_k=2, d_ff=512,
-                          capacity_factor=1.25, x_dtype="f32", batch=4),
+                          capacity_factor=1.25, x_dtype="f32", expert_dtype="f32", batch=4),
     "dispatch_identity": Workload("dispatch_identity", tokens=32768, d_model=2048, n_experts=64,
                                   top_k=8, d_ff=0, capacity_factor=1.0, router_from_logits=True,
                                   expert="identity"),
