@@ -435,3 +435,34 @@ def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype):
     print(f"  d_router (aux only): normwise {err:.2e}", flush=True)
     assert err < 1e-4
     assert float(m.expert_w_gate.value.grad.abs().max()) == 0.0
+
+
+def test_module_trains(gpu):
+    """End to end: the module as the reference's train step uses it
+    (train.py:191-200: output loss plus weighted z and balance losses),
+    Adam on every trainable parameter through torch autograd; a target made
+    by a second MoE of the same shape is learnable, so the loss must fall."""
+    torch.manual_seed(0)
+    Bq, Sq, D, F, N, Kk = 2, 128, 256, 256, 8, 2
+    student = MoE(D, F, N, Kk, 1, 0.05, 2.5, torch.bfloat16, rngs=3, device=gpu)
+    teacher = MoE(D, F, N, Kk, 1, 0.05, 2.5, torch.bfloat16, rngs=4, device=gpu)
+    x = torch.randn(Bq, Sq, D, generator=torch.Generator(device=gpu).manual_seed(6),
+                    device=gpu).to(torch.bfloat16)
+    with torch.no_grad():
+        target, _ = teacher(x)
+    params = [p.value for n, p in student.named_params().items() if n != "bias"]
+    for p in params:
+        p.requires_grad_(True)
+    opt = torch.optim.Adam(params, lr=3e-3)
+    losses = []
+    for step in range(40):
+        opt.zero_grad(set_to_none=True)
+        out, aux = student(x)
+        loss = ((out - target) ** 2).mean() + 1e-3 * aux["router_z_loss"] \
+            + 1e-2 * aux["balance_loss"]
+        loss.backward()
+        opt.step()
+        losses.append(float(loss))
+    print(f"module training: loss {losses[0]:.4e} -> {losses[-1]:.4e}", flush=True)
+    assert all(np.isfinite(losses))
+    assert losses[-1] < 0.5 * losses[0]
