@@ -38,28 +38,72 @@ __global__ __launch_bounds__(256) void pack_transpose_kernel(const TW* __restric
   const int p0 = blockIdx.x * 64;  // destination row (output column, packed)
   const int dst_rows = GATE_UP ? 2 * cols_c : cols_c;
   const int64_t src_stride_e = static_cast<int64_t>(rows_r) * cols_c;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int rr = ty; rr < 64; rr += 4) {
-    const int r = r0 + rr;
-    const int p = p0 + tx;
-    float v = 0.0f;
-    if (r < rows_r && p < dst_rows) {
-      const TW* s = src0;
-      int col = p;
-      if (GATE_UP) {
-        s = ((p & 63) < 32) ? src0 : src1;
-        col = (p >> 6) * 32 + (p & 31);
-      }
-      v = load_w(s, e * src_stride_e + static_cast<int64_t>(r) * cols_c + col);
+  const int tid = threadIdx.x;
+  // Load: 4 consecutive tile columns per thread (16 threads per source row,
+  // 16 rows per pass); the four stay inside one 32-column gate or up block.
+  {
+    const int q = (tid & 15) * 4;
+    const int p = p0 + q;
+    const TW* srcp = src0;
+    int col = p;
+    if (GATE_UP) {
+      srcp = ((p & 63) < 32) ? src0 : src1;
+      col = (p >> 6) * 32 + (p & 31);
     }
-    tile[rr][tx] = v;
+    const bool vec = p + 3 < dst_rows && (cols_c & 3) == 0;  // aligned 4-column groups
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const int rr = (tid >> 4) + 16 * pass;
+      const int r = r0 + rr;
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (r < rows_r) {
+        const int64_t base = e * src_stride_e + static_cast<int64_t>(r) * cols_c + col;
+        if (vec) {
+          if constexpr (sizeof(TW) == 4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(srcp + base);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = x[k];
+          } else {
+            const uint2 x = *reinterpret_cast<const uint2*>(srcp + base);
+            v[0] = __uint_as_float(x.x << 16);
+            v[1] = __uint_as_float(x.x & 0xffff0000u);
+            v[2] = __uint_as_float(x.y << 16);
+            v[3] = __uint_as_float(x.y & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (p + k < dst_rows) v[k] = load_w(srcp, base + k);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) tile[rr][q + k] = v[k];
+    }
   }
   __syncthreads();
-  for (int pp = ty; pp < 64; pp += 4) {
-    const int p = p0 + pp;
-    const int r = r0 + tx;
-    if (p < dst_rows && r < rows_r)
-      dst[(static_cast<int64_t>(e) * dst_rows + p) * rows_r + r] = f32_to_bf16_bits(tile[tx][pp]);
+  // Store: 8 consecutive reduction-dim values of one destination row per
+  // thread as one 16-byte store (8 threads per 128-byte row, 32 rows per
+  // pass).
+  {
+    const int r8 = (tid & 7) * 8;
+    const int r = r0 + r8;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int pp = (tid >> 3) + 32 * pass;
+      const int p = p0 + pp;
+      if (p >= dst_rows) continue;
+      uint16_t* d = dst + (static_cast<int64_t>(e) * dst_rows + p) * rows_r + r;
+      if (r + 7 < rows_r && (rows_r & 7) == 0) {
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          o[k] = static_cast<uint32_t>(f32_to_bf16_bits(tile[r8 + 2 * k][pp])) |
+                 (static_cast<uint32_t>(f32_to_bf16_bits(tile[r8 + 2 * k + 1][pp])) << 16);
+        *reinterpret_cast<u32x4*>(d) = o;
+      } else {
+        for (int k = 0; k < 8 && r + k < rows_r; ++k) d[k] = f32_to_bf16_bits(tile[r8 + k][pp]);
+      }
+    }
   }
 }
 
