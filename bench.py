@@ -16,13 +16,18 @@ input resident in HBM before the timed region.  One JSON line on stdout:
              this host's cores on up to 16384 tokens of the same workload (all of
              the headline workload)
 
-With --backward the line is the data-gradient backward pass instead (bf16
-SwiGLU workloads): combine VJP, g/u recompute, both data-gradient GEMMs,
-SwiGLU VJP, gather VJP and router VJP, timed per stage the same way, for the
+With --backward the line is the layer backward instead (bf16 SwiGLU
+workloads): data and weight gradients, timed per stage the same way, for the
 cotangent of the layer output; the forward's intermediates are computed once
 before the timed region.
 
-Usage: python bench.py [--steps K] [--warmup W] [--spinup-ms MS] [--workload NAME] [--no-cpu-baseline] [--backward]
+With --train the line is one training step of the drop-in module
+(hanuman_amd.moe.MoE at the workload's shape, plus its one shared expert):
+forward, loss.backward() through the module's autograd node (output, z and
+balance losses, as train.py:191-200), and an in-place parameter update, so
+every step re-packs the expert operands as a trainer's step does.
+
+Usage: python bench.py [--steps K] [--warmup W] [--spinup-ms MS] [--workload NAME] [--no-cpu-baseline] [--backward | --train]
 """
 from __future__ import annotations
 
@@ -139,6 +144,8 @@ def main():
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384,
                     help="tokens of the CPU-baseline sample (capped at the workload's; the "
                          "default is the whole headline workload, ~10 s of CPU work)")
+    ap.add_argument("--train", action="store_true",
+                    help="time one training step of the MoE module (forward, backward, update)")
     ap.add_argument("--backward", action="store_true",
                     help="time the data-gradient backward pass instead of the forward")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -171,6 +178,10 @@ def main():
     fp8 = wl.expert_dtype == "fp8"
     if args.backward:
         bench_backward(args, name, wl, layer)
+        return
+    if args.train:
+        del layer
+        bench_train(args, name, wl)
         return
     # bf16 SwiGLU experts: the row permutation is done by the gate/up GEMM's
     # own loads (no dispatched copy of x), so there is no separate stage.
@@ -481,6 +492,66 @@ def bench_backward(args, name, wl, layer):
         "roofline": roofline, "kernels": kernels, "cpu_baseline": None,
         "data_gradients_ms": round(sum(stage_ms[st] for st in stages[:stages.index("permute_xs")]), 4),
         "weight_gradients_ms": round(sum(stage_ms[st] for st in stages[stages.index("permute_xs"):]), 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_train(args, name, wl):
+    """One training step of the drop-in module at `wl`'s shape."""
+    import torch
+    from hanuman_amd.moe import MoE
+
+    if wl.router_from_logits or wl.expert != "swiglu" or wl.expert_dtype != "bf16":
+        raise SystemExit("--train needs a bf16 SwiGLU workload with a router weight")
+    dev = torch.device("cuda", 0)
+    B = wl.batch if wl.tokens % wl.batch == 0 else 1
+    S = wl.tokens // B
+    m = MoE(wl.d_model, wl.d_ff, wl.n_experts, wl.top_k, 1, 0.02, 1.0, torch.bfloat16,
+            rngs=args.seed, device=dev, routing=wl.routing, capacity_factor=wl.capacity_factor)
+    params = [p.value for n, p in m.named_params().items() if n != "bias"]
+    for p in params:
+        p.requires_grad_(True)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    x = torch.randn(B, S, wl.d_model, generator=gen, device=dev).to(torch.bfloat16)
+    dy = torch.randn(B, S, wl.d_model, generator=gen, device=dev)
+
+    def step():
+        for p in params:
+            p.grad = None
+        out, aux = m(x)
+        loss = (out * dy).sum() + 1e-3 * aux["router_z_loss"] + 1e-2 * aux["balance_loss"]
+        loss.backward()
+        with torch.no_grad():   # the update: every master changes, so the operands re-pack
+            for p in params:
+                p.add_(p.grad, alpha=-1e-9)
+
+    t_warm = time.perf_counter()
+    warm_steps = 0
+    while warm_steps < args.warmup or (time.perf_counter() - t_warm) * 1e3 < args.spinup_ms:
+        step()
+        warm_steps += 1
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    log(f"[bench] train step {ms:.4f} ms/step, {wl.tokens / ms / 1e3:.3f} M tokens/s")
+    line = {
+        "metric": "MoE layer training step (forward, backward, update) tokens/s (1 GPU)",
+        "value": round(wl.tokens / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "warmup_steps_run": warm_steps,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded normal inputs, weights and output cotangent)",
+        "config": {"workload": name + " training step (module with one shared expert)",
+                   "tokens": wl.tokens, "d_model": wl.d_model, "n_experts": wl.n_experts,
+                   "top_k": wl.top_k, "d_ff": wl.d_ff, "capacity_factor": wl.capacity_factor,
+                   "n_shared_experts": 1, "parallelism": "single GPU, all experts resident"},
+        "roofline": None, "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
 
