@@ -78,6 +78,14 @@ SIGNATURES = {
     "hmoe_router_aux_bwd": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz, _vp]),
     "hmoe_grouped_gate_up_f32": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hmoe_grouped_down_f32": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_combine_bwd_f32": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _f32, _vp]),
+    "hmoe_grouped_dgrad_down_f32": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_swiglu_bwd_f32": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp,
+                                                   _vp, _vp, _vp]),
+    "hmoe_grouped_dgrad_gate_up_f32": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp,
+                                              _vp]),
+    "hmoe_grouped_wgrad_gate_up_f32": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_grouped_wgrad_down_f32": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "hmoe_router_dx": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp]),
     "hmoe_grouped_wgrad_down": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
     "hmoe_grouped_wgrad_gate_up": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),

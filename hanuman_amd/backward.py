@@ -31,6 +31,10 @@ all tokens, its output cotangent ``bf16(dy / n_shared)`` from
 ``hmoe_combine_bwd``) and the aux losses (``moe.py:253-283``,
 ``hmoe_router_aux_bwd`` into ``d_logits``).
 
+For the float32 compute dtype, :func:`moe_backward_f32` is the same VJP on
+the float32 kernels (``hmoe_combine_bwd_f32``, ``hmoe_grouped_*_f32``) with
+the masters as they are and no rounding points.
+
 Every step runs in the library on the current stream; there is no CPU
 fallback.
 """
@@ -185,6 +189,74 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
     dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, plan.offsets)
     del xs, dgu
     dwd = K.grouped_wgrad_down(fwd["h"], d_ys, plan.offsets)
+    d_router = K.router_dw(x, d_logits) if router_w is not None else None
+    res.update(dx=dx, d_router=d_router, dWg=dwg, dWu=dwu, dWd=dwd, d_logits=d_logits,
+               d_gates=d_gates)
+    return res
+
+
+def _shared_backward_f32(x32: torch.Tensor, d_shared: torch.Tensor, h_shared, masters) -> dict:
+    """Float32 VJP of the shared expert(s): ``masters = (w_gate, w_up, w_down,
+    n_shared)`` (2-D for one shared expert, stacked for several), ``d_shared =
+    dy / n_shared``, ``h_shared`` the forward's ``h`` per shared expert."""
+    w_gate, w_up, w_down, n_shared = masters
+    if n_shared == 1:
+        w_gate, w_up, w_down = (w.unsqueeze(0) for w in (w_gate, w_up, w_down))
+    T = x32.shape[0]
+    off = torch.tensor([0, T], dtype=torch.int32, device=x32.device)
+    dx, dwg, dwu, dwd = None, [], [], []
+    for i, h in enumerate(h_shared):
+        wg, wu, wd = (w[i:i + 1].contiguous() for w in (w_gate, w_up, w_down))
+        dh = K.grouped_dgrad_down_f32(d_shared, off, wd)
+        dgu = K.grouped_gate_up_swiglu_bwd_f32(x32, off, wg, wu, dh)
+        d = K.grouped_dgrad_gate_up_f32(dgu, off, wg, wu)
+        dx = d if dx is None else dx.add_(d)
+        g_, u_ = K.grouped_wgrad_gate_up_f32(x32, dgu, off)
+        dwg.append(g_)
+        dwu.append(u_)
+        dwd.append(K.grouped_wgrad_down_f32(h, d_shared, off))
+    return {"dx": dx, "dWg": torch.cat(dwg), "dWu": torch.cat(dwu), "dWd": torch.cat(dwd)}
+
+
+def moe_backward_f32(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict, masters, dy,
+                     *, mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0,
+                     shared=None, h_shared=None, aux: tuple | None = None) -> dict:
+    """:func:`moe_backward` for the float32 compute dtype: ``masters =
+    (w_gate, w_up, w_down)`` float32 as they are, ``fwd`` adds the forward's
+    dispatched rows ``xs`` (float32), ``shared = (w_gate, w_up, w_down,
+    n_shared)`` or None.  Same results dict."""
+    plan = fwd["plan"]
+    N = plan.n_experts
+    wg, wu, wd = masters
+    n_sh = shared[3] if shared is not None else 0
+    d_ys, d_gates, d_sh = K.combine_bwd_f32(dy, fwd["ys"], plan, fwd["gates"], n_sh)
+    xs = fwd["xs"]
+    dh = K.grouped_dgrad_down_f32(d_ys, plan.offsets, wd)
+    dgu = K.grouped_gate_up_swiglu_bwd_f32(xs, plan.offsets, wg, wu, dh)
+    del dh
+    d_xs = K.grouped_dgrad_gate_up_f32(dgu, plan.offsets, wg, wu)
+    res = {}
+    residual = None
+    if shared is not None:
+        x32 = x if x.dtype == torch.float32 else x.float()   # x.astype(dtype), moe.py:198
+        sh = _shared_backward_f32(x32.contiguous(), d_sh, h_shared, shared)
+        residual = sh["dx"]
+        dws = [sh[k] for k in ("dWg", "dWu", "dWd")]
+        if n_sh == 1:
+            dws = [w[0] for w in dws]
+        res.update(dWg_shared=dws[0], dWu_shared=dws[1], dWd_shared=dws[2])
+    dx = K.gather_bwd(d_xs, plan, residual=residual)
+    del d_xs, residual
+    d_logits = K.router_bwd(fwd["logits"], fwd["top_idx"], fwd["gates"], d_gates, N, mode,
+                            routed_scaling_factor)
+    if aux is not None:
+        batch, seq, d_losses = aux
+        K.router_aux_bwd(fwd["logits"], fwd["top_idx"], batch, seq, d_losses, d_logits)
+    if router_w is not None:
+        K.router_dx(d_logits, router_w, dx)
+    dwg, dwu = K.grouped_wgrad_gate_up_f32(xs, dgu, plan.offsets)
+    del dgu
+    dwd = K.grouped_wgrad_down_f32(fwd["h"], d_ys, plan.offsets)
     d_router = K.router_dw(x, d_logits) if router_w is not None else None
     res.update(dx=dx, d_router=d_router, dWg=dwg, dWu=dwu, dWd=dwd, d_logits=d_logits,
                d_gates=d_gates)

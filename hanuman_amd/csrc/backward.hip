@@ -97,6 +97,57 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
   if (lane == 0) d_gates[w] = pos >= 0 ? bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(part))) : 0.0f;
 }
 
+// Float32 rows (compute dtype float32): d_ys[pos(t,k)] = dy[t] * g[t,k] and
+// d_g[t,k] = f32(sum_d dy[t,d] * ys[pos,d]), the sum in float64 (products of
+// two float32 values are exact there), lane partials in column order, then a
+// fixed tree; d_shared[t] = dy[t] / shared_div.  Same wave layout as above.
+__global__ __launch_bounds__(256) void combine_bwd_f32_kernel(
+    const float* __restrict__ dy, const float* __restrict__ ys,
+    const int32_t* __restrict__ slot_pos, const float* __restrict__ gates, int64_t tokens,
+    int top_k, int d_model, float* __restrict__ d_ys, float* __restrict__ d_gates,
+    float* __restrict__ d_shared, float shared_div) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (w >= tokens * top_k) return;
+  const int64_t t = w / top_k;
+  const int k = static_cast<int>(w - t * top_k);
+  const int32_t pos = slot_pos[w];
+  const bool shared = d_shared != nullptr && k == 0;
+  if (pos < 0 && !shared) {
+    if (lane == 0) d_gates[w] = 0.0f;
+    return;
+  }
+  const float g = gates[w];
+  const int chunks = d_model / 4;
+  const float* dy_row = dy + t * d_model;
+  const float* y_row = ys + static_cast<int64_t>(pos < 0 ? 0 : pos) * d_model;
+  float* o_row = d_ys + static_cast<int64_t>(pos < 0 ? 0 : pos) * d_model;
+  double part = 0.0;
+  for (int c = lane; c < chunks; c += 64) {
+    const f32x4 d = *reinterpret_cast<const f32x4*>(dy_row + c * 4);
+    if (shared) {
+      f32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = d[i] / shared_div;
+      *reinterpret_cast<f32x4*>(d_shared + t * d_model + c * 4) = o;
+    }
+    if (pos >= 0) {
+      const f32x4 y = *reinterpret_cast<const f32x4*>(y_row + c * 4);
+      f32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] = d[i] * g;
+        part += static_cast<double>(d[i]) * static_cast<double>(y[i]);
+      }
+      *reinterpret_cast<f32x4*>(o_row + c * 4) = o;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+  if (lane == 0) d_gates[w] = pos >= 0 ? static_cast<float>(part) : 0.0f;
+}
+
 // ---- SwiGLU VJP -------------------------------------------------------------
 // h = silu(g) * u: dg = dh * u * silu'(g), du = dh * silu(g), silu'(g) =
 // s (1 + g (1 - s)), s = 1 / (1 + e^-g), in float32 with one bf16 rounding
@@ -418,6 +469,28 @@ extern "C" int hmoe_combine_bwd(const float* dy, const void* ys, const int32_t* 
                      static_cast<uint16_t*>(d_ys), d_gates, static_cast<uint16_t*>(d_shared),
                      shared_div);
   return check_launch("hmoe_combine_bwd");
+}
+
+extern "C" int hmoe_combine_bwd_f32(const float* dy, const float* ys, const int32_t* slot_pos,
+                                    const float* gates, int64_t tokens, int top_k, int d_model,
+                                    float* d_ys, float* d_gates, float* d_shared, float shared_div,
+                                    hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(tokens >= 0, "combine_bwd_f32: tokens must be >= 0");
+  HMOE_REQUIRE(top_k >= 1 && top_k <= kMaxKBwd, "combine_bwd_f32: top_k must be in [1, %d] (got %d)",
+               kMaxKBwd, top_k);
+  HMOE_REQUIRE(d_model >= 4 && d_model % 4 == 0,
+               "combine_bwd_f32: d_model must be a multiple of 4 (got %d)", d_model);
+  if (tokens == 0) return HMOE_OK;
+  HMOE_REQUIRE(dy && ys && slot_pos && gates && d_ys && d_gates,
+               "combine_bwd_f32: null pointer argument");
+  HMOE_REQUIRE(d_shared == nullptr || shared_div >= 1.0f,
+               "combine_bwd_f32: shared_div must be the number of shared experts (>= 1)");
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens * top_k, 4)));
+  hipLaunchKernelGGL(combine_bwd_f32_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     dy, ys, slot_pos, gates, tokens, top_k, d_model, d_ys, d_gates, d_shared,
+                     shared_div);
+  return check_launch("hmoe_combine_bwd_f32");
 }
 
 extern "C" int hmoe_swiglu_bwd(const void* dh, const void* gu, const int32_t* offsets,

@@ -307,6 +307,112 @@ def grouped_gate_up_f32(xs: torch.Tensor, offsets: torch.Tensor, w_gate: torch.T
     return h
 
 
+def combine_bwd_f32(dy: torch.Tensor, ys: torch.Tensor, plan: Plan, gates: torch.Tensor,
+                    n_shared: int = 0):
+    """VJP of :func:`combine` for float32 rows (compute dtype float32):
+    ``(d_ys f32 [rows, D], d_gates f32 [T, K], d_shared)`` with ``d_shared =
+    dy / n_shared`` ``[T, D]`` when ``n_shared > 0``, else None."""
+    for t, n in ((dy, "dy"), (ys, "ys"), (gates, "gates")):
+        _check(t, n, 2)
+    T, D = dy.shape
+    K = plan.top_k
+    if (dy.dtype != torch.float32 or ys.dtype != torch.float32 or ys.shape[1] != D
+            or tuple(gates.shape) != (T, K) or gates.dtype != torch.float32
+            or plan.slot_pos.numel() != T * K):
+        raise ValueError("combine_bwd_f32: inconsistent shapes or dtypes")
+    d_ys = torch.empty_like(ys)
+    d_g = torch.empty((T, K), dtype=torch.float32, device=dy.device)
+    d_sh = torch.empty((T, D), dtype=torch.float32, device=dy.device) if n_shared > 0 else None
+    call("hmoe_combine_bwd_f32", _ptr(dy), _ptr(ys), _ptr(plan.slot_pos), _ptr(gates), T, K, D,
+         _ptr(d_ys), _ptr(d_g), _ptr(d_sh), float(max(n_shared, 1)), _stream())
+    return d_ys, d_g, d_sh
+
+
+def _f32_operands(name: str, *ts):
+    for t in ts:
+        _check(t, name)
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name} takes float32 operands")
+
+
+def grouped_dgrad_down_f32(d_ys: torch.Tensor, offsets: torch.Tensor,
+                           w_down: torch.Tensor) -> torch.Tensor:
+    """Float32 ``dh = d_ys Wd[e]^T`` per expert segment, ``[rows, F]``."""
+    _f32_operands("grouped_dgrad_down_f32", d_ys, w_down)
+    _check(offsets, "offsets", 1)
+    R, D = d_ys.shape
+    N, F, D2 = w_down.shape
+    if D2 != D or offsets.numel() != N + 1:
+        raise ValueError("grouped_dgrad_down_f32: inconsistent shapes")
+    dh = torch.empty((R, F), dtype=torch.float32, device=d_ys.device)
+    call("hmoe_grouped_dgrad_down_f32", _ptr(d_ys), _ptr(offsets), N, R, D, F, _ptr(w_down),
+         _ptr(dh), _stream())
+    return dh
+
+
+def grouped_gate_up_swiglu_bwd_f32(xs: torch.Tensor, offsets: torch.Tensor, w_gate: torch.Tensor,
+                                   w_up: torch.Tensor, dh: torch.Tensor) -> torch.Tensor:
+    """g, u recomputed from ``xs`` and the VJP of ``h = silu(g) * u``:
+    float32 ``[rows, 2F]`` = ``[dg | du]``."""
+    _f32_operands("grouped_gate_up_swiglu_bwd_f32", xs, w_gate, w_up, dh)
+    _check(offsets, "offsets", 1)
+    R, D = xs.shape
+    N, D2, F = w_gate.shape
+    if (D2 != D or tuple(w_up.shape) != (N, D, F) or tuple(dh.shape) != (R, F)
+            or offsets.numel() != N + 1):
+        raise ValueError("grouped_gate_up_swiglu_bwd_f32: inconsistent shapes")
+    dgu = torch.empty((R, 2 * F), dtype=torch.float32, device=xs.device)
+    call("hmoe_grouped_gate_up_swiglu_bwd_f32", _ptr(xs), _ptr(offsets), N, R, D, F, _ptr(w_gate),
+         _ptr(w_up), _ptr(dh), _ptr(dgu), _stream())
+    return dgu
+
+
+def grouped_dgrad_gate_up_f32(dgu: torch.Tensor, offsets: torch.Tensor, w_gate: torch.Tensor,
+                              w_up: torch.Tensor) -> torch.Tensor:
+    """Float32 ``d_xs = dg Wg[e]^T + du Wu[e]^T`` per segment, ``[rows, D]``."""
+    _f32_operands("grouped_dgrad_gate_up_f32", dgu, w_gate, w_up)
+    _check(offsets, "offsets", 1)
+    R, F2 = dgu.shape
+    N, D, F = w_gate.shape
+    if F2 != 2 * F or tuple(w_up.shape) != (N, D, F) or offsets.numel() != N + 1:
+        raise ValueError("grouped_dgrad_gate_up_f32: inconsistent shapes")
+    d_xs = torch.empty((R, D), dtype=torch.float32, device=dgu.device)
+    call("hmoe_grouped_dgrad_gate_up_f32", _ptr(dgu), _ptr(offsets), N, R, D, F, _ptr(w_gate),
+         _ptr(w_up), _ptr(d_xs), _stream())
+    return d_xs
+
+
+def grouped_wgrad_gate_up_f32(xs: torch.Tensor, dgu: torch.Tensor, offsets: torch.Tensor):
+    """Float32 ``(dWg, dWu)`` ``[N, D, F]`` = ``xs^T dg``, ``xs^T du`` per segment."""
+    _f32_operands("grouped_wgrad_gate_up_f32", xs, dgu)
+    _check(offsets, "offsets", 1)
+    R, D = xs.shape
+    F = dgu.shape[1] // 2
+    if dgu.shape[0] != R or dgu.shape[1] != 2 * F:
+        raise ValueError("grouped_wgrad_gate_up_f32: inconsistent shapes")
+    N = offsets.numel() - 1
+    dwg = torch.empty((N, D, F), dtype=torch.float32, device=xs.device)
+    dwu = torch.empty((N, D, F), dtype=torch.float32, device=xs.device)
+    call("hmoe_grouped_wgrad_gate_up_f32", _ptr(xs), _ptr(dgu), _ptr(offsets), N, D, F, _ptr(dwg),
+         _ptr(dwu), _stream())
+    return dwg, dwu
+
+
+def grouped_wgrad_down_f32(h: torch.Tensor, d_ys: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
+    """Float32 ``dWd[e] = h^T d_ys`` per segment, ``[N, F, D]``."""
+    _f32_operands("grouped_wgrad_down_f32", h, d_ys)
+    _check(offsets, "offsets", 1)
+    R, F = h.shape
+    D = d_ys.shape[1]
+    if d_ys.shape[0] != R:
+        raise ValueError("grouped_wgrad_down_f32: h and d_ys must have the same rows")
+    N = offsets.numel() - 1
+    dwd = torch.empty((N, F, D), dtype=torch.float32, device=h.device)
+    call("hmoe_grouped_wgrad_down_f32", _ptr(h), _ptr(d_ys), _ptr(offsets), N, F, D, _ptr(dwd),
+         _stream())
+    return dwd
+
+
 def grouped_down_f32(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor) -> torch.Tensor:
     """Float32 ``ys = h Wd[e]`` per expert segment (``moe.py:73``), master
     ``[N, F, D]`` as it is."""

@@ -66,12 +66,15 @@ def _require_bf16_compute(dtype: torch.dtype):
             f"compute dtype {dtype} is not built")
 
 
-def _f32_swiglu_one(x32: torch.Tensor, wg, wu, wd) -> torch.Tensor:
+def _f32_swiglu_one(x32: torch.Tensor, wg, wu, wd, hs: list | None = None) -> torch.Tensor:
     """One float32 SwiGLU (``moe.py:23-29`` with dtype float32): one segment
-    of all rows on the float32 grouped GEMMs, masters as they are."""
+    of all rows on the float32 grouped GEMMs, masters as they are.  ``hs``
+    collects ``h`` for the backward."""
     off = _offsets_one_group(x32.shape[0], x32.device)
     h = K.grouped_gate_up_f32(x32, off, wg.float().unsqueeze(0).contiguous(),
                               wu.float().unsqueeze(0).contiguous())
+    if hs is not None:
+        hs.append(h)
     return K.grouped_down_f32(h, off, wd.float().unsqueeze(0).contiguous())
 
 
@@ -273,10 +276,10 @@ class MoE:
         if self.dtype == torch.float32:
             wg, wu, wdn = self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value
             if self.n_shared_experts == 1:
-                return _f32_swiglu_one(x_flat, wg, wu, wdn)
+                return _f32_swiglu_one(x_flat, wg, wu, wdn, hs)
             acc = torch.zeros((T, wdn.shape[-1]), dtype=torch.float32, device=x_flat.device)
             for i in range(self.n_shared_experts):
-                acc += _f32_swiglu_one(x_flat, wg[i], wu[i], wdn[i])
+                acc += _f32_swiglu_one(x_flat, wg[i], wu[i], wdn[i], hs)
             return acc / self.n_shared_experts
         for wgu, wd in self._packed_shared():
             h = K.grouped_gate_up(x_flat, off, wgu)
@@ -305,8 +308,6 @@ class MoE:
         are differentiable, ``expert_counts`` is not (``train.py:191-200``
         differentiates the same outputs)."""
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self._params())):
-            if self.dtype != torch.bfloat16:
-                raise NotImplementedError("the backward is built for the bfloat16 compute dtype")
             out, z, bal, ent, counts = _MoEFunction.apply(self, x, *self._params())
             return out, {"router_z_loss": z, "balance_loss": bal, "mean_entropy": ent,
                          "expert_counts": counts}
@@ -342,10 +343,16 @@ class MoE:
             h = K.grouped_gate_up_f32(xs, plan.offsets, self.expert_w_gate.value.float().contiguous(),
                                       self.expert_w_up.value.float().contiguous())
             ys = K.grouped_down_f32(h, plan.offsets, self.expert_w_down.value.float().contiguous())
-            shared = self._shared_ffn(x2.float().contiguous())
+            hs = [] if save else None
+            shared = self._shared_ffn(x2.float().contiguous(), hs)
             out = K.combine(ys, plan, gates, shared, torch.float32)
             losses, counts = K.router_aux(logits, top_idx, B, S)
-            return out.reshape(B, S, D), losses, counts, None
+            saved = None
+            if save:
+                saved = {"x": x2, "logits": logits, "top_idx": top_idx, "gates": gates,
+                         "plan": plan, "xs": xs, "h": h, "ys": ys, "h_shared": hs, "mode": mode,
+                         "rsf": rsf, "batch": B, "seq": S}
+            return out.reshape(B, S, D), losses, counts, saved
         wgu, wd = self._packed_routed()
         if x2.dtype == torch.bfloat16:
             # the gate/up GEMM gathers its rows from x (moe.py:56 fused)
@@ -397,7 +404,7 @@ class _MoEFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_out, d_z, d_bal, d_ent, d_counts):
-        from .backward import moe_backward
+        from .backward import moe_backward, moe_backward_f32
         layer, sv = ctx.layer, ctx.saved
         ctx.saved = None
         x2 = sv["x"]
@@ -408,14 +415,26 @@ class _MoEFunction(torch.autograd.Function):
         zero = torch.zeros((), dtype=torch.float32, device=dev)
         d_losses = torch.stack([(g.float() if g is not None else zero)
                                 for g in (d_z, d_bal, d_ent)]).contiguous()
-        ops, shared = layer._backward_operands()
-        wgu, _ = layer._packed_routed()
         router_w = layer.router.value.float().contiguous()
-        g = moe_backward(x2, router_w, {k: sv[k] for k in ("logits", "top_idx", "gates", "plan",
-                                                           "h", "ys")},
-                         wgu, ops, dy, mode=sv["mode"], routed_scaling_factor=sv["rsf"],
-                         shared=shared, h_shared=sv["h_shared"],
-                         aux=(sv["batch"], sv["seq"], d_losses))
+        aux = (sv["batch"], sv["seq"], d_losses)
+        if layer.dtype == torch.float32:
+            masters = tuple(p.value.float().contiguous() for p in
+                            (layer.expert_w_gate, layer.expert_w_up, layer.expert_w_down))
+            shared = None
+            if layer.n_shared_experts > 0:
+                shared = tuple(p.value.float().contiguous() for p in
+                               (layer.shared_w_gate, layer.shared_w_up, layer.shared_w_down))
+                shared = shared + (layer.n_shared_experts,)
+            g = moe_backward_f32(x2, router_w, sv, masters, dy, mode=sv["mode"],
+                                 routed_scaling_factor=sv["rsf"], shared=shared,
+                                 h_shared=sv["h_shared"], aux=aux)
+        else:
+            ops, shared = layer._backward_operands()
+            wgu, _ = layer._packed_routed()
+            g = moe_backward(x2, router_w, {k: sv[k] for k in ("logits", "top_idx", "gates",
+                                                               "plan", "h", "ys")},
+                             wgu, ops, dy, mode=sv["mode"], routed_scaling_factor=sv["rsf"],
+                             shared=shared, h_shared=sv["h_shared"], aux=aux)
         dx = g["dx"].reshape(ctx.x_shape).to(ctx.x_dtype)
         sg, su, sd = ctx.shared_shapes
         return (None, dx, g["d_router"], g["dWg"], g["dWu"], g["dWd"],

@@ -216,6 +216,45 @@ int hmoe_grouped_down_f32(const float* h, const int32_t* offsets, int n_experts,
                           int64_t rows_cap, int d_ff, int d_model, const float* w_down, float* ys,
                           hmoe_stream_t stream);
 
+/* Backward of the float32 compute dtype (the VJP of moe.py:70-85 with
+ * dtype = float32, routing held fixed; replaces what jax.value_and_grad,
+ * train.py:266, derives for these lines), on the masters as they are.
+ * d_model and d_ff are multiples of 64 in all of them.
+ *
+ * combine_bwd_f32: the VJP of hmoe_combine for float32 rows:
+ *   d_ys[pos(t,k)] = dy[t] * g[t,k], d_gates[t,k] = sum_d dy[t,d] *
+ *   ys[pos(t,k),d] (float64 sum, rounded once), 0 for a dropped slot;
+ *   d_shared [T, D] (or NULL) = dy / shared_div.  d_model % 4 == 0.
+ * dgrad_down_f32: dh [rows_cap, F] = d_ys W_down[e]^T per segment.
+ * gate_up_swiglu_bwd_f32: g = xs W_gate[e], u = xs W_up[e] recomputed and
+ *   dgu [rows_cap, 2F] = [dg | du] (columns [0, F) and [F, 2F)) for the
+ *   cotangent dh [rows_cap, F] of h = silu(g) * u.
+ * dgrad_gate_up_f32: d_xs [rows_cap, D] = dg W_gate[e]^T + du W_up[e]^T.
+ * wgrad_gate_up_f32: dw_gate, dw_up [N, D, F] = xs^T dg, xs^T du over each
+ *   segment (an empty segment gives zeros).
+ * wgrad_down_f32: dw_down [N, F, D] = h^T d_ys over each segment.
+ * Rows past offsets[N] are neither read by the weight gradients nor
+ * written by the others. */
+int hmoe_combine_bwd_f32(const float* dy, const float* ys, const int32_t* slot_pos,
+                         const float* gates, int64_t tokens, int top_k, int d_model, float* d_ys,
+                         float* d_gates, float* d_shared, float shared_div, hmoe_stream_t stream);
+int hmoe_grouped_dgrad_down_f32(const float* d_ys, const int32_t* offsets, int n_experts,
+                                int64_t rows_cap, int d_model, int d_ff, const float* w_down,
+                                float* dh, hmoe_stream_t stream);
+int hmoe_grouped_gate_up_swiglu_bwd_f32(const float* xs, const int32_t* offsets, int n_experts,
+                                        int64_t rows_cap, int d_model, int d_ff,
+                                        const float* w_gate, const float* w_up, const float* dh,
+                                        float* dgu, hmoe_stream_t stream);
+int hmoe_grouped_dgrad_gate_up_f32(const float* dgu, const int32_t* offsets, int n_experts,
+                                   int64_t rows_cap, int d_model, int d_ff, const float* w_gate,
+                                   const float* w_up, float* d_xs, hmoe_stream_t stream);
+int hmoe_grouped_wgrad_gate_up_f32(const float* xs, const float* dgu, const int32_t* offsets,
+                                   int n_experts, int d_model, int d_ff, float* dw_gate,
+                                   float* dw_up, hmoe_stream_t stream);
+int hmoe_grouped_wgrad_down_f32(const float* h, const float* d_ys, const int32_t* offsets,
+                                int n_experts, int d_ff, int d_model, float* dw_down,
+                                hmoe_stream_t stream);
+
 /* ---- combine: moe.py:80-85 (replaces `ys[inv]` and the weighted einsum) - */
 
 /* out[t] = sum_k g'[t,k] * ys[slot_pos[t*K+k]] (+ residual[t]), g' the gates

@@ -437,6 +437,107 @@ def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype):
     assert float(m.expert_w_gate.value.grad.abs().max()) == 0.0
 
 
+def test_f32_expert_backward_kernels(gpu):
+    """The float32 backward GEMMs per expert segment against float64 numpy
+    products (a library routine): an empty segment (zero weight gradients),
+    segments that end inside a 64-row tile, rows past the last segment."""
+    rng = np.random.default_rng(31)
+    D, F = 128, 192
+    offs = np.array([0, 40, 40, 161, 230], np.int32)
+    N, R = len(offs) - 1, 256
+    xs = rng.standard_normal((R, D)).astype(np.float32)
+    wg, wu = (0.1 * rng.standard_normal((N, D, F))).astype(np.float32), \
+        (0.1 * rng.standard_normal((N, D, F))).astype(np.float32)
+    wd = (0.1 * rng.standard_normal((N, F, D))).astype(np.float32)
+    d_ys = rng.standard_normal((R, D)).astype(np.float32)
+    dh = rng.standard_normal((R, F)).astype(np.float32)
+    h = rng.standard_normal((R, F)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(gpu)
+    off = t(offs)
+    print("f32 backward kernels", flush=True)
+    g_dh = host(K.grouped_dgrad_down_f32(t(d_ys), off, t(wd)))
+    g_dgu = host(K.grouped_gate_up_swiglu_bwd_f32(t(xs), off, t(wg), t(wu), t(dh)))
+    dgu_in = rng.standard_normal((R, 2 * F)).astype(np.float32)
+    g_dxs = host(K.grouped_dgrad_gate_up_f32(t(dgu_in), off, t(wg), t(wu)))
+    g_dwg, g_dwu = (host(a) for a in K.grouped_wgrad_gate_up_f32(t(xs), t(dgu_in), off))
+    g_dwd = host(K.grouped_wgrad_down_f32(t(h), t(d_ys), off))
+    torch.cuda.synchronize()
+    f = lambda a: a.astype(np.float64)
+    for e in range(N):
+        lo, hi = offs[e], offs[e + 1]
+        x_e, g_e, u_e = f(xs[lo:hi]), f(wg[e]), f(wu[e])
+        rows = slice(lo, hi)
+        checks = [("dh", g_dh[rows], f(d_ys[rows]) @ f(wd[e]).T)]
+        gg, uu = x_e @ g_e, x_e @ u_e
+        s = 1.0 / (1.0 + np.exp(-gg))
+        d = f(dh[rows])
+        checks += [("dg", g_dgu[rows, :F], d * uu * s * (1 + gg * (1 - s))),
+                   ("du", g_dgu[rows, F:], d * gg * s),
+                   ("d_xs", g_dxs[rows], f(dgu_in[rows, :F]) @ g_e.T + f(dgu_in[rows, F:]) @ u_e.T),
+                   ("dWg", g_dwg[e], x_e.T @ f(dgu_in[rows, :F])),
+                   ("dWu", g_dwu[e], x_e.T @ f(dgu_in[rows, F:])),
+                   ("dWd", g_dwd[e], f(h[rows]).T @ f(d_ys[rows]))]
+        for name, got, want in checks:
+            if hi == lo and name.startswith("dW"):
+                assert np.all(got == 0.0), (name, e)
+                continue
+            if hi == lo:
+                continue
+            err = O.normwise_rel_err(got, want)
+            assert err < 1e-5, (name, e, err)
+
+
+@pytest.mark.parametrize("n_shared,cf", [(1, None), (2, 1.0)])
+def test_module_autograd_float32_matches_oracle(gpu, n_shared, cf):
+    """dtype float32: the module's backward on the float32 kernels, every
+    gradient against the oracle's float64 VJP on the forward's own routing
+    (no rounding points; the float32 GEMM sums are the only difference)."""
+    Bq, Sq, D, F, N, Kk = 2, 160, 256, 256, 8, 2
+    m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.float32, rngs=1, device=gpu,
+            capacity_factor=cf)
+    m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))
+    names = ("router", "expert_w_gate", "expert_w_up", "expert_w_down",
+             "shared_w_gate", "shared_w_up", "shared_w_down")
+    for n in names:
+        getattr(m, n).value.requires_grad_(True)
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(Bq, Sq, D, generator=gen, device=gpu).requires_grad_(True)
+    dy = torch.randn(Bq, Sq, D, generator=gen, device=gpu)
+    c_z, c_b = 0.37, 0.81
+    print(f"module autograd float32 n_shared={n_shared} cf={cf}", flush=True)
+    out, aux = m(x)
+    loss = (out * dy).sum() + c_z * aux["router_z_loss"] + c_b * aux["balance_loss"]
+    loss.backward()
+    torch.cuda.synchronize()
+    assert out.grad_fn is not None and x.grad is not None and x.grad.dtype == torch.float32
+    with torch.no_grad():
+        _, _, _, sv = m._forward(x.detach(), save=True)
+    T = Bq * Sq
+    idx = host(sv["top_idx"])
+    cap = O.capacity_of(T, Kk, N, cf)
+    ref_plan = O.dispatch_plan(idx, N, cap)
+    xn = host(x.detach()).reshape(T, D)
+    p = {n: getattr(m, n).value.detach().cpu().numpy() for n in names}
+    ref_fwd = {"logits": host(sv["logits"]), "top_idx": idx, "gates": host(sv["gates"]),
+               "plan": ref_plan, "xs": O.permute_rows(xn, ref_plan["perm_src"], Kk),
+               "ys": host(sv["ys"])}
+    ref = B.moe_backward(xn, p, host(dy).reshape(T, D), ref_fwd, routing="sigmoid", rsf=2.5,
+                         precision="fp64", n_shared=n_shared, batch_shape=(Bq, Sq),
+                         d_aux=(c_z, c_b, 0.0))
+    pairs = [("dx", x.grad, ref["dx"]), ("d_router", m.router.value.grad, ref["d_router"]),
+             ("dWg", m.expert_w_gate.value.grad, ref["dWg"]),
+             ("dWu", m.expert_w_up.value.grad, ref["dWu"]),
+             ("dWd", m.expert_w_down.value.grad, ref["dWd"]),
+             ("dWg_shared", m.shared_w_gate.value.grad, ref["dWg_shared"]),
+             ("dWu_shared", m.shared_w_up.value.grad, ref["dWu_shared"]),
+             ("dWd_shared", m.shared_w_down.value.grad, ref["dWd_shared"])]
+    for name, got, want in pairs:
+        got = host(got).reshape(np.shape(want))
+        err = O.normwise_rel_err(got, want)
+        print(f"  {name}: normwise {err:.2e}", flush=True)
+        assert err < 1e-4, (name, err)
+
+
 def test_module_trains(gpu):
     """End to end: the module as the reference's train step uses it
     (train.py:191-200: output loss plus weighted z and balance losses),
