@@ -298,7 +298,7 @@ def main():
         # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
         kname = ("grouped_gemm_dma<true, true>" if fp8
-                 else "grouped_gemm_f32_kernel<true>" if wl.expert_dtype == "f32"
+                 else "grouped_gemm_f32_kernel<1, false>" if wl.expert_dtype == "f32"
                  else f"grouped_gemm_regs<true, {'true' if odd else 'false'}, "
                       f"{'true' if fused else 'false'}, false>")
         flop, peak = work["gate_up"][1], work["gate_up"][2]
