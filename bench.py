@@ -501,18 +501,19 @@ def bench_train(args, name, wl):
     import torch
     from hanuman_amd.moe import MoE
 
-    if wl.router_from_logits or wl.expert != "swiglu" or wl.expert_dtype != "bf16":
-        raise SystemExit("--train needs a bf16 SwiGLU workload with a router weight")
+    if wl.router_from_logits or wl.expert != "swiglu" or wl.expert_dtype not in ("bf16", "f32"):
+        raise SystemExit("--train needs a bf16 or float32 SwiGLU workload with a router weight")
+    dt = torch.float32 if wl.expert_dtype == "f32" else torch.bfloat16
     dev = torch.device("cuda", 0)
     B = wl.batch if wl.tokens % wl.batch == 0 else 1
     S = wl.tokens // B
-    m = MoE(wl.d_model, wl.d_ff, wl.n_experts, wl.top_k, 1, 0.02, 1.0, torch.bfloat16,
+    m = MoE(wl.d_model, wl.d_ff, wl.n_experts, wl.top_k, 1, 0.02, 1.0, dt,
             rngs=args.seed, device=dev, routing=wl.routing, capacity_factor=wl.capacity_factor)
     params = [p.value for n, p in m.named_params().items() if n != "bias"]
     for p in params:
         p.requires_grad_(True)
     gen = torch.Generator(device=dev).manual_seed(args.seed)
-    x = torch.randn(B, S, wl.d_model, generator=gen, device=dev).to(torch.bfloat16)
+    x = torch.randn(B, S, wl.d_model, generator=gen, device=dev).to(dt)
     dy = torch.randn(B, S, wl.d_model, generator=gen, device=dev)
 
     def step():
@@ -545,7 +546,7 @@ def bench_train(args, name, wl):
         "value": round(wl.tokens / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "warmup_steps_run": warm_steps,
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
+        "vs_baseline": None, "dtype": "f32" if dt == torch.float32 else "bf16",
         "data": "synthetic (seeded normal inputs, weights and output cotangent)",
         "config": {"workload": name + " training step (module with one shared expert)",
                    "tokens": wl.tokens, "d_model": wl.d_model, "n_experts": wl.n_experts,
