@@ -229,14 +229,17 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
       dl = ds * a * (1.0f - a);
     }
   }
-  for (int n = lane; n < n_experts; n += 64) {
+  // The loop bound is the same for every lane, so every shuffle runs with the
+  // whole wave active (a shuffle that reads an inactive lane returns 0).
+  for (int n0 = 0; n0 < n_experts; n0 += 64) {
+    const int n = n0 + lane;
     float v = 0.0f;
     for (int j = 0; j < top_k; ++j) {
       const int ej = __shfl(my_e, j, 64);
       const float dj = __shfl(dl, j, 64);
       if (ej == n) v = dj;
     }
-    d_logits[t * n_experts + n] = v;
+    if (n < n_experts) d_logits[t * n_experts + n] = v;
   }
 }
 

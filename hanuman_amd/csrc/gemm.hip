@@ -23,7 +23,8 @@
 // wave owns a 128 x 128 quarter of the tile and runs 4 x 16 bf16 MFMAs
 // (v_mfma_f32_32x32x16_bf16) or 2 x 16 fp8 MFMAs per step from the current
 // LDS stage; two stages alternate.  An LDS row holds 128 bytes as eight
-// 16-byte chunks; chunk c of row r is stored at position c ^ (r & 7).
+// 16-byte chunks; chunk c of row r is stored at position c ^ lds_swz(r)
+// (lds_swz below: conflict-free fragment reads over the 64 LDS banks).
 //   * bf16 (grouped_gemm_regs): global loads run two K steps ahead into two
 //     register slots (2 x 64 KB per workgroup in flight) and each slot is
 //     written into the other stage during the step before it is used; the
@@ -71,15 +72,17 @@ __device__ __forceinline__ float silu_f32(float g) {
 }
 
 // Exclusive scan of per-expert m-tile counts into tstart[0..n_experts];
-// returns the total.  Every thread takes four experts.
+// returns the total.  NT threads, each taking kMaxExperts / NT experts.
+template <int NT = kThreads>
 __device__ __forceinline__ int scan_tiles(const int32_t* __restrict__ offsets, int n_experts,
                                           int32_t* tstart, int32_t* scan_tmp) {
+  constexpr int kPer = kMaxExperts / NT;
   const int tid = threadIdx.x;
-  int local[4];
+  int local[kPer];
   int sum = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = tid * 4 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid * kPer + j;
     int tiles = 0;
     if (e < n_experts) tiles = (offsets[e + 1] - offsets[e] + kBM - 1) / kBM;
     local[j] = tiles;
@@ -87,7 +90,7 @@ __device__ __forceinline__ int scan_tiles(const int32_t* __restrict__ offsets, i
   }
   scan_tmp[tid] = sum;
   __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {
+  for (int off = 1; off < NT; off <<= 1) {
     const int v = tid >= off ? scan_tmp[tid - off] : 0;
     __syncthreads();
     scan_tmp[tid] += v;
@@ -95,12 +98,12 @@ __device__ __forceinline__ int scan_tiles(const int32_t* __restrict__ offsets, i
   }
   int run = scan_tmp[tid] - sum;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = tid * 4 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid * kPer + j;
     if (e < n_experts) tstart[e] = run;
     run += local[j];
   }
-  if (tid == kThreads - 1) tstart[n_experts] = scan_tmp[kThreads - 1];
+  if (tid == NT - 1) tstart[n_experts] = scan_tmp[NT - 1];
   __syncthreads();
   return tstart[n_experts];
 }
@@ -122,6 +125,17 @@ __device__ __forceinline__ void decode_tile(int t, int n_tiles_n, const int32_t*
   n0 = n_tile * kBN;
 }
 
+// Position of the 16-byte chunks of LDS row r: chunk c sits at c ^ lds_swz(r).
+// A fragment read has lanes 0..31 on 32 consecutive rows (128 bytes apart)
+// at the same chunk; the LDS serves 16 lanes of a 16-byte read per pass from
+// 64 four-byte banks, i.e. one 256-byte span, which rows r and r + 1 already
+// fill.  So the eight rows of one parity among 16 consecutive rows must take
+// eight different positions: r & 7 alone repeats every 8 rows (rows r and
+// r + 8 would collide); flipping the low bit with bit 3 separates them.
+// Rows of one 8-row group still take eight different positions, so reads in
+// passes of 8 lanes over 32 banks stay conflict-free as well.
+__device__ __forceinline__ int lds_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // Element-type traits: bf16 (32x32x16 MFMA, 64 elements = 128 bytes per LDS
@@ -137,7 +151,7 @@ struct GemmElem<false> {
   typedef bf16x8 frag_t;
   // Lane L, sub-step s: row L&31, 16-byte chunk 2s + L/32.
   __device__ static frag_t read(const uint8_t* base, int row_byte, int row, int s, int half) {
-    return *reinterpret_cast<const bf16x8*>(base + row_byte + (((2 * s + half) ^ (row & 7)) * 16));
+    return *reinterpret_cast<const bf16x8*>(base + row_byte + (((2 * s + half) ^ lds_swz(row)) * 16));
   }
   __device__ static f32x16 mfma(const frag_t& b, const frag_t& a, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
@@ -151,8 +165,8 @@ struct GemmElem<true> {
   // Lane L, sub-step s: row L&31, 32 bytes = chunks 4s + 2(L/32) and the next.
   __device__ static frag_t read(const uint8_t* base, int row_byte, int row, int s, int half) {
     const int c0 = 4 * s + 2 * half;
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(base + row_byte + ((c0 ^ (row & 7)) * 16));
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(base + row_byte + (((c0 + 1) ^ (row & 7)) * 16));
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(base + row_byte + ((c0 ^ lds_swz(row)) * 16));
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(base + row_byte + (((c0 + 1) ^ lds_swz(row)) * 16));
     frag_t f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -502,7 +516,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
   // (tid&7) ^ (row&7) = (tid&7) ^ ((tid>>3)&7).  One wave instruction writes
   // 1 KB of contiguous LDS.
   const int ld_r = tid >> 3;
-  const int ld_c = (tid & 7) ^ (ld_r & 7);
+  const int ld_c = (tid & 7) ^ lds_swz(ld_r);
   const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
   uint32_t a_off[8];
   const uint8_t* a_tile = A;
@@ -698,13 +712,13 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   // ---- global -> registers -> LDS --------------------------------------------
   // Round i (0..7) of a K step: this thread loads 16-byte chunk ld_c of A row
   // and B row i*32 + ld_r (eight threads cover a row's 128 bytes) and stores it
-  // at position ld_c ^ (row & 7) of the LDS row.  Loads run two K steps ahead
+  // at position ld_c ^ lds_swz(row) of the LDS row.  Loads run two K steps ahead
   // of the MFMAs in two register slots; a slot is written to the idle LDS
   // stage one step ahead, so the barrier at the end of a step never waits for
   // global memory.
   const int ld_r = tid >> 3;
   const int ld_c = tid & 7;
-  const int st_pos = (ld_c ^ (ld_r & 7)) * 16;
+  const int st_pos = (ld_c ^ lds_swz(ld_r)) * 16;
   const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
   uint32_t a_off[8];
   const uint8_t* a_tile = A;

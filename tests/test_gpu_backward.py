@@ -183,7 +183,9 @@ def test_gather_bwd_bit_exact(gpu, T, D, N, Kk, cf):
 
 
 @pytest.mark.parametrize("mode", ["softmax", "sigmoid"])
-@pytest.mark.parametrize("T,N,Kk", [(1000, 64, 8), (257, 200, 6), (64, 8, 2)])
+# N % 64 < K puts selected experts in a partial last 64-expert chunk
+@pytest.mark.parametrize("T,N,Kk", [(1000, 64, 8), (257, 200, 6), (64, 8, 2), (300, 66, 8),
+                                    (300, 130, 4)])
 def test_router_bwd(gpu, mode, T, N, Kk):
     rng = np.random.default_rng(T + N)
     logits = rng.standard_normal((T, N)).astype(np.float32)
@@ -317,7 +319,8 @@ def test_router_dw(gpu, x_dtype):
     assert O.normwise_rel_err(got, ref) < 1e-5
 
 
-@pytest.mark.parametrize("Bq,Sq,N,Kk", [(2, 300, 64, 8), (3, 70, 200, 6), (1, 64, 8, 2)])
+@pytest.mark.parametrize("Bq,Sq,N,Kk", [(2, 300, 64, 8), (3, 70, 200, 6), (1, 64, 8, 2),
+                                        (2, 150, 66, 8)])
 def test_router_aux_bwd(gpu, Bq, Sq, N, Kk):
     rng = np.random.default_rng(Bq * Sq + N)
     T = Bq * Sq
@@ -369,14 +372,15 @@ def test_gate_up_raw_matches_gather(gpu):
     assert torch.equal(a[:kept], b[:kept])
 
 
-@pytest.mark.parametrize("n_shared,cf,x_dtype", [(1, None, "bf16"), (2, 1.0, "bf16"),
-                                                 (1, 1.0, "f32")])
-def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype):
+@pytest.mark.parametrize("n_shared,cf,x_dtype,N,Kk", [(1, None, "bf16", 8, 2), (2, 1.0, "bf16", 8, 2),
+                                                      (1, 1.0, "f32", 8, 2),
+                                                      (1, None, "bf16", 66, 8)])
+def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype, N, Kk):
     """MoE.__call__ under torch autograd: loss = <dy, out> + c_z z_loss +
     c_b balance_loss (train.py:191-200), backward through the library's VJP
     of the whole module, every gradient against the bf16-mode oracle fed
     with the forward's own routing."""
-    Bq, Sq, D, F, N, Kk = 2, 160, 256, 256, 8, 2
+    Bq, Sq, D, F = 2, 160, 256, 256
     m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.bfloat16, rngs=1, device=gpu,
             capacity_factor=cf)
     m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))
@@ -391,7 +395,7 @@ def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype):
     x.requires_grad_(True)
     dy = torch.randn(Bq, Sq, D, generator=gen, device=gpu)
     c_z, c_b = 0.37, 0.81
-    print(f"module autograd n_shared={n_shared} cf={cf} x {x_dtype}", flush=True)
+    print(f"module autograd n_shared={n_shared} cf={cf} x {x_dtype} N={N} K={Kk}", flush=True)
     out, aux = m(x)
     loss = (out * dy).sum() + c_z * aux["router_z_loss"] + c_b * aux["balance_loss"]
     loss.backward()
@@ -492,7 +496,7 @@ def test_module_autograd_float32_matches_oracle(gpu, n_shared, cf):
     """dtype float32: the module's backward on the float32 kernels, every
     gradient against the oracle's float64 VJP on the forward's own routing
     (no rounding points; the float32 GEMM sums are the only difference)."""
-    Bq, Sq, D, F, N, Kk = 2, 160, 256, 256, 8, 2
+    Bq, Sq, D, F = 2, 160, 256, 256
     m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.float32, rngs=1, device=gpu,
             capacity_factor=cf)
     m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))
