@@ -71,6 +71,16 @@ __device__ __forceinline__ float silu_f32(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
+// h = bf16(silu(g) * u) at moe.py:70-72's rounding points: g and u are the
+// bf16 outputs of the two ragged_dot calls (their dtype is the input dtype),
+// so both are rounded to bf16 first; silu and the product run in float32
+// and h is rounded once more by the caller.  The backward's recompute rounds
+// at the same points, so its VJP is the VJP of this forward.
+__device__ __forceinline__ float swiglu_bf16_points(float g, float u) {
+  const uint32_t gu = pack_bf16x2_rne(g, u);
+  return silu_f32(__uint_as_float(gu << 16)) * __uint_as_float(gu & 0xffff0000u);
+}
+
 // Exclusive scan of per-expert m-tile counts into tstart[0..n_experts];
 // returns the total.  NT threads, each taking kMaxExperts / NT experts.
 template <int NT = kThreads>
@@ -215,7 +225,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], uint16_t* 
                 gv = gv * sa * sb[(2 * p) * 32 + g * 8 + q];
                 uv = uv * sa * sb[(2 * p + 1) * 32 + g * 8 + q];
               }
-              h[q] = silu_f32(gv) * uv;
+              h[q] = swiglu_bf16_points(gv, uv);
             }
             uint2 pk;
             pk.x = pack_bf16x2_rne(h[0], h[1]);
@@ -362,7 +372,7 @@ __device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4],
             gv = gv * sa * sg[q];
             uv = uv * sa * su[q];
           }
-          h[q] = silu_f32(gv) * uv;
+          h[q] = swiglu_bf16_points(gv, uv);
         }
         uint2 pk;
         pk.x = pack_bf16x2_rne(h[0], h[1]);

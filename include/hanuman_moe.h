@@ -161,10 +161,12 @@ int hmoe_pack_fp8_down(const void* w_down, int w_dtype, int n_experts, int d_ff,
 /* ---- grouped expert GEMMs: moe.py:67-74 (replaces the three
  *      `jax.lax.ragged_dot` calls and the SwiGLU between them) ------------- */
 
-/* h[r, :] = bf16( silu(xs[r]·Wg[e]) * (xs[r]·Wu[e]) ) for rows r of expert e's
- * segment [offsets[e], offsets[e+1]).  xs [rows_cap, D] bf16, packed gate/up
- * from hmoe_pack_gate_up, h [rows_cap, F] bf16.  fp32 accumulation.
- * D % 64 == 0, F % 128 == 0, N <= 1024. */
+/* h[r, :] = bf16( silu(g) * u ) for rows r of expert e's segment
+ * [offsets[e], offsets[e+1]), with g = bf16(xs[r]·Wg[e]) and
+ * u = bf16(xs[r]·Wu[e]) (fp32 accumulation, rounded to bf16 as the
+ * `ragged_dot` outputs of moe.py:70-71 are; silu and the product in fp32,
+ * moe.py:72).  xs [rows_cap, D] bf16, packed gate/up from hmoe_pack_gate_up,
+ * h [rows_cap, F] bf16.  D % 64 == 0, F % 128 == 0, N <= 1024. */
 int hmoe_grouped_gate_up(const void* xs, const int32_t* offsets, int n_experts,
                          int64_t rows_cap, int d_model, int d_ff,
                          const void* w_gate_up_packed, void* h, hmoe_stream_t stream);
@@ -191,7 +193,8 @@ int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
 
 /* fp8 expert GEMMs (workload rule): e4m3 operands on the CDNA4 32x32x64
  * fp8 MFMA with float32 accumulation; the accumulators are dequantised with
- * the row scale times the column scale, then (gate/up) the SwiGLU is applied.
+ * the row scale times the column scale, then (gate/up) g and u are rounded to
+ * bf16 and the SwiGLU is applied as in hmoe_grouped_gate_up.
  * h and ys are bf16.  gate/up: D % 128 == 0, F % 128 == 0; down: F % 128 == 0,
  * D % 256 == 0. */
 int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_scale, const int32_t* offsets,

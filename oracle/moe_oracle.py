@@ -451,7 +451,9 @@ def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s):
 
     ``xs_q [R, D]`` codes with per-row scales ``xs_s``; ``wg_q/wu_q [N, D, F]``
     codes with per-column scales ``[N, F]``; ``wd_q [N, F, D]`` with ``[N, D]``.
-    ``g = (x.wg) * sx * sg``, ``u`` likewise, ``h = bf16(silu(g) * u)``; h is
+    ``g = bf16((x.wg) * sx * sg)``, ``u`` likewise (rounded to bf16 as the
+    bf16 path's ``ragged_dot`` outputs are, ``moe.py:70-71``),
+    ``h = bf16(silu(g) * u)``; h is
     re-quantised per row (:func:`quantize_rows_e4m3`) and
     ``ys = bf16((hq.wd) * sh * sd)``.  Dot products of decoded codes in
     float64.  Returns (ys float32 of bf16 values, h, hq, hs)."""
@@ -468,6 +470,8 @@ def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s):
         x = e4m3_decode(xs_q[a:b]).astype(F64) * np.asarray(xs_s[a:b], F64)[:, None]
         g = (x @ e4m3_decode(wg_q[e]).astype(F64)) * np.asarray(wg_s[e], F64)[None, :]
         u = (x @ e4m3_decode(wu_q[e]).astype(F64)) * np.asarray(wu_s[e], F64)[None, :]
+        g = bf16_round(g.astype(F32)).astype(F64)
+        u = bf16_round(u.astype(F32)).astype(F64)
         h[a:b] = bf16_round((silu(g) * u).astype(F32))
     total = int(offsets[-1])
     hq = np.zeros((R, F), np.uint8)

@@ -496,7 +496,7 @@ def test_module_autograd_float32_matches_oracle(gpu, n_shared, cf):
     """dtype float32: the module's backward on the float32 kernels, every
     gradient against the oracle's float64 VJP on the forward's own routing
     (no rounding points; the float32 GEMM sums are the only difference)."""
-    Bq, Sq, D, F = 2, 160, 256, 256
+    Bq, Sq, D, F, N, Kk = 2, 160, 256, 256, 8, 2
     m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.float32, rngs=1, device=gpu,
             capacity_factor=cf)
     m.bias.value.copy_(torch.linspace(-0.02, 0.02, N, device=gpu))

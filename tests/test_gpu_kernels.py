@@ -16,6 +16,15 @@ from hanuman_amd import kernels as K
 pytestmark = pytest.mark.gpu
 
 
+
+def swiglu_ref(g, u):
+    """h from float64 products at the kernels' rounding points: g and u
+    rounded to bf16 first (the ragged_dot outputs, moe.py:70-71), then
+    silu(g) * u (moe.py:72)."""
+    g = O.bf16_round(np.asarray(g, np.float32)).astype(np.float64)
+    u = O.bf16_round(np.asarray(u, np.float32)).astype(np.float64)
+    return g / (1 + np.exp(-g)) * u
+
 def dev_f32(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
 
@@ -273,7 +282,7 @@ def test_grouped_gemm(gpu, case):
         x64 = xs[a:b].astype(np.float64)
         g = x64 @ wgb[e]
         u = x64 @ wub[e]
-        h_ref = g / (1 + np.exp(-g)) * u
+        h_ref = swiglu_ref(g, u)
         err_h = np.abs(h_host[a:b] - h_ref)
         assert np.all(err_h <= 8e-3 * np.abs(h_ref) + 1e-3 * np.abs(h_ref).max()), \
             f"h expert {e}: max err {err_h.max()}"
@@ -312,7 +321,7 @@ def test_grouped_gemm_odd_k_steps(gpu, case):
                 continue
             x64 = xs[a:b].astype(np.float64)
             g, u = x64 @ wgb[e], x64 @ wub[e]
-            ref = g / (1 + np.exp(-g)) * u
+            ref = swiglu_ref(g, u)
             err = np.abs(out[a:b] - ref)
             assert np.all(err <= 8e-3 * np.abs(ref) + 1e-3 * np.abs(ref).max()), f"h expert {e}: {err.max()}"
     else:
@@ -475,7 +484,7 @@ def test_grouped_gemm_fp8(gpu, case):
             continue
         g = (x64[a:b] @ O.e4m3_decode(wq["wg_q"][e]).astype(np.float64)) * wq["wg_s"][e]
         u = (x64[a:b] @ O.e4m3_decode(wq["wu_q"][e]).astype(np.float64)) * wq["wu_s"][e]
-        h_ref = g / (1 + np.exp(-g)) * u
+        h_ref = swiglu_ref(g, u)
         err_h = np.abs(h_host[a:b] - h_ref)
         assert np.all(err_h <= 8e-3 * np.abs(h_ref) + 1e-3 * np.abs(h_ref).max()), \
             f"h expert {e}: max err {err_h.max()}"

@@ -65,25 +65,61 @@ def test_workload_reduced_tokens(gpu, name, tokens):
         assert err < (1e-5 if wl.expert_dtype == "f32" else BF16_TOL)
 
 
-def sampled_token_ref(inp, idx, gates, plan, tokens):
-    """fp32 (float64 arithmetic) output of selected tokens from the oracle's
-    routing and plan: y[t] = sum_k keep * bf16(g) * expert_e(x[t])."""
-    K = inp.wl.top_k
-    keep = plan["keep"].reshape(-1, K)[tokens]
-    sel = idx[tokens]
-    g16 = O.bf16_round(gates[tokens]).astype(np.float64)
-    x = O.bf16_round(inp.x[tokens]).astype(np.float64)
-    out = np.zeros((len(tokens), inp.x.shape[1]))
-    for e in np.unique(sel):
-        for k in range(K):
-            rows = np.nonzero((sel[:, k] == e) & (keep[:, k] > 0))[0]
-            if rows.size == 0:
+def full_output_ref(x, w_gate, w_up, w_down, gates, plan, K):
+    """The whole [T, D] layer output in float32 arithmetic on the fp32
+    weights given, on the plan given (the GPU's own routing, which the tests
+    check bit-exact first): per expert, the kept rows' tokens go through the
+    SwiGLU as float32 BLAS products, and each token gets bf16(gate) times its
+    row (moe.py:80-85).  A token meets an expert at most once, so the
+    scatter per expert has no repeated index."""
+    from threadpoolctl import threadpool_limits
+    import os
+    T, D = x.shape
+    out = np.zeros((T, D), np.float32)
+    off = np.asarray(plan["offsets"])
+    perm = np.asarray(plan["perm_src"])
+    g16 = O.bf16_round(np.asarray(gates, np.float32)).reshape(-1)
+    with threadpool_limits(min(16, len(os.sched_getaffinity(0)))):
+        for e in range(len(off) - 1):
+            a, b = int(off[e]), int(off[e + 1])
+            if b <= a:
                 continue
-            g = x[rows] @ inp.w_gate[e].astype(np.float64)
-            u = x[rows] @ inp.w_up[e].astype(np.float64)
-            y = (g / (1 + np.exp(-g)) * u) @ inp.w_down[e].astype(np.float64)
-            out[rows] += g16[rows, k:k + 1] * y
+            slots = perm[a:b]
+            toks = slots // K
+            xe = x[toks]
+            g = xe @ w_gate[e]
+            u = xe @ w_up[e]
+            ys = ((g / (1.0 + np.exp(-g))) * u).astype(np.float32) @ w_down[e]
+            out[toks] += g16[slots][:, None] * ys
     return out
+
+
+@pytest.mark.parametrize("name", ["full_bf16", "skewed_bf16"])
+def test_rounding_points_match_reference_bf16_mode(gpu, name):
+    """The bf16 layer rounds where moe.py:70-85 rounds: g and u to bf16 (the
+    ragged_dot outputs), h = bf16(silu(g) u), ys bf16, gates to bf16 in the
+    combine.  Against the oracle's bf16 mode (the same rounding points,
+    float32 dot products) the output agrees to 5e-3 normwise; a forward
+    that skipped any of these roundings would sit near the 2e-2 distance
+    to the float64 result instead."""
+    wl = W.WORKLOADS[name].scaled(2048)
+    inp = W.make_inputs(wl, seed=3)
+    params = {"router": inp.router, "expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
+              "expert_w_down": inp.w_down}
+    kw = dict(top_k=wl.top_k, routing="softmax", capacity_factor=wl.capacity_factor,
+              logits=inp.logits if wl.router_from_logits else None)
+    ref16 = O.moe_forward(inp.x, params, precision="bf16", **kw)
+    ref64 = O.moe_forward(inp.x, params, precision="fp32", **kw)
+    res = DeviceLayer(inp, gpu).forward()
+    torch.cuda.synchronize()
+    check_routing_and_plan(res, ref16["top_idx"], ref16["gates"], ref16["plan"])
+    out = host(res["out"])
+    e16 = O.normwise_rel_err(out, ref16["out"])
+    e64 = O.normwise_rel_err(out, ref64["out"])
+    print(f"{name} T={wl.tokens}: normwise err {e16:.3e} against the bf16-mode oracle, "
+          f"{e64:.3e} against the float64 result", flush=True)
+    assert e16 < 5e-3
+    assert e64 < BF16_TOL
 
 
 @pytest.mark.parametrize("name", ["full_bf16", "skewed_bf16"])
@@ -99,12 +135,13 @@ def test_workload_full_size(gpu, name):
     dropped = 1.0 - plan["keep"].mean()
     print(f"{name}: dropped fraction {dropped:.4f}, counts min/max "
           f"{plan['counts'].min()}/{plan['counts'].max()}", flush=True)
-    rng = np.random.default_rng(1)
-    tokens = np.sort(rng.choice(wl.tokens, 128, replace=False))
-    ref = sampled_token_ref(inp, idx, gates, plan, tokens)
-    got = host(res["out"])[tokens]
-    err = O.normwise_rel_err(got, ref)
-    print(f"{name}: sampled-token normwise rel err {err:.3e}", flush=True)
+    out = host(res["out"])
+    ref = full_output_ref(inp.x, inp.w_gate, inp.w_up, inp.w_down, gates, plan, wl.top_k)
+    err = O.normwise_rel_err(out, ref)
+    tok = np.linalg.norm(out - ref, axis=1) / np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+    print(f"{name}: whole output [{wl.tokens}, {wl.d_model}] normwise rel err {err:.3e}, "
+          f"worst token {tok.max():.3e}, max abs / max |ref| "
+          f"{np.abs(out - ref).max() / np.abs(ref).max():.3e}", flush=True)
     assert err < BF16_TOL
     # size-independent property: the fused gate/up (rows gathered from x by
     # the GEMM) equals the unfused permute + gate/up on the kept rows, bit for bit
@@ -228,13 +265,18 @@ def test_fp8_workload_full_size(gpu):
     wq = O.quantize_expert_weights({"expert_w_gate": inp.w_gate, "expert_w_up": inp.w_up,
                                     "expert_w_down": inp.w_down})
     deq = O.dequantized_weights(wq)
-    sub = W.Inputs(wl, inp.x, router=inp.router, w_gate=deq["expert_w_gate"],
-                   w_up=deq["expert_w_up"], w_down=deq["expert_w_down"])
-    rng = np.random.default_rng(1)
-    tokens = np.sort(rng.choice(wl.tokens, 128, replace=False))
-    ref = sampled_token_ref(sub, idx, gates, plan, tokens)
-    err = O.normwise_rel_err(host(res["out"])[tokens], ref)
-    print(f"fp8 full size: sampled-token normwise err {err:.3e}", flush=True)
+    out = host(res["out"])
+    ref = full_output_ref(inp.x, deq["expert_w_gate"], deq["expert_w_up"], deq["expert_w_down"],
+                          gates, plan, wl.top_k)
+    err = O.normwise_rel_err(out, ref)
+    tok = np.linalg.norm(out - ref, axis=1) / np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+    # the same layer on the unquantised float32 weights: reported, not bounded
+    # (the e4m3 rule's own error there is ~6.5 %)
+    ref32 = full_output_ref(inp.x, inp.w_gate, inp.w_up, inp.w_down, gates, plan, wl.top_k)
+    err32 = O.normwise_rel_err(out, ref32)
+    print(f"fp8 full size: whole output normwise err {err:.3e} (worst token {tok.max():.3e}) "
+          f"against the float32 layer on the dequantised weights; {err32:.3e} against the "
+          f"unquantised float32 weights", flush=True)
     assert err < FP8_TOL
 
 

@@ -299,6 +299,100 @@ def test_aux_closed_forms():
     assert aux["expert_counts"].tolist() == [B * S // 2] * N
 
 
+def test_aux_hand_computed_non_uniform():
+    """N = 2, logits [0, ln 3]: sigmoid scores [1/2, 3/4] normalise to
+    p = [0.4, 0.6] (a softmax would give [0.25, 0.75]); logsumexp = ln 4.
+    Worked by hand from moe.py:255-283, not from the oracle's formula."""
+    logits = np.array([[0.0, math.log(3.0)]], np.float32)
+    scores = np.array([[0.5, 0.75]], np.float32)
+    aux = O.aux_losses(logits, scores, np.array([[1]], np.int32), 1, 1, 2)
+    p0 = 0.5 / (1.25 + 1e-9)
+    p1 = 0.75 / (1.25 + 1e-9)
+    assert math.isclose(aux["router_z_loss"], math.log(4.0) ** 2, rel_tol=1e-6)
+    ent = -(p0 * math.log(p0 + 1e-9) + p1 * math.log(p1 + 1e-9))
+    assert math.isclose(aux["mean_entropy"], ent, rel_tol=1e-9)
+    assert abs(aux["mean_entropy"] - 0.6730116670092565) < 1e-8    # -(0.4 ln 0.4 + 0.6 ln 0.6)
+    # one token, top-1 on expert 1: fractions [0, 1], mean probs [0.4, 0.6]
+    assert math.isclose(aux["balance_loss"], 2 * p1, rel_tol=1e-9)
+    assert aux["expert_counts"].tolist() == [0.0, 1.0]
+
+
+def test_aux_balance_is_per_sequence():
+    """Two sequences that route to different experts: per sequence b,
+    N * sum_n f[b,n] * mean_s p[b,s,n] (moe.py:268-277).  Sequence 0 sends
+    both tokens to expert 0 with p = [0.6, 0.4]; sequence 1 sends them to
+    expert 1 with p = [0.4, 0.6] and [0.2, 0.8]: 2 * 0.6 = 1.2 and
+    2 * 0.7 = 1.4, mean 1.3.  Fractions or mean probabilities taken over the
+    whole batch would give 2 * (0.5 * 0.4 + 0.5 * 0.6) = 1.0."""
+    B, S, N = 2, 2, 2
+    probs = np.array([[0.6, 0.4], [0.6, 0.4], [0.4, 0.6], [0.2, 0.8]])
+    scores = probs.astype(np.float32)           # already normalised: sum 1
+    logits = np.zeros((B * S, N), np.float32)
+    top = np.array([[0], [0], [1], [1]], np.int32)
+    aux = O.aux_losses(logits, scores, top, B, S, N)
+    assert math.isclose(aux["balance_loss"], 1.3, rel_tol=1e-7)
+    assert aux["expert_counts"].tolist() == [2.0, 2.0]
+
+
+def test_aux_matches_python_loops():
+    """Plain nested loops over (b, s, n) on a tiny random case, written from
+    the text of moe.py:253-283 (logsumexp via max-shift, bincount by counting)."""
+    rng = np.random.default_rng(17)
+    B, S, N, K = 3, 5, 6, 2
+    logits = (1.7 * rng.standard_normal((B * S, N))).astype(np.float32)
+    scores = O.sigmoid_det(logits)
+    top = np.stack([rng.choice(N, K, replace=False) for _ in range(B * S)]).astype(np.int32)
+    aux = O.aux_losses(logits, scores, top, B, S, N)
+    z = ent = bal = 0.0
+    total = [0] * N
+    for b in range(B):
+        cnt = [0] * N
+        mp = [0.0] * N
+        for s_ in range(S):
+            t = b * S + s_
+            row = [float(v) for v in logits[t]]
+            m = max(row)
+            lse = m + math.log(sum(math.exp(v - m) for v in row))
+            z += lse * lse
+            sc = [float(v) for v in scores[t]]
+            den = sum(sc) + 1e-9
+            for n in range(N):
+                p = sc[n] / den
+                mp[n] += p / S
+                ent -= p * math.log(p + 1e-9)
+            for k in range(K):
+                cnt[int(top[t, k])] += 1
+        bal += N * sum(cnt[n] / (S * K) * mp[n] for n in range(N))
+        total = [a + c for a, c in zip(total, cnt)]
+    assert math.isclose(aux["router_z_loss"], z / (B * S), rel_tol=1e-12)
+    assert math.isclose(aux["mean_entropy"], ent / (B * S), rel_tol=1e-12)
+    assert math.isclose(aux["balance_loss"], bal / B, rel_tol=1e-12)
+    assert aux["expert_counts"].tolist() == [float(c) for c in total]
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_shared_expert_is_one_segment_expert_ffn(precision):
+    """One shared expert (moe.py:161-163) is the routed SwiGLU on a single
+    segment holding every token (expert_ffn, pinned by numpy.matmul above);
+    three shared experts (moe.py:164-168) are the mean of three such calls,
+    and three identical experts equal one."""
+    rng = np.random.default_rng(23)
+    T, D, F = 40, 32, 24
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    wg, wu = (0.2 * rng.standard_normal((2, 3, D, F))).astype(np.float32)
+    wd = (0.2 * rng.standard_normal((3, F, D))).astype(np.float32)
+    seg = np.array([0, T])
+    ones = [O.expert_ffn(x, seg, wg[i][None], wu[i][None], wd[i][None], precision) for i in range(3)]
+    one = O.shared_expert(x, wg[0], wu[0], wd[0], 1, precision)
+    np.testing.assert_array_equal(one, ones[0])
+    three = O.shared_expert(x, wg, wu, wd, 3, precision)
+    mean = (ones[0].astype(np.float64) + ones[1] + ones[2]) / 3
+    np.testing.assert_allclose(three, mean, rtol=1e-6, atol=1e-7)
+    same = O.shared_expert(x, np.stack([wg[0]] * 3), np.stack([wu[0]] * 3), np.stack([wd[0]] * 3),
+                           3, precision)
+    np.testing.assert_allclose(same, ones[0], rtol=1e-6, atol=1e-7)
+
+
 # ------------------------------------------------------------------- fp8 --
 
 def test_quantize_rows_e4m3_rule_matches_torch_conversion():
@@ -370,8 +464,11 @@ def test_expert_ffn_fp8_reduces_to_library_matmul_on_exact_operands():
         a, b = offsets[e], offsets[e + 1]
         if b == a:
             continue
+        # g and u are rounded to bf16 before the SwiGLU (moe.py:70-72's points)
         g = np.matmul(x[a:b].astype(np.float64), wg[e].astype(np.float64))
         u = np.matmul(x[a:b].astype(np.float64), wu[e].astype(np.float64))
+        g = O.bf16_round(g.astype(np.float32)).astype(np.float64)
+        u = O.bf16_round(u.astype(np.float32)).astype(np.float64)
         assert np.array_equal(h[a:b], O.bf16_round((g / (1 + np.exp(-g)) * u).astype(np.float32)))
         hh = O.e4m3_decode(hq[a:b]).astype(np.float64) * hs[a:b, None]
         y = np.matmul(hh, wd[e].astype(np.float64))
