@@ -205,11 +205,14 @@ struct Chunk8<float> {
   __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
 };
 
+// The dispatched rows are written once and read later by another kernel, so
+// the stores are non-temporal (the full bf16 workload's permutation: 117.5 ->
+// 105.4 us measured; non-temporal loads of x on top of that were slower).
 template <typename TI, typename TO>
 __device__ __forceinline__ void store8(TO* dst, const Chunk8<TI>& c);
 template <>
 __device__ __forceinline__ void store8<uint16_t, uint16_t>(uint16_t* dst, const Chunk8<uint16_t>& c) {
-  *reinterpret_cast<u32x4*>(dst) = c.v;
+  __builtin_nontemporal_store(c.v, reinterpret_cast<u32x4*>(dst));
 }
 template <>
 __device__ __forceinline__ void store8<float, uint16_t>(uint16_t* dst, const Chunk8<float>& c) {
@@ -218,12 +221,12 @@ __device__ __forceinline__ void store8<float, uint16_t>(uint16_t* dst, const Chu
   o[1] = pack_bf16x2(c.a[2], c.a[3]);
   o[2] = pack_bf16x2(c.b[0], c.b[1]);
   o[3] = pack_bf16x2(c.b[2], c.b[3]);
-  *reinterpret_cast<u32x4*>(dst) = o;
+  __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst));
 }
 template <>
 __device__ __forceinline__ void store8<float, float>(float* dst, const Chunk8<float>& c) {
-  *reinterpret_cast<f32x4*>(dst) = c.a;
-  *reinterpret_cast<f32x4*>(dst + 4) = c.b;
+  __builtin_nontemporal_store(c.a, reinterpret_cast<f32x4*>(dst));
+  __builtin_nontemporal_store(c.b, reinterpret_cast<f32x4*>(dst + 4));
 }
 template <>
 __device__ __forceinline__ void store8<uint16_t, float>(float* dst, const Chunk8<uint16_t>& c) {
@@ -232,8 +235,8 @@ __device__ __forceinline__ void store8<uint16_t, float>(float* dst, const Chunk8
     a[i] = c.get(i);
     b[i] = c.get(4 + i);
   }
-  *reinterpret_cast<f32x4*>(dst) = a;
-  *reinterpret_cast<f32x4*>(dst + 4) = b;
+  __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(dst));
+  __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(dst + 4));
 }
 
 constexpr int kPermUnroll = 4;
