@@ -40,6 +40,8 @@ SIGNATURES = {
     "hmoe_router_from_logits": (_i32, [_vp, _vp, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
     "hmoe_dispatch_plan": (_i32, [_vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _sz, _vp]),
+    "hmoe_dispatch_plan_noalloc": (_i32, [_vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp,
+                                          _vp]),
     "hmoe_permute_rows": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp]),
     "hmoe_packed_gate_up_bytes": (_sz, [_i32, _i32, _i32]),
     "hmoe_pack_gate_up": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),

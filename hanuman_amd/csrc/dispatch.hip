@@ -11,6 +11,8 @@
 //      fixes keep (rank < C), slot_pos and perm_src; no atomic decides a value.
 // Permutation: one wave per token reads the row once and writes its kept
 // slots' rows (token-centric, so x is read exactly once).
+#include <mutex>
+
 #include "hmoe_common.h"
 
 namespace hmoe {
@@ -473,34 +475,36 @@ extern "C" size_t hmoe_plan_workspace_bytes(int64_t tokens, int top_k, int n_exp
   return static_cast<size_t>(hmoe::plan_blocks(tokens * top_k)) * n_experts * sizeof(int32_t);
 }
 
-extern "C" int hmoe_dispatch_plan(const int32_t* top_idx, int64_t tokens, int top_k,
-                                  int n_experts, int64_t capacity, int32_t* counts,
-                                  int32_t* offsets, int32_t* slot_pos, int32_t* perm_src,
-                                  uint8_t* keep, void* workspace, size_t workspace_bytes,
-                                  hmoe_stream_t stream) {
-  using namespace hmoe;
-  HMOE_REQUIRE(tokens >= 0 && top_k >= 1, "dispatch_plan: need tokens >= 0 and top_k >= 1");
+namespace hmoe {
+namespace {
+
+// Argument checks shared by the two plan entry points.
+int check_plan_args(const int32_t* top_idx, int64_t tokens, int top_k, int n_experts,
+                    int64_t capacity, int32_t* counts, int32_t* offsets, int32_t* slot_pos,
+                    int32_t* perm_src, uint8_t* keep, const char* what) {
+  HMOE_REQUIRE(tokens >= 0 && top_k >= 1, "%s: need tokens >= 0 and top_k >= 1", what);
   HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
-               "dispatch_plan: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
-  HMOE_REQUIRE(capacity >= 1, "dispatch_plan: capacity must be >= 1 (got %lld)",
-               (long long)capacity);
+               "%s: n_experts must be in [1, %d] (got %d)", what, kMaxExperts, n_experts);
+  HMOE_REQUIRE(capacity >= 1, "%s: capacity must be >= 1 (got %lld)", what, (long long)capacity);
   const int64_t rows = tokens * top_k;
-  HMOE_REQUIRE(rows < (int64_t(1) << 31), "dispatch_plan: T*K must fit in int32 (got %lld)",
+  HMOE_REQUIRE(rows < (int64_t(1) << 31), "%s: T*K must fit in int32 (got %lld)", what,
                (long long)rows);
-  HMOE_REQUIRE(counts && offsets, "dispatch_plan: null pointer argument");
-  const size_t need = hmoe_plan_workspace_bytes(tokens, top_k, n_experts);
-  HMOE_REQUIRE_CODE(workspace_bytes >= need, HMOE_ERR_WORKSPACE,
-                    "dispatch_plan: workspace of %zu bytes is smaller than the %zu required",
-                    workspace_bytes, need);
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  HMOE_REQUIRE(counts && offsets, "%s: null pointer argument", what);
+  HMOE_REQUIRE(rows == 0 || (top_idx && slot_pos && perm_src && keep),
+               "%s: null pointer argument", what);
+  return HMOE_OK;
+}
+
+// The three plan passes on the per-block histogram buffer `hist`
+// (plan_blocks(T*K) * N int32, every entry written by the histogram pass
+// before it is read, so it needs no clearing).
+int launch_plan(const int32_t* top_idx, int64_t tokens, int top_k, int n_experts,
+                int64_t capacity, int32_t* counts, int32_t* offsets, int32_t* slot_pos,
+                int32_t* perm_src, uint8_t* keep, int32_t* hist, hipStream_t s) {
+  const int64_t rows = tokens * top_k;
   const int64_t rows_cap = hmoe_rows_cap(tokens, top_k, n_experts, capacity);
-  const int64_t nblk64 = plan_blocks(rows);
-  HMOE_REQUIRE(nblk64 < (int64_t(1) << 30), "dispatch_plan: too many slots");
-  const int nblk = static_cast<int>(nblk64);
+  const int nblk = static_cast<int>(plan_blocks(rows));
   if (rows > 0) {
-    HMOE_REQUIRE(top_idx && slot_pos && perm_src && keep && workspace,
-                 "dispatch_plan: null pointer argument");
-    int32_t* hist = static_cast<int32_t*>(workspace);
     hipLaunchKernelGGL(plan_histogram_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
                        n_experts, hist);
     if (int rc = check_launch("dispatch_plan/histogram")) return rc;
@@ -515,6 +519,92 @@ extern "C" int hmoe_dispatch_plan(const int32_t* top_idx, int64_t tokens, int to
   hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, static_cast<int32_t*>(nullptr), 0,
                      n_experts, capacity, counts, offsets);
   return check_launch("dispatch_plan/scan");
+}
+
+// Plan scratch for hmoe_dispatch_plan_noalloc: the per-block histogram in a
+// fixed device array, one copy per GPU for the life of the process.  Host
+// code never uses the array's name as an address: each device's copy is
+// looked up once (hipGetSymbolAddress, with that device current) and the
+// kernels get that pointer.
+constexpr size_t kPlanScratchInts = size_t(1) << 18;  // 1 MiB
+static __device__ __align__(256) int32_t scratch[kPlanScratchInts];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kScratchDevices];
+
+// This device's copy of `scratch` (resolved on its first use).
+int plan_scratch(int dev, int32_t** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("dispatch_plan_noalloc: cannot resolve the plan scratch on device %d: %s", dev,
+                hipGetErrorString(e));
+      return HMOE_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return HMOE_OK;
+}
+
+}  // namespace
+}  // namespace hmoe
+
+extern "C" int hmoe_dispatch_plan(const int32_t* top_idx, int64_t tokens, int top_k,
+                                  int n_experts, int64_t capacity, int32_t* counts,
+                                  int32_t* offsets, int32_t* slot_pos, int32_t* perm_src,
+                                  uint8_t* keep, void* workspace, size_t workspace_bytes,
+                                  hmoe_stream_t stream) {
+  using namespace hmoe;
+  if (int rc = check_plan_args(top_idx, tokens, top_k, n_experts, capacity, counts, offsets,
+                               slot_pos, perm_src, keep, "dispatch_plan"))
+    return rc;
+  const size_t need = hmoe_plan_workspace_bytes(tokens, top_k, n_experts);
+  HMOE_REQUIRE_CODE(workspace_bytes >= need, HMOE_ERR_WORKSPACE,
+                    "dispatch_plan: workspace of %zu bytes is smaller than the %zu required",
+                    workspace_bytes, need);
+  HMOE_REQUIRE(tokens * top_k == 0 || workspace, "dispatch_plan: null pointer argument");
+  return launch_plan(top_idx, tokens, top_k, n_experts, capacity, counts, offsets, slot_pos,
+                     perm_src, keep, static_cast<int32_t*>(workspace),
+                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hmoe_dispatch_plan_noalloc(const int32_t* top_idx, int64_t tokens, int top_k,
+                                          int n_experts, int64_t capacity, int32_t* counts,
+                                          int32_t* offsets, int32_t* slot_pos, int32_t* perm_src,
+                                          uint8_t* keep, hmoe_stream_t stream) {
+  using namespace hmoe;
+  if (int rc = check_plan_args(top_idx, tokens, top_k, n_experts, capacity, counts, offsets,
+                               slot_pos, perm_src, keep, "dispatch_plan_noalloc"))
+    return rc;
+  const size_t need = hmoe_plan_workspace_bytes(tokens, top_k, n_experts);
+  HMOE_REQUIRE_CODE(need <= kPlanScratchInts * sizeof(int32_t), HMOE_ERR_WORKSPACE,
+                    "dispatch_plan_noalloc: the plan needs %zu bytes of scratch, more than the "
+                    "%zu this entry point holds (ceil(T*K / %d) * N int32); use "
+                    "hmoe_dispatch_plan with a workspace",
+                    need, kPlanScratchInts * sizeof(int32_t), kSlotsPerBlock);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_error("dispatch_plan_noalloc: cannot query the current device (or device id >= %d)",
+              kScratchDevices);
+    return HMOE_ERR_HIP;
+  }
+  if (s != nullptr) {
+    int sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev) {
+      set_error("dispatch_plan_noalloc: the stream belongs to device %d, the current device is "
+                "%d; make the stream's device current", sdev, dev);
+      return HMOE_ERR_INVALID;
+    }
+  }
+  int32_t* hist = nullptr;
+  if (int rc = plan_scratch(dev, &hist)) return rc;
+  return launch_plan(top_idx, tokens, top_k, n_experts, capacity, counts, offsets, slot_pos,
+                     perm_src, keep, hist, s);
 }
 
 extern "C" int hmoe_permute_rows(const void* x, int x_dtype, int64_t tokens, int d_model,

@@ -103,6 +103,20 @@ int hmoe_dispatch_plan(const int32_t* top_idx, int64_t tokens, int top_k,
                        uint8_t* keep, void* workspace, size_t workspace_bytes,
                        hmoe_stream_t stream);
 
+/* The same plan without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops).  No counterpart in the reference.  The per-block histogram lives
+ * in a fixed 1 MiB device array of the library, one per GPU for the life of
+ * the process, so ceil(T*K / 1024) * N <= 262144 (e.g. T*K up to 4M slots
+ * at N = 64); larger plans return HMOE_ERR_WORKSPACE.  The stream's device
+ * must be the current device.  Calls on one GPU share the array: two calls
+ * that overlap in time on the same GPU (different streams) race; calls
+ * ordered on one stream do not.  Allocates nothing. */
+int hmoe_dispatch_plan_noalloc(const int32_t* top_idx, int64_t tokens, int top_k,
+                               int n_experts, int64_t capacity, int32_t* counts,
+                               int32_t* offsets, int32_t* slot_pos, int32_t* perm_src,
+                               uint8_t* keep, hmoe_stream_t stream);
+
 /* ---- row permutation: moe.py:56,198 (replaces `x.astype(dtype)` and
  *      `x_flat[order // K]`) ------------------------------------------------ */
 
