@@ -172,6 +172,172 @@ __global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(
     perm_src[j] = -1;
 }
 
+// Rank pass with the scan folded in (plans of at most kFusedScanBlocks
+// blocks): every workgroup derives what plan_scan_kernel would have given it
+// from the per-block histogram itself -- its block's base per expert (the
+// sum over earlier blocks), the totals and the kept-row offsets -- so the
+// plan is two launches.  The histogram is nblk * N int32 (32 KB at 16384
+// tokens x top-8 x 64 experts), read from L2 by every workgroup; sums run
+// in a fixed order, so every workgroup gets the same totals.  Workgroup 0
+// writes counts and offsets.
+constexpr int kFusedScanBlocks = 256;
+
+__global__ __launch_bounds__(kPlanThreads) void plan_rank_fused_kernel(
+    const int32_t* __restrict__ top_idx, int64_t rows, int n_experts, int64_t capacity,
+    const int32_t* __restrict__ hist, int nblk, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ slot_pos, int32_t* __restrict__ perm_src,
+    uint8_t* __restrict__ keep, int64_t rows_cap) {
+  __shared__ int32_t whist[4][kMaxExperts];
+  __shared__ int32_t part_pre[kMaxExperts];   // per (group, expert) partial sums
+  __shared__ int32_t part_tot[kMaxExperts];
+  __shared__ int32_t s_off[kMaxExperts + 1];  // kept-row offsets
+  __shared__ int32_t s_scan[kPlanThreads];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int b = blockIdx.x;
+  const int64_t blk_base = static_cast<int64_t>(b) * kSlotsPerBlock;
+  const int64_t wave_base = blk_base + static_cast<int64_t>(wave) * kSlotsPerWave;
+
+  // This lane's four slots (wave_base + lane + 64 c), loaded once and kept
+  // for the rank loop below.
+  constexpr int kSlotIters = kSlotsPerWave / 64;
+  int ev[kSlotIters];
+#pragma unroll
+  for (int c = 0; c < kSlotIters; ++c) {
+    const int64_t s = wave_base + 64 * c + lane;
+    ev[c] = s < rows ? top_idx[s] : -1;
+  }
+  for (int i = tid; i < 4 * kMaxExperts; i += kPlanThreads) (&whist[0][0])[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < kSlotIters; ++c)
+    if (static_cast<unsigned>(ev[c]) < static_cast<unsigned>(n_experts)) atomicAdd(&whist[wave][ev[c]], 1);
+  // Histogram sums: G groups of N threads (G = 256 / N; G = 1 with thread
+  // tid taking experts tid, tid + 256, ... when N > 256); group g sums the
+  // blocks g, g + G, ..., so the 64 lanes of a wave read 64 consecutive
+  // experts of one block.
+  const int G = n_experts >= kPlanThreads ? 1 : kPlanThreads / n_experts;
+  for (int idx = tid; idx < (G > 1 ? G * n_experts : n_experts); idx += kPlanThreads) {
+    const int g = G > 1 ? idx / n_experts : 0;
+    const int e = G > 1 ? idx - g * n_experts : idx;
+    int32_t pre = 0, tot = 0;
+    int bb = g;
+    // eight loads in flight at a time (the sums are exact integer sums)
+    for (; bb + 7 * G < nblk; bb += 8 * G) {
+      int32_t c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = hist[static_cast<int64_t>(bb + u * G) * n_experts + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        tot += c[u];
+        if (bb + u * G < b) pre += c[u];
+      }
+    }
+    for (; bb < nblk; bb += G) {
+      const int32_t c = hist[static_cast<int64_t>(bb) * n_experts + e];
+      tot += c;
+      if (bb < b) pre += c;
+    }
+    part_pre[idx] = pre;
+    part_tot[idx] = tot;
+  }
+  __syncthreads();
+  // Per expert: base of this block, total, kept rows (in part_tot[e]).
+  for (int e = tid; e < n_experts; e += kPlanThreads) {
+    int32_t pre = 0, tot = 0;
+    for (int g = 0; g < G; ++g) {
+      pre += part_pre[g * n_experts + e];
+      tot += part_tot[g * n_experts + e];
+    }
+    if (b == 0) counts[e] = tot;
+    // per-wave bases of this block's four waves
+    int32_t run = pre;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int32_t c = whist[w][e];
+      whist[w][e] = run;
+      run += c;
+    }
+    s_off[e] = static_cast<int32_t>(tot < capacity ? tot : capacity);
+  }
+  __syncthreads();
+  // Exclusive scan of the kept counts over the experts: each thread a run of
+  // kPer consecutive experts, a Hillis-Steele scan over the 256 run sums.
+  constexpr int kPer = kMaxExperts / kPlanThreads;
+  int32_t local[kPer];
+  int32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid * kPer + j;
+    local[j] = e < n_experts ? s_off[e] : 0;
+    sum += local[j];
+  }
+  s_scan[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int32_t v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  {
+    int32_t run = s_scan[tid] - sum;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid * kPer + j;
+      if (e < n_experts) s_off[e] = run;
+      run += local[j];
+    }
+    if (tid == kPlanThreads - 1) s_off[n_experts] = s_scan[kPlanThreads - 1];
+  }
+  __syncthreads();
+  if (b == 0)
+    for (int e = tid; e <= n_experts; e += kPlanThreads) offsets[e] = s_off[e];
+
+  const int nbits = n_experts > 1 ? 32 - __builtin_clz(static_cast<unsigned>(n_experts - 1)) : 0;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int32_t* my_hist = whist[wave];
+#pragma unroll
+  for (int ci = 0; ci < kSlotIters; ++ci) {
+    const int64_t s = wave_base + 64 * ci + lane;
+    int e = ev[ci];
+    const bool valid = static_cast<unsigned>(e) < static_cast<unsigned>(n_experts);
+    if (!valid) e = 0;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (e >> bit) & 1;
+      const uint64_t bal = __ballot(on);
+      peers &= on ? bal : ~bal;
+    }
+    int32_t base = 0;
+    if (valid) base = my_hist[e];
+    const int32_t rank = base + __popcll(peers & lt_mask);
+    const bool leader = valid && ((peers & lt_mask) == 0);
+    if (leader) my_hist[e] = base + __popcll(peers);
+    if (s < rows && !valid) {  // out-of-range expert id: never dispatched
+      keep[s] = 0;
+      slot_pos[s] = -1;
+    }
+    if (valid) {
+      const bool kept = rank < capacity;
+      keep[s] = kept ? 1 : 0;
+      if (kept) {
+        const int32_t pos = s_off[e] + rank;
+        slot_pos[s] = pos;
+        perm_src[pos] = static_cast<int32_t>(s);
+      } else {
+        slot_pos[s] = -1;
+      }
+    }
+  }
+  // Rows past the kept total hold -1.
+  const int64_t total = s_off[n_experts];
+  for (int64_t j = total + static_cast<int64_t>(b) * kPlanThreads + tid; j < rows_cap;
+       j += static_cast<int64_t>(gridDim.x) * kPlanThreads)
+    perm_src[j] = -1;
+}
+
 // ------------------------------------------------------------ permutation --
 template <typename TI>
 struct Chunk8;
@@ -504,6 +670,15 @@ int launch_plan(const int32_t* top_idx, int64_t tokens, int top_k, int n_experts
   const int64_t rows = tokens * top_k;
   const int64_t rows_cap = hmoe_rows_cap(tokens, top_k, n_experts, capacity);
   const int nblk = static_cast<int>(plan_blocks(rows));
+  if (rows > 0 && nblk <= kFusedScanBlocks) {
+    hipLaunchKernelGGL(plan_histogram_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
+                       n_experts, hist);
+    if (int rc = check_launch("dispatch_plan/histogram")) return rc;
+    hipLaunchKernelGGL(plan_rank_fused_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
+                       n_experts, capacity, hist, nblk, counts, offsets, slot_pos, perm_src, keep,
+                       rows_cap);
+    return check_launch("dispatch_plan/rank");
+  }
   if (rows > 0) {
     hipLaunchKernelGGL(plan_histogram_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
                        n_experts, hist);
