@@ -78,5 +78,33 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+XLA_FFI_SRC = PKG / "xla_ffi" / "hmoe_xla_ffi.cc"
+XLA_FFI_LIB = PKG / "xla_ffi" / "libhanuman_moe_xla.so"
+
+
+def build_xla_ffi(verbose: bool = False) -> Path | None:
+    """Compiles the XLA FFI handlers (``xla_ffi/hmoe_xla_ffi.cc``) against
+    JAX's FFI headers and links them to ``libhanuman_moe.so``; returns None
+    (and builds nothing) when JAX is not importable, since the headers ship
+    with it."""
+    import importlib.util
+    if importlib.util.find_spec("jax") is None:
+        if verbose:
+            print("xla_ffi: jax is not importable here; the handlers are not built", flush=True)
+        return None
+    import jax  # noqa: PLC0415
+    inc = jax.ffi.include_dir()
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-shared",
+           f"-I{inc}", f"-I{ROOT / 'include'}", str(XLA_FFI_SRC), f"-L{PKG}", "-lhanuman_moe",
+           "-Wl,-rpath,$ORIGIN/..", "-o", str(XLA_FFI_LIB)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"xla_ffi build failed:\n{r.stdout}{r.stderr}")
+    return XLA_FFI_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    build_xla_ffi(verbose=True)

@@ -1,0 +1,458 @@
+// XLA FFI handlers for the forward entry points of libhanuman_moe.so.
+//
+// The reference layer is JAX (model/moe.py).  A maintainer keeps its Python
+// and replaces the router lines (moe.py:175-192) and the body of
+// ragged_dispatch (moe.py:37-85) with custom calls to these handlers.  Each
+// handler forwards XLA-owned device buffers and XLA's stream to one hmoe_*
+// entry point of include/hanuman_moe.h and turns a non-zero status into an
+// ffi::Error; none allocates, synchronises or keeps a pointer past the call.
+//
+// Build (needs JAX's FFI headers, jax.ffi.include_dir(); hanuman_amd/build.py
+// build_xla_ffi() runs it when jax is importable):
+//   hipcc --offload-arch=gfx950 -O2 -std=c++17 -fPIC -shared \
+//     -I<jax.ffi.include_dir()> -I include hanuman_amd/xla_ffi/hmoe_xla_ffi.cc \
+//     -L hanuman_amd -lhanuman_moe -Wl,-rpath,'$ORIGIN/..' \
+//     -o hanuman_amd/xla_ffi/libhanuman_moe_xla.so
+// Registration (Python), once per process:
+//   lib = ctypes.cdll.LoadLibrary(".../libhanuman_moe_xla.so")
+//   jax.ffi.register_ffi_target("hmoe_router", jax.ffi.pycapsule(lib.HmoeRouter),
+//                               platform="ROCM")
+// and likewise for every XLA_FFI_DEFINE_HANDLER_SYMBOL below (symbol name =
+// the target name in CamelCase).  Output shapes are static: rows_cap =
+// hmoe_rows_cap(T, K, N, C), workspaces from hmoe_plan_workspace_bytes and
+// hmoe_aux_workspace_bytes, packed weights from hmoe_packed_*_bytes.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "hanuman_moe.h"
+#include "xla/ffi/api/ffi.h"
+
+namespace ffi = xla::ffi;
+
+namespace {
+
+ffi::Error Status(int rc) {
+  if (rc == HMOE_OK) return ffi::Error::Success();
+  const ffi::ErrorCode code = rc == HMOE_ERR_HIP           ? ffi::ErrorCode::kInternal
+                              : rc == HMOE_ERR_UNSUPPORTED ? ffi::ErrorCode::kUnimplemented
+                                                           : ffi::ErrorCode::kInvalidArgument;
+  return ffi::Error(code, hmoe_last_error());
+}
+
+// hmoe dtype code of a float buffer (F32 or BF16); -1 otherwise.
+int DtypeCode(ffi::DataType t) {
+  switch (t) {
+    case ffi::DataType::F32: return HMOE_F32;
+    case ffi::DataType::BF16: return HMOE_BF16;
+    default: return -1;
+  }
+}
+
+ffi::Error BadDtype(const char* what) {
+  return ffi::Error(ffi::ErrorCode::kInvalidArgument,
+                    std::string(what) + ": expected a float32 or bfloat16 buffer");
+}
+
+hmoe_stream_t S(hipStream_t s) { return static_cast<hmoe_stream_t>(s); }
+
+// Leading dimension (rows) and trailing dimension of a rank-2 buffer.
+template <typename B>
+int64_t Rows(const B& b) { return b.dimensions()[0]; }
+template <typename B>
+int64_t Cols(const B& b) { return b.dimensions()[b.dimensions().size() - 1]; }
+
+}  // namespace
+
+// ---- router: moe.py:175-192 -------------------------------------------------
+// x [T, D] (f32/bf16), router_w [D, N] (f32/bf16), bias [N] f32 ->
+// logits [T, N] f32, top_idx [T, K] s32, gates [T, K] f32.
+static ffi::Error RouterImpl(hipStream_t stream, ffi::AnyBuffer x, ffi::AnyBuffer w,
+                             ffi::Buffer<ffi::F32> bias, int64_t mode, float rsf,
+                             ffi::ResultBuffer<ffi::F32> logits,
+                             ffi::ResultBuffer<ffi::S32> top_idx,
+                             ffi::ResultBuffer<ffi::F32> gates) {
+  const int xd = DtypeCode(x.element_type()), wd = DtypeCode(w.element_type());
+  if (xd < 0) return BadDtype("hmoe_router x");
+  if (wd < 0) return BadDtype("hmoe_router router_w");
+  const int64_t T = Rows(x);
+  const int D = static_cast<int>(Cols(x)), N = static_cast<int>(Cols(w));
+  const int K = static_cast<int>(Cols(*top_idx));
+  return Status(hmoe_router(x.untyped_data(), xd, w.untyped_data(), wd, bias.typed_data(), T, D,
+                            N, K, static_cast<int>(mode), rsf, logits->typed_data(),
+                            top_idx->typed_data(), gates->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeRouter, RouterImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Attr<int64_t>("mode")
+                                  .Attr<float>("routed_scaling_factor")
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+// logits [T, N] f32, bias [N] f32 -> top_idx [T, K] s32, gates [T, K] f32.
+static ffi::Error RouterFromLogitsImpl(hipStream_t stream, ffi::Buffer<ffi::F32> logits,
+                                       ffi::Buffer<ffi::F32> bias, int64_t mode, float rsf,
+                                       ffi::ResultBuffer<ffi::S32> top_idx,
+                                       ffi::ResultBuffer<ffi::F32> gates) {
+  return Status(hmoe_router_from_logits(
+      logits.typed_data(), bias.typed_data(), Rows(logits), static_cast<int>(Cols(logits)),
+      static_cast<int>(Cols(*top_idx)), static_cast<int>(mode), rsf, top_idx->typed_data(),
+      gates->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeRouterFromLogits, RouterFromLogitsImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Attr<int64_t>("mode")
+                                  .Attr<float>("routed_scaling_factor")
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+// ---- dispatch plan: moe.py:54-57, 80 ---------------------------------------
+// top_idx [T, K] s32 -> counts [N], offsets [N+1], slot_pos [T*K],
+// perm_src [rows_cap] s32, keep [T*K] u8, workspace u8.
+static ffi::Error DispatchPlanImpl(hipStream_t stream, ffi::Buffer<ffi::S32> top_idx,
+                                   int64_t capacity, ffi::ResultBuffer<ffi::S32> counts,
+                                   ffi::ResultBuffer<ffi::S32> offsets,
+                                   ffi::ResultBuffer<ffi::S32> slot_pos,
+                                   ffi::ResultBuffer<ffi::S32> perm_src,
+                                   ffi::ResultBuffer<ffi::U8> keep,
+                                   ffi::ResultBuffer<ffi::U8> workspace) {
+  return Status(hmoe_dispatch_plan(
+      top_idx.typed_data(), Rows(top_idx), static_cast<int>(Cols(top_idx)),
+      static_cast<int>(counts->element_count()), capacity, counts->typed_data(),
+      offsets->typed_data(), slot_pos->typed_data(), perm_src->typed_data(), keep->typed_data(),
+      workspace->untyped_data(), workspace->size_bytes(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeDispatchPlan, DispatchPlanImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Attr<int64_t>("capacity")
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>());
+
+// ---- row permutation: moe.py:56, 198 ----------------------------------------
+// x [T, D] (f32/bf16), slot_pos [T*K] s32 -> xs [rows_cap, D] (f32/bf16).
+static ffi::Error PermuteRowsImpl(hipStream_t stream, ffi::AnyBuffer x,
+                                  ffi::Buffer<ffi::S32> slot_pos, ffi::Result<ffi::AnyBuffer> xs) {
+  const int xd = DtypeCode(x.element_type()), od = DtypeCode(xs->element_type());
+  if (xd < 0 || od < 0) return BadDtype("hmoe_permute_rows");
+  const int64_t T = Rows(x);
+  const int K = static_cast<int>(slot_pos.element_count() / (T > 0 ? T : 1));
+  return Status(hmoe_permute_rows(x.untyped_data(), xd, T, static_cast<int>(Cols(x)), K,
+                                  slot_pos.typed_data(), xs->untyped_data(), od, S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoePermuteRows, PermuteRowsImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::AnyBuffer>());
+
+// x [T, D] (f32/bf16), slot_pos [T*K] -> xs_q [rows_cap, D] u8 (e4m3 codes),
+// xs_scale [rows_cap] f32.
+static ffi::Error PermuteRowsFp8Impl(hipStream_t stream, ffi::AnyBuffer x,
+                                     ffi::Buffer<ffi::S32> slot_pos,
+                                     ffi::ResultBuffer<ffi::U8> xs_q,
+                                     ffi::ResultBuffer<ffi::F32> xs_scale) {
+  const int xd = DtypeCode(x.element_type());
+  if (xd < 0) return BadDtype("hmoe_permute_rows_fp8");
+  const int64_t T = Rows(x);
+  const int K = static_cast<int>(slot_pos.element_count() / (T > 0 ? T : 1));
+  return Status(hmoe_permute_rows_fp8(x.untyped_data(), xd, T, static_cast<int>(Cols(x)), K,
+                                      slot_pos.typed_data(), xs_q->typed_data(),
+                                      xs_scale->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoePermuteRowsFp8, PermuteRowsFp8Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+// a [rows, cols] bf16, offsets [N+1] s32 -> q [rows, cols] u8, scale [rows] f32.
+static ffi::Error QuantizeRowsFp8Impl(hipStream_t stream, ffi::Buffer<ffi::BF16> a,
+                                      ffi::Buffer<ffi::S32> offsets,
+                                      ffi::ResultBuffer<ffi::U8> q,
+                                      ffi::ResultBuffer<ffi::F32> scale) {
+  return Status(hmoe_quantize_rows_fp8(a.untyped_data(), Rows(a), static_cast<int>(Cols(a)),
+                                       offsets.typed_data(),
+                                       static_cast<int>(offsets.element_count() - 1),
+                                       q->typed_data(), scale->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeQuantizeRowsFp8, QuantizeRowsFp8Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+// ---- expert weight packing: moe.py:204-206 (once per parameter update) -----
+// w_gate, w_up [N, D, F] (f32/bf16) -> packed gate/up (hmoe_packed_gate_up_bytes).
+static ffi::Error PackGateUpImpl(hipStream_t stream, ffi::AnyBuffer wg, ffi::AnyBuffer wu,
+                                 ffi::ResultBuffer<ffi::U8> packed) {
+  const int d = DtypeCode(wg.element_type());
+  if (d < 0 || DtypeCode(wu.element_type()) != d) return BadDtype("hmoe_pack_gate_up");
+  auto dims = wg.dimensions();
+  return Status(hmoe_pack_gate_up(wg.untyped_data(), wu.untyped_data(), d,
+                                  static_cast<int>(dims[0]), static_cast<int>(dims[1]),
+                                  static_cast<int>(dims[2]), packed->untyped_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoePackGateUp, PackGateUpImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::U8>>());
+
+// w_down [N, F, D] (f32/bf16) -> packed down (hmoe_packed_down_bytes).
+static ffi::Error PackDownImpl(hipStream_t stream, ffi::AnyBuffer wd,
+                               ffi::ResultBuffer<ffi::U8> packed) {
+  const int d = DtypeCode(wd.element_type());
+  if (d < 0) return BadDtype("hmoe_pack_down");
+  auto dims = wd.dimensions();
+  return Status(hmoe_pack_down(wd.untyped_data(), d, static_cast<int>(dims[0]),
+                               static_cast<int>(dims[1]), static_cast<int>(dims[2]),
+                               packed->untyped_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoePackDown, PackDownImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::U8>>());
+
+// e4m3 packing with per-output-channel scales ([N][2F] / [N][D] f32).
+static ffi::Error PackFp8GateUpImpl(hipStream_t stream, ffi::AnyBuffer wg, ffi::AnyBuffer wu,
+                                    ffi::ResultBuffer<ffi::U8> packed,
+                                    ffi::ResultBuffer<ffi::F32> scales) {
+  const int d = DtypeCode(wg.element_type());
+  if (d < 0 || DtypeCode(wu.element_type()) != d) return BadDtype("hmoe_pack_fp8_gate_up");
+  auto dims = wg.dimensions();
+  return Status(hmoe_pack_fp8_gate_up(wg.untyped_data(), wu.untyped_data(), d,
+                                      static_cast<int>(dims[0]), static_cast<int>(dims[1]),
+                                      static_cast<int>(dims[2]), packed->typed_data(),
+                                      scales->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoePackFp8GateUp, PackFp8GateUpImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+static ffi::Error PackFp8DownImpl(hipStream_t stream, ffi::AnyBuffer wd,
+                                  ffi::ResultBuffer<ffi::U8> packed,
+                                  ffi::ResultBuffer<ffi::F32> scales) {
+  const int d = DtypeCode(wd.element_type());
+  if (d < 0) return BadDtype("hmoe_pack_fp8_down");
+  auto dims = wd.dimensions();
+  return Status(hmoe_pack_fp8_down(wd.untyped_data(), d, static_cast<int>(dims[0]),
+                                   static_cast<int>(dims[1]), static_cast<int>(dims[2]),
+                                   packed->typed_data(), scales->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoePackFp8Down, PackFp8DownImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+// ---- grouped expert GEMMs: moe.py:67-74 -------------------------------------
+// xs [rows_cap, D] bf16, offsets [N+1], packed gate/up -> h [rows_cap, F] bf16.
+static ffi::Error GroupedGateUpImpl(hipStream_t stream, ffi::Buffer<ffi::BF16> xs,
+                                    ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+                                    ffi::ResultBuffer<ffi::BF16> h) {
+  return Status(hmoe_grouped_gate_up(xs.untyped_data(), offsets.typed_data(),
+                                     static_cast<int>(offsets.element_count() - 1), Rows(xs),
+                                     static_cast<int>(Cols(xs)), static_cast<int>(Cols(*h)),
+                                     w.untyped_data(), h->untyped_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUp, GroupedGateUpImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
+// x [T, D] bf16 (rows gathered through perm_src, moe.py:56 fused), perm_src
+// [rows_cap], offsets [N+1], packed gate/up -> h [rows_cap, F] bf16.
+static ffi::Error GroupedGateUpGatherImpl(hipStream_t stream, ffi::Buffer<ffi::BF16> x,
+                                          ffi::Buffer<ffi::S32> perm_src,
+                                          ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+                                          int64_t top_k, ffi::ResultBuffer<ffi::BF16> h) {
+  return Status(hmoe_grouped_gate_up_gather(
+      x.untyped_data(), Rows(x), static_cast<int>(top_k), perm_src.typed_data(),
+      offsets.typed_data(), static_cast<int>(offsets.element_count() - 1), Rows(*h),
+      static_cast<int>(Cols(x)), static_cast<int>(Cols(*h)), w.untyped_data(), h->untyped_data(),
+      S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpGather, GroupedGateUpGatherImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Attr<int64_t>("top_k")
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
+// h [rows_cap, F] bf16, offsets, packed down -> ys [rows_cap, D] bf16.
+static ffi::Error GroupedDownImpl(hipStream_t stream, ffi::Buffer<ffi::BF16> h,
+                                  ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+                                  ffi::ResultBuffer<ffi::BF16> ys) {
+  return Status(hmoe_grouped_down(h.untyped_data(), offsets.typed_data(),
+                                  static_cast<int>(offsets.element_count() - 1), Rows(h),
+                                  static_cast<int>(Cols(h)), static_cast<int>(Cols(*ys)),
+                                  w.untyped_data(), ys->untyped_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedDown, GroupedDownImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
+// e4m3 expert GEMMs (the fp8 workload rule).
+static ffi::Error GroupedGateUpFp8Impl(hipStream_t stream, ffi::Buffer<ffi::U8> xs_q,
+                                       ffi::Buffer<ffi::F32> xs_scale,
+                                       ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+                                       ffi::Buffer<ffi::F32> w_scales,
+                                       ffi::ResultBuffer<ffi::BF16> h) {
+  return Status(hmoe_grouped_gate_up_fp8(
+      xs_q.typed_data(), xs_scale.typed_data(), offsets.typed_data(),
+      static_cast<int>(offsets.element_count() - 1), Rows(xs_q), static_cast<int>(Cols(xs_q)),
+      static_cast<int>(Cols(*h)), w.typed_data(), w_scales.typed_data(), h->untyped_data(),
+      S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpFp8, GroupedGateUpFp8Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
+static ffi::Error GroupedDownFp8Impl(hipStream_t stream, ffi::Buffer<ffi::U8> h_q,
+                                     ffi::Buffer<ffi::F32> h_scale, ffi::Buffer<ffi::S32> offsets,
+                                     ffi::Buffer<ffi::U8> w, ffi::Buffer<ffi::F32> w_scales,
+                                     ffi::ResultBuffer<ffi::BF16> ys) {
+  return Status(hmoe_grouped_down_fp8(
+      h_q.typed_data(), h_scale.typed_data(), offsets.typed_data(),
+      static_cast<int>(offsets.element_count() - 1), Rows(h_q), static_cast<int>(Cols(h_q)),
+      static_cast<int>(Cols(*ys)), w.typed_data(), w_scales.typed_data(), ys->untyped_data(),
+      S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedDownFp8, GroupedDownFp8Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
+// float32 compute dtype: masters as they are.
+static ffi::Error GroupedGateUpF32Impl(hipStream_t stream, ffi::Buffer<ffi::F32> xs,
+                                       ffi::Buffer<ffi::S32> offsets,
+                                       ffi::Buffer<ffi::F32> w_gate, ffi::Buffer<ffi::F32> w_up,
+                                       ffi::ResultBuffer<ffi::F32> h) {
+  return Status(hmoe_grouped_gate_up_f32(
+      xs.typed_data(), offsets.typed_data(), static_cast<int>(offsets.element_count() - 1),
+      Rows(xs), static_cast<int>(Cols(xs)), static_cast<int>(Cols(*h)), w_gate.typed_data(),
+      w_up.typed_data(), h->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpF32, GroupedGateUpF32Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+static ffi::Error GroupedDownF32Impl(hipStream_t stream, ffi::Buffer<ffi::F32> h,
+                                     ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::F32> w_down,
+                                     ffi::ResultBuffer<ffi::F32> ys) {
+  return Status(hmoe_grouped_down_f32(h.typed_data(), offsets.typed_data(),
+                                      static_cast<int>(offsets.element_count() - 1), Rows(h),
+                                      static_cast<int>(Cols(h)), static_cast<int>(Cols(*ys)),
+                                      w_down.typed_data(), ys->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedDownF32, GroupedDownF32Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
+// ---- combine: moe.py:80-85 (+ the shared expert's output, moe.py:249-251) ---
+// ys [rows, D] (bf16/f32), slot_pos [T*K], gates [T, K] f32, residual [T, D]
+// (f32/bf16; pass a zero-size buffer for none) -> out [T, D] (f32/bf16).
+static ffi::Error CombineImpl(hipStream_t stream, ffi::AnyBuffer ys,
+                              ffi::Buffer<ffi::S32> slot_pos, ffi::Buffer<ffi::F32> gates,
+                              ffi::AnyBuffer residual, ffi::Result<ffi::AnyBuffer> out) {
+  const int yd = DtypeCode(ys.element_type()), od = DtypeCode(out->element_type());
+  if (yd < 0 || od < 0) return BadDtype("hmoe_combine");
+  const bool has_res = residual.element_count() > 0;
+  const int rd = has_res ? DtypeCode(residual.element_type()) : HMOE_F32;
+  if (rd < 0) return BadDtype("hmoe_combine residual");
+  return Status(hmoe_combine(ys.untyped_data(), yd, slot_pos.typed_data(), gates.typed_data(),
+                             has_res ? residual.untyped_data() : nullptr, rd, Rows(gates),
+                             static_cast<int>(Cols(gates)), static_cast<int>(Cols(*out)),
+                             out->untyped_data(), od, S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeCombine, CombineImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>());
+
+// ---- aux outputs: moe.py:253-292 --------------------------------------------
+// logits [B*S, N] f32, top_idx [B*S, K] -> losses [3] f32 (z, balance,
+// entropy), expert_counts [N] f32, workspace u8 (hmoe_aux_workspace_bytes).
+static ffi::Error RouterAuxImpl(hipStream_t stream, ffi::Buffer<ffi::F32> logits,
+                                ffi::Buffer<ffi::S32> top_idx, int64_t batch,
+                                ffi::ResultBuffer<ffi::F32> losses,
+                                ffi::ResultBuffer<ffi::F32> expert_counts,
+                                ffi::ResultBuffer<ffi::U8> workspace) {
+  const int64_t T = Rows(logits);
+  const int B = static_cast<int>(batch);
+  return Status(hmoe_router_aux(logits.typed_data(), top_idx.typed_data(), B,
+                                static_cast<int>(B > 0 ? T / B : 0),
+                                static_cast<int>(Cols(logits)), static_cast<int>(Cols(top_idx)),
+                                losses->typed_data(), expert_counts->typed_data(),
+                                workspace->untyped_data(), workspace->size_bytes(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeRouterAux, RouterAuxImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Attr<int64_t>("batch")
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>());
