@@ -115,7 +115,8 @@ def moe_backward_weights(x: torch.Tensor, fwd: dict, data: dict) -> dict:
     return {"dWg": dwg, "dWu": dwu, "dWd": dwd, "d_router": d_router}
 
 
-def shared_backward(xc: torch.Tensor, d_shared: torch.Tensor, h_shared, ops: SharedOperands) -> dict:
+def shared_backward(xc: torch.Tensor, d_shared: torch.Tensor, h_shared, ops: SharedOperands,
+                    weights: bool = True) -> dict:
     """VJP of the shared expert(s) for the output cotangent ``d_shared``
     (``bf16(dy / n_shared)`` from :func:`kernels.combine_bwd`): each SwiGLU
     (``moe.py:23-29``) is one segment of all ``T`` rows on the grouped
@@ -130,10 +131,14 @@ def shared_backward(xc: torch.Tensor, d_shared: torch.Tensor, h_shared, ops: Sha
         dh = K.grouped_dgrad_down(d_shared, off, down_dgrad)
         dgu = K.grouped_gate_up_swiglu_bwd(xc, off, fwd_gu, dh)
         dxs.append(K.grouped_dgrad_gate_up(dgu, off, gu_dgrad))
-        g_, u_ = K.grouped_wgrad_gate_up(xc, dgu, off)
-        dwg.append(g_)
-        dwu.append(u_)
-        dwd.append(K.grouped_wgrad_down(h, d_shared, off))
+        if weights:
+            g_, u_ = K.grouped_wgrad_gate_up(xc, dgu, off)
+            dwg.append(g_)
+            dwu.append(u_)
+            dwd.append(K.grouped_wgrad_down(h, d_shared, off))
+    if not weights:
+        dx = dxs[0] if ops.n_shared == 1 else sum(d.float() for d in dxs)
+        return {"dx": dx, "dWg": None, "dWu": None, "dWd": None}
     if ops.n_shared == 1:
         return {"dx": dxs[0], "dWg": dwg[0][0], "dWu": dwu[0][0], "dWd": dwd[0][0]}
     # several shared experts: their input gradients add in float32
@@ -147,7 +152,7 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
                  w_gate_up: torch.Tensor, ops: BackwardOperands, dy: torch.Tensor, *,
                  mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0,
                  shared: SharedOperands | None = None, h_shared=None,
-                 aux: tuple | None = None) -> dict:
+                 aux: tuple | None = None, need: dict | None = None) -> dict:
     """The whole module's VJP (``moe.py:170-294``): every input and weight
     gradient for the cotangent ``dy`` (f32 ``[T, D]``) of ``out`` and, with
     ``aux = (batch, seq, d_losses)``, the cotangents ``d_losses`` (f32 ``[3]``:
@@ -159,8 +164,10 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
     Returns ``dx`` f32 ``[T, D]``, ``d_router`` f32 ``[D, N]`` (None without a
     router weight), ``dWg``, ``dWu`` ``[N, D, F]``, ``dWd`` ``[N, F, D]`` and
     ``dWg_shared``, ``dWu_shared``, ``dWd_shared`` when there is a shared
-    expert.
+    expert.  ``need`` (``{"router", "experts", "shared"}`` -> bool, default
+    all) skips the weight gradients not asked for; those entries are None.
     """
+    need = {"router": True, "experts": True, "shared": True, **(need or {})}
     plan = fwd["plan"]
     N = plan.n_experts
     xc = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)   # x.astype(dtype), moe.py:198
@@ -173,7 +180,7 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
     res = {}
     residual = None
     if shared is not None:
-        sh = shared_backward(xc, d_sh, h_shared, shared)
+        sh = shared_backward(xc, d_sh, h_shared, shared, weights=need["shared"])
         residual = sh["dx"]
         res.update(dWg_shared=sh["dWg"], dWu_shared=sh["dWu"], dWd_shared=sh["dWd"])
     dx = K.gather_bwd(d_xs, plan, residual=residual)
@@ -185,11 +192,14 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
         K.router_aux_bwd(fwd["logits"], fwd["top_idx"], batch, seq, d_losses, d_logits)
     if router_w is not None:
         K.router_dx(d_logits, router_w, dx)
-    xs = K.permute_rows(x, plan, torch.bfloat16)
-    dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, plan.offsets)
-    del xs, dgu
-    dwd = K.grouped_wgrad_down(fwd["h"], d_ys, plan.offsets)
-    d_router = K.router_dw(x, d_logits) if router_w is not None else None
+    dwg = dwu = dwd = None
+    if need["experts"]:
+        xs = K.permute_rows(x, plan, torch.bfloat16)
+        dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, plan.offsets)
+        del xs
+        dwd = K.grouped_wgrad_down(fwd["h"], d_ys, plan.offsets)
+    del dgu
+    d_router = K.router_dw(x, d_logits) if router_w is not None and need["router"] else None
     res.update(dx=dx, d_router=d_router, dWg=dwg, dWu=dwu, dWd=dwd, d_logits=d_logits,
                d_gates=d_gates)
     return res
@@ -220,11 +230,13 @@ def _shared_backward_f32(x32: torch.Tensor, d_shared: torch.Tensor, h_shared, ma
 
 def moe_backward_f32(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict, masters, dy,
                      *, mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0,
-                     shared=None, h_shared=None, aux: tuple | None = None) -> dict:
+                     shared=None, h_shared=None, aux: tuple | None = None,
+                     need: dict | None = None) -> dict:
     """:func:`moe_backward` for the float32 compute dtype: ``masters =
     (w_gate, w_up, w_down)`` float32 as they are, ``fwd`` adds the forward's
     dispatched rows ``xs`` (float32), ``shared = (w_gate, w_up, w_down,
-    n_shared)`` or None.  Same results dict."""
+    n_shared)`` or None.  Same results dict and ``need``."""
+    need = {"router": True, "experts": True, "shared": True, **(need or {})}
     plan = fwd["plan"]
     N = plan.n_experts
     wg, wu, wd = masters
@@ -254,10 +266,12 @@ def moe_backward_f32(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict, 
         K.router_aux_bwd(fwd["logits"], fwd["top_idx"], batch, seq, d_losses, d_logits)
     if router_w is not None:
         K.router_dx(d_logits, router_w, dx)
-    dwg, dwu = K.grouped_wgrad_gate_up_f32(xs, dgu, plan.offsets)
+    dwg = dwu = dwd = None
+    if need["experts"]:
+        dwg, dwu = K.grouped_wgrad_gate_up_f32(xs, dgu, plan.offsets)
+        dwd = K.grouped_wgrad_down_f32(fwd["h"], d_ys, plan.offsets)
     del dgu
-    dwd = K.grouped_wgrad_down_f32(fwd["h"], d_ys, plan.offsets)
-    d_router = K.router_dw(x, d_logits) if router_w is not None else None
+    d_router = K.router_dw(x, d_logits) if router_w is not None and need["router"] else None
     res.update(dx=dx, d_router=d_router, dWg=dwg, dWu=dwu, dWd=dwd, d_logits=d_logits,
                d_gates=d_gates)
     return res

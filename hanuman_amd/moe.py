@@ -13,6 +13,8 @@ resident in one GPU's HBM, so ``mesh`` must be None or hold one device.
 """
 from __future__ import annotations
 
+import weakref
+
 import numpy as np
 import torch
 
@@ -79,17 +81,24 @@ def _f32_swiglu_one(x32: torch.Tensor, wg, wu, wd, hs: list | None = None) -> to
 
 
 class _PackCache:
-    """Packed bf16 operands of fp32 master weights, rebuilt when a master changes."""
+    """Packed bf16 operands of fp32 master weights, rebuilt when a master
+    changes: a different tensor object (held by weak reference and compared
+    by identity, so a new tensor at a freed address is not mistaken for the
+    old one) or an in-place update (the tensor's version counter)."""
 
     def __init__(self):
-        self._key = None
+        self._refs = None
+        self._versions = None
         self._val = None
 
     def get(self, tensors, build):
-        key = tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype) for t in tensors)
-        if key != self._key:
+        same = (self._refs is not None and len(self._refs) == len(tensors)
+                and all(r() is t for r, t in zip(self._refs, tensors))
+                and all(t._version == v for t, v in zip(tensors, self._versions)))
+        if not same:
             self._val = build()
-            self._key = key
+            self._refs = tuple(weakref.ref(t) for t in tensors)
+            self._versions = tuple(t._version for t in tensors)
         return self._val
 
 
@@ -248,12 +257,16 @@ class MoE:
         from safetensors.numpy import load_file
         self.load_state(load_file(str(path)))
 
-    def _packed_routed(self):
-        wg, wu, wd = self.expert_w_gate.value, self.expert_w_up.value, self.expert_w_down.value
+    def _packed_routed(self, masters=None):
+        """Packed routed-expert operands of ``masters`` (default: the current
+        parameters)."""
+        wg, wu, wd = masters if masters is not None else (
+            self.expert_w_gate.value, self.expert_w_up.value, self.expert_w_down.value)
         return self._routed_pack.get((wg, wu, wd), lambda: (K.pack_gate_up(wg, wu), K.pack_down(wd)))
 
-    def _packed_shared(self):
-        wg, wu, wd = self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value
+    def _packed_shared(self, masters=None):
+        wg, wu, wd = masters if masters is not None else (
+            self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value)
 
         def build():
             if self.n_shared_experts == 1:
@@ -372,32 +385,48 @@ class MoE:
                      "batch": B, "seq": S}
         return out.reshape(B, S, D), losses, counts, saved
 
-    def _backward_operands(self):
-        """Packed backward operands of the routed and shared experts, cached
-        like the forward's packs (rebuilt when a master changes)."""
+    def _backward_operands(self, masters):
+        """Packed backward operands of the routed and shared experts for the
+        masters ``(wg, wu, wd, swg, swu, swd)`` the forward used, cached like
+        the forward's packs (rebuilt when a master changes)."""
         if not hasattr(self, "_bwd_pack"):
             self._bwd_pack = _PackCache()
-        wg, wu, wd = self.expert_w_gate.value, self.expert_w_up.value, self.expert_w_down.value
-        swg, swu, swd = self.shared_w_gate.value, self.shared_w_up.value, self.shared_w_down.value
+        wg, wu, wd, swg, swu, swd = masters
         from .backward import BackwardOperands, SharedOperands
 
         def build():
             return (BackwardOperands(wg, wu, wd),
-                    SharedOperands(swg, swu, swd, self.n_shared_experts, self._packed_shared()))
+                    SharedOperands(swg, swu, swd, self.n_shared_experts,
+                                   self._packed_shared((swg, swu, swd))))
         return self._bwd_pack.get((wg, wu, wd, swg, swu, swd), build)
 
 
 class _MoEFunction(torch.autograd.Function):
     """``MoE.__call__`` as one autograd node: forward on the library, backward
-    the library's VJP of the whole module (routing held fixed)."""
+    the library's VJP of the whole module (routing held fixed).  Every
+    residual, and every parameter tensor the forward read, goes through
+    ``save_for_backward``: a second backward through a retained graph works,
+    and an in-place change of a parameter between forward and backward raises
+    (torch's saved-tensor version check) instead of giving gradients of
+    other weights."""
+
+    _PLAN = ("counts", "offsets", "slot_pos", "perm_src", "keep")
 
     @staticmethod
     def forward(ctx, layer, x, router, wg, wu, wd, swg, swu, swd):
         out, losses, counts, saved = layer._forward(x, save=True)
+        plan = saved["plan"]
+        hs = list(saved["h_shared"] or [])
         ctx.layer = layer
-        ctx.saved = saved
+        ctx.meta = {"capacity": plan.capacity, "rows_cap": plan.rows_cap,
+                    "n_experts": plan.n_experts, "top_k": plan.top_k, "mode": saved["mode"],
+                    "rsf": saved["rsf"], "batch": saved["batch"], "seq": saved["seq"],
+                    "n_hs": len(hs), "f32": "xs" in saved}
         ctx.x_shape, ctx.x_dtype = x.shape, x.dtype
-        ctx.shared_shapes = (swg.shape, swu.shape, swd.shape)
+        ctx.save_for_backward(saved["x"], saved["logits"], saved["top_idx"], saved["gates"],
+                              *(getattr(plan, k) for k in _MoEFunction._PLAN),
+                              saved["h"], saved["ys"], saved.get("xs"), *hs,
+                              router, wg, wu, wd, swg, swu, swd)
         ctx.mark_non_differentiable(counts)
         z, bal, ent = (v.clone() for v in losses.unbind())
         return out, z, bal, ent, counts
@@ -405,9 +434,15 @@ class _MoEFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_out, d_z, d_bal, d_ent, d_counts):
         from .backward import moe_backward, moe_backward_f32
-        layer, sv = ctx.layer, ctx.saved
-        ctx.saved = None
-        x2 = sv["x"]
+        layer, m = ctx.layer, ctx.meta
+        st = list(ctx.saved_tensors)
+        x2, logits, top_idx, gates = st[0:4]
+        plan = K.Plan(*st[4:9], m["capacity"], m["rows_cap"], m["n_experts"], m["top_k"])
+        h, ys, xs = st[9:12]
+        hs = st[12:12 + m["n_hs"]]
+        router, wg, wu, wd, swg, swu, swd = st[12 + m["n_hs"]:]
+        fwd = {"logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan, "h": h,
+               "ys": ys}
         T, D = x2.shape
         dev = x2.device
         dy = (d_out.reshape(T, D).float().contiguous() if d_out is not None
@@ -415,28 +450,32 @@ class _MoEFunction(torch.autograd.Function):
         zero = torch.zeros((), dtype=torch.float32, device=dev)
         d_losses = torch.stack([(g.float() if g is not None else zero)
                                 for g in (d_z, d_bal, d_ent)]).contiguous()
-        router_w = layer.router.value.float().contiguous()
-        aux = (sv["batch"], sv["seq"], d_losses)
-        if layer.dtype == torch.float32:
-            masters = tuple(p.value.float().contiguous() for p in
-                            (layer.expert_w_gate, layer.expert_w_up, layer.expert_w_down))
+        router_w = router.float().contiguous()
+        aux = (m["batch"], m["seq"], d_losses)
+        ng = ctx.needs_input_grad  # (layer, x, router, wg, wu, wd, swg, swu, swd)
+        need = {"router": ng[2], "experts": any(ng[3:6]), "shared": any(ng[6:9])}
+        if m["f32"]:
+            fwd["xs"] = xs
+            masters = tuple(t.float().contiguous() for t in (wg, wu, wd))
             shared = None
             if layer.n_shared_experts > 0:
-                shared = tuple(p.value.float().contiguous() for p in
-                               (layer.shared_w_gate, layer.shared_w_up, layer.shared_w_down))
+                shared = tuple(t.float().contiguous() for t in (swg, swu, swd))
                 shared = shared + (layer.n_shared_experts,)
-            g = moe_backward_f32(x2, router_w, sv, masters, dy, mode=sv["mode"],
-                                 routed_scaling_factor=sv["rsf"], shared=shared,
-                                 h_shared=sv["h_shared"], aux=aux)
+            g = moe_backward_f32(x2, router_w, fwd, masters, dy, mode=m["mode"],
+                                 routed_scaling_factor=m["rsf"], shared=shared, h_shared=hs,
+                                 aux=aux, need=need)
         else:
-            ops, shared = layer._backward_operands()
-            wgu, _ = layer._packed_routed()
-            g = moe_backward(x2, router_w, {k: sv[k] for k in ("logits", "top_idx", "gates",
-                                                               "plan", "h", "ys")},
-                             wgu, ops, dy, mode=sv["mode"], routed_scaling_factor=sv["rsf"],
-                             shared=shared, h_shared=sv["h_shared"], aux=aux)
-        dx = g["dx"].reshape(ctx.x_shape).to(ctx.x_dtype)
-        sg, su, sd = ctx.shared_shapes
-        return (None, dx, g["d_router"], g["dWg"], g["dWu"], g["dWd"],
-                g["dWg_shared"].reshape(sg), g["dWu_shared"].reshape(su),
-                g["dWd_shared"].reshape(sd))
+            ops, shared = layer._backward_operands((wg, wu, wd, swg, swu, swd))
+            wgu, _ = layer._packed_routed((wg, wu, wd))
+            g = moe_backward(x2, router_w, fwd, wgu, ops, dy, mode=m["mode"],
+                             routed_scaling_factor=m["rsf"], shared=shared, h_shared=hs,
+                             aux=aux, need=need)
+        dx = g["dx"].reshape(ctx.x_shape).to(ctx.x_dtype) if ng[1] else None
+
+        def shaped(key, like, wanted):
+            return g[key].reshape(like.shape) if wanted and g.get(key) is not None else None
+        return (None, dx, g["d_router"] if ng[2] else None,
+                g["dWg"] if ng[3] else None, g["dWu"] if ng[4] else None,
+                g["dWd"] if ng[5] else None,
+                shaped("dWg_shared", swg, ng[6]), shaped("dWu_shared", swu, ng[7]),
+                shaped("dWd_shared", swd, ng[8]))

@@ -573,3 +573,50 @@ def test_module_trains(gpu, dtype):
     print(f"module training ({dtype}): loss {losses[0]:.4e} -> {losses[-1]:.4e}", flush=True)
     assert all(np.isfinite(losses))
     assert losses[-1] < 0.5 * losses[0]
+
+
+def test_module_autograd_saved_tensors(gpu):
+    """The autograd node keeps its residuals and the forward's parameters as
+    saved tensors: a second backward through a retained graph gives the same
+    gradients, an in-place parameter update between forward and backward
+    raises (torch's version check), and with only the input requiring grad
+    the input gradient is unchanged and no weight gradient is produced."""
+    Bq, Sq, D, F, N, Kk = 1, 128, 256, 256, 8, 2
+    m = MoE(D, F, N, Kk, 1, 0.05, 2.5, torch.bfloat16, rngs=3, device=gpu)
+    names = ("router", "expert_w_gate", "expert_w_up", "expert_w_down",
+             "shared_w_gate", "shared_w_up", "shared_w_down")
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    x = torch.randn(Bq, Sq, D, generator=gen, device=gpu).to(torch.bfloat16)
+    dy = torch.randn(Bq, Sq, D, generator=gen, device=gpu)
+    for n in names:
+        getattr(m, n).value.requires_grad_(True)
+    xg = x.clone().requires_grad_(True)
+    out, aux = m(xg)
+    loss = (out * dy).sum() + 0.3 * aux["router_z_loss"]
+    loss.backward(retain_graph=True)
+    first = {n: getattr(m, n).value.grad.clone() for n in names}
+    dx_first = xg.grad.clone()
+    for n in names:
+        getattr(m, n).value.grad = None
+    xg.grad = None
+    loss.backward()
+    torch.cuda.synchronize()
+    for n in names:
+        assert torch.equal(getattr(m, n).value.grad, first[n]), n
+    assert torch.equal(xg.grad, dx_first)
+    # an in-place update of a parameter the forward read
+    out, aux = m(x)
+    with torch.no_grad():
+        m.expert_w_up.value.mul_(1.0)
+    with pytest.raises(RuntimeError):
+        out.sum().backward()
+    # only the input requires grad
+    for n in names:
+        getattr(m, n).value.grad = None
+        getattr(m, n).value.requires_grad_(False)
+    xg2 = x.clone().requires_grad_(True)
+    out, aux = m(xg2)
+    ((out * dy).sum() + 0.3 * aux["router_z_loss"]).backward()
+    torch.cuda.synchronize()
+    assert torch.equal(xg2.grad, dx_first)
+    assert all(getattr(m, n).value.grad is None for n in names)

@@ -102,3 +102,25 @@ def test_moe_state_round_trip(tmp_path):
     del missing["bias"]
     with pytest.raises(KeyError, match="bias"):
         c.load_state(missing)
+
+
+def test_pack_cache_rebuilds_on_identity_or_version():
+    """The packed-operand cache rebuilds for a different tensor object (even
+    with equal contents) and after an in-place update, and not otherwise."""
+    import torch
+    from hanuman_amd.moe import _PackCache
+    builds = []
+    c = _PackCache()
+    a = torch.ones(4)
+    b = torch.zeros(4)
+    c.get((a, b), lambda: builds.append(1) or len(builds))
+    c.get((a, b), lambda: builds.append(1) or len(builds))
+    assert len(builds) == 1
+    a.add_(1.0)
+    c.get((a, b), lambda: builds.append(1) or len(builds))
+    assert len(builds) == 2
+    a2 = a.clone()
+    c.get((a2, b), lambda: builds.append(1) or len(builds))
+    assert len(builds) == 3
+    c.get((a2, b), lambda: builds.append(1) or len(builds))
+    assert len(builds) == 3
