@@ -540,9 +540,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
     a_tile = A + static_cast<int64_t>(r0) * row_bytes;
     b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes;
-    // Rows past the buffer (the last tile of the last segment) are clamped to
-    // its last row; their results are never stored.
-    const int64_t lim = a_rows - 1 - r0;
+    // Rows past the expert's segment are clamped to its last row (repeated
+    // loads of one row hit the caches); their results are never stored.
+    const int64_t lim = row_end - 1 - r0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int rr = i * 32 + ld_r;
@@ -747,7 +747,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     int64_t row0, row_end;
     decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
-    const int64_t lim = a_rows - 1 - r0;
+    // rows past the segment repeat its last row (its token row stays cached)
+    const int64_t lim = row_end - 1 - r0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int rr = i * 32 + ld_r;
@@ -765,9 +766,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes), 0,
         b_tile_bytes, kBufferWord3);
-    // Rows past the buffer (the last tile of the last segment) are clamped to
-    // its last row; their results are never stored.
-    const int64_t lim = a_rows - 1 - r0;
+    // Rows past the expert's segment are clamped to its last row (repeated
+    // loads of one row hit the caches); their results are never stored.
+    const int64_t lim = row_end - 1 - r0;
     if (GATHER) {
       // Row offsets into x from the sources prefetched one tile earlier; rows
       // without a source (-1) read token 0, and a source past the token count
