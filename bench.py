@@ -74,6 +74,8 @@ def algorithmic(wl, kept_rows: int) -> dict:
     # dispatch: read every token once, write the kept rows (+ scales), read the slot map
     w["permute"] = ("hbm", T * D * x_in + kept_rows * (D * ex + (4 if fp8 else 0)) + R * 4,
                     HBM_PEAK_GBS)
+    # fp8 on bf16 tokens: x quantised per token (read once, codes and scales written)
+    w["quant_x"] = ("hbm", T * D * x_in + T * D + T * 4, HBM_PEAK_GBS)
     if wl.expert == "swiglu":
         w["gate_up"] = ("mfma", 2 * 2 * kept_rows * D * F, mfma_peak)
         if fp8:
@@ -186,7 +188,8 @@ def main():
     # bf16 SwiGLU experts: the row permutation is done by the gate/up GEMM's
     # own loads (no dispatched copy of x), so there is no separate stage.
     fused = layer.fused_dispatch
-    stages = ["router", "plan"] + ([] if fused else ["permute"])
+    fp8_gather = layer.fp8_gather
+    stages = ["router", "plan"] + (["quant_x"] if fp8_gather else [] if fused else ["permute"])
     if wl.expert == "swiglu":
         stages += ["gate_up", "quant_h", "down"] if fp8 else ["gate_up", "down"]
     stages += ["combine"]
@@ -205,7 +208,17 @@ def main():
         mark()
         plan = K.dispatch_plan(top_idx, wl.n_experts, layer.capacity, layer.workspace)
         mark()
-        if fp8:
+        if fp8 and fp8_gather:
+            x_q, x_s = K.quantize_rows_fp8(layer.x)
+            mark()
+            h = K.grouped_gate_up_fp8_gather(x_q, x_s, plan, layer.w_gate_up,
+                                             layer.w_gate_up_scale)
+            mark()
+            h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
+            mark()
+            ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, layer.w_down, layer.w_down_scale)
+            mark()
+        elif fp8:
             xs_q, xs_s = K.permute_rows_fp8(layer.x, plan)
             mark()
             h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, layer.w_gate_up, layer.w_gate_up_scale)
@@ -323,7 +336,7 @@ def main():
         # Dominant kernel: the gate/up grouped GEMM with the fused SwiGLU
         # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
-        kname = ("grouped_gemm_dma<true, true>" if fp8
+        kname = (f"grouped_gemm_w8_fp8<true, {'true' if fp8_gather else 'false'}>" if fp8
                  else "grouped_gemm_f32_kernel<1, false>" if wl.expert_dtype == "f32"
                  else f"grouped_gemm_regs<true, {'true' if odd else 'false'}, "
                       f"{'true' if fused else 'false'}, false>")

@@ -59,6 +59,8 @@ SIGNATURES = {
     "hmoe_packed_fp8_down_bytes": (_sz, [_i32, _i32, _i32]),
     "hmoe_pack_fp8_down": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "hmoe_grouped_gate_up_fp8": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_fp8_gather": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32,
+                                               _i32, _vp, _vp, _vp, _vp]),
     "hmoe_grouped_down_fp8": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hmoe_aux_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "hmoe_router_aux": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),

@@ -10,38 +10,38 @@
 // packed columns alternate 32 gate / 32 up columns of the same h columns and
 // the epilogue writes h = bf16(silu(gate) * up).
 //
-// Persistent kernels: one workgroup (4 waves) per CU loops over 256 x 256
-// output tiles.  Tiles are numbered expert by expert (ceil(rows_e / 256)
-// m-tiles each, n fastest); every workgroup computes the numbering from
-// `offsets`, so the launch never depends on the routing.  The tile range is
-// split evenly over the 8 XCDs (workgroup i runs on XCD i % 8) and the
-// workgroups of an XCD stride through their range together, so at any moment
-// an XCD works on a few consecutive m-tiles of one expert and shares their A
-// rows and B columns in its L2.
-//
-// Main loop (per K step of 128 bytes per row: 64 bf16 or 128 e4m3): each
-// wave owns a 128 x 128 quarter of the tile and runs 4 x 16 bf16 MFMAs
-// (v_mfma_f32_32x32x16_bf16) or 2 x 16 fp8 MFMAs per step from the current
-// LDS stage; two stages alternate.  An LDS row holds 128 bytes as eight
-// 16-byte chunks; chunk c of row r is stored at position c ^ lds_swz(r)
-// (lds_swz below: conflict-free fragment reads over the 64 LDS banks).
-//   * bf16 (grouped_gemm_regs): global loads run two K steps ahead into two
-//     register slots (2 x 64 KB per workgroup in flight) and each slot is
-//     written into the other stage during the step before it is used; the
-//     loads, LDS writes and fragment reads of each sub-step are interleaved
-//     between its MFMAs, and a step ends with one barrier that never waits
-//     for global memory.
-//   * fp8 (grouped_gemm_dma): the next step's tiles go straight from global
-//     memory into the other stage (global_load_lds_dwordx4), because the
+// Persistent kernels: one workgroup per CU loops over 256 x 256 output
+// tiles.  Tiles are numbered expert by expert (ceil(rows_e / 256) m-tiles
+// each, n fastest); every workgroup computes the numbering from `offsets`,
+// so the launch never depends on the routing.  The tile range is split
+// evenly over the 8 XCDs (workgroup i runs on XCD i % 8) and the workgroups
+// of an XCD stride through their range together, so at any moment an XCD
+// works on a few consecutive m-tiles of one expert and shares their A rows
+// and B columns in its L2.  The load side runs on into the next tile, so the
+// pipeline does not drain between tiles.
+//   * bf16 (grouped_gemm_regs, 4 waves, each a 128 x 128 quarter of the
+//     tile): a K step is 64 values = 128 bytes of every A and B row, 4 x 16
+//     v_mfma_f32_32x32x16_bf16 per wave from the current LDS stage; two
+//     stages alternate.  An LDS row holds 128 bytes as eight 16-byte chunks;
+//     chunk c of row r is stored at position c ^ lds_swz(r) (conflict-free
+//     fragment reads over the 64 LDS banks).  Global loads run two K steps
+//     ahead into two register slots (2 x 64 KB per workgroup in flight) and
+//     each slot is written into the other stage during the step before it is
+//     used; the loads, LDS writes and fragment reads of each sub-step are
+//     interleaved between its MFMAs, and a step ends with one barrier that
+//     never waits for global memory.
+//   * e4m3 (grouped_gemm_w8_fp8, 8 waves = 2 per SIMD, each a 128 x 64 block):
+//     a K step is 64 values = 64 bytes per row, one 32x32x64 fp8 MFMA per
+//     fragment pair; the tiles go straight from global memory into a ring of
+//     four LDS stages (buffer_load ... lds, three steps ahead), because the
 //     32-byte fp8 fragments leave no registers for load staging.
-// The load side runs on into the next tile, so the pipeline does not drain
-// between tiles.
 #include <atomic>
 
 #include "hmoe_common.h"
 
 namespace hmoe {
 namespace {
+
 
 constexpr int kBM = HMOE_GEMM_TILE_M;
 constexpr int kBN = 256;
@@ -150,8 +150,7 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // Element-type traits: bf16 (32x32x16 MFMA, 64 elements = 128 bytes per LDS
 // row per K step, 4 sub-steps) or OCP e4m3 (32x32x64 MFMA at unit block
-// scales, 128 elements per K step, 2 sub-steps).  Either way a K step moves
-// 128 bytes of every A and B row, so the LDS layout and the DMA are the same.
+// scales; its fragments are read by grouped_gemm_w8_fp8 itself).
 template <bool FP8>
 struct GemmElem;
 template <>
@@ -169,92 +168,12 @@ struct GemmElem<false> {
 };
 template <>
 struct GemmElem<true> {
-  static constexpr int kBytes = 1;
-  static constexpr int kSub = 2;
   typedef i32x8 frag_t;
-  // Lane L, sub-step s: row L&31, 32 bytes = chunks 4s + 2(L/32) and the next.
-  __device__ static frag_t read(const uint8_t* base, int row_byte, int row, int s, int half) {
-    const int c0 = 4 * s + 2 * half;
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(base + row_byte + ((c0 ^ lds_swz(row)) * 16));
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(base + row_byte + (((c0 + 1) ^ lds_swz(row)) * 16));
-    frag_t f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[i] = static_cast<int>(lo[i]);
-      f[4 + i] = static_cast<int>(hi[i]);
-    }
-    return f;
-  }
   __device__ static f32x16 mfma(const frag_t& b, const frag_t& a, const f32x16& c) {
     // Format 0 = e4m3 for both operands; E8M0 block scales 127 = 1.0.
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 127, 0, 127);
   }
 };
-
-// Epilogue of one tile: acc[i][j] lane L, element r is token row
-// wm*128 + i*32 + (L&31) and column wn*128 + j*32 + (r/4)*8 + (L/32)*4 + r%4.
-// With FP8 the accumulators are dequantised by the row and column scales;
-// with SWIGLU the gate/up column pairs become h = bf16(silu(gate) * up).
-template <bool SWIGLU, bool FP8>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], uint16_t* __restrict__ C,
-                                           int64_t ldc, const float* __restrict__ a_scale,
-                                           const float* __restrict__ b_scale, int ncols, int e,
-                                           int64_t row0, int64_t row_end, int n0, int wm, int wn,
-                                           int lane) {
-  const int frow = lane & 31;
-  const int col_lane = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + wm * 128 + i * 32 + frow;
-    if (row < row_end) {
-      uint16_t* crow = C + row * ldc;
-      const float sa = FP8 ? a_scale[row] : 1.0f;
-      const float* sb = FP8 ? b_scale + static_cast<int64_t>(e) * ncols + n0 + wn * 128 + col_lane : nullptr;
-      if (SWIGLU) {
-        const int hbase = (n0 + wn * 128) / 2;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float h[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float gv = acc[i][2 * p][g * 4 + q];
-              float uv = acc[i][2 * p + 1][g * 4 + q];
-              if (FP8) {
-                gv = gv * sa * sb[(2 * p) * 32 + g * 8 + q];
-                uv = uv * sa * sb[(2 * p + 1) * 32 + g * 8 + q];
-              }
-              h[q] = swiglu_bf16_points(gv, uv);
-            }
-            uint2 pk;
-            pk.x = pack_bf16x2_rne(h[0], h[1]);
-            pk.y = pack_bf16x2_rne(h[2], h[3]);
-            *reinterpret_cast<uint2*>(crow + hbase + p * 32 + g * 8 + col_lane) = pk;
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float v[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              v[q] = acc[i][j][g * 4 + q];
-              if (FP8) v[q] = v[q] * sa * sb[j * 32 + g * 8 + q];
-            }
-            uint2 pk;
-            pk.x = pack_bf16x2_rne(v[0], v[1]);
-            pk.y = pack_bf16x2_rne(v[2], v[3]);
-            *reinterpret_cast<uint2*>(crow + n0 + wn * 128 + j * 32 + g * 8 + col_lane) = pk;
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
 
 // Workgroup barrier that waits for this wave's LDS operations only.  Global
 // loads in flight stay in flight: their results land in registers, and the
@@ -272,17 +191,12 @@ __device__ __forceinline__ void barrier_lds() {
 // rather than by a branch.  The barriers wait for LDS operations only: the
 // stores stay in flight while the next tile starts.
 
-// FP8: the accumulators are dequantised first, acc * s_row * s_col, with the
-// tile's 256 row scales at ssc[0..255] and 256 column scales at ssc[256..511]
-// (LDS).
-
 // Without SwiGLU (the down GEMM): 512-byte rows, so the 256 x 256 tile goes in
 // two passes of 128 rows (rows i = 2q, 2q+1 of every wave in pass q).
-template <bool FP8>
 __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_t* lds,
                                                uint16_t* __restrict__ C, int64_t ldc, int64_t row0,
                                                int64_t row_end, int n0, int wm, int wn, int lane,
-                                               int tid, const float* ssc) {
+                                               int tid) {
   const int frow = lane & 31;
   const int half = lane >> 5;
   const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
@@ -299,7 +213,6 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_
     for (int ii = 0; ii < 2; ++ii) {
       const int i = 2 * q + ii;
       const int l = wm * 64 + ii * 32 + frow;
-      const float sa = FP8 ? ssc[wm * 128 + i * 32 + frow] : 1.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -307,12 +220,6 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] = acc[i][j][g * 4 + r];
-          if (FP8) {
-            const f32x4 sb =
-                *reinterpret_cast<const f32x4*>(ssc + kBM + wn * 128 + j * 32 + g * 8 + half * 4);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = v[r] * sa * sb[r];
-          }
           uint2 pk;
           pk.x = pack_bf16x2_rne(v[0], v[1]);
           pk.y = pack_bf16x2_rne(v[2], v[3]);
@@ -338,11 +245,10 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint8_
 // gate/up column blocks is half the tile's columns, 256-byte rows, so the
 // whole tile fits the stage in one pass.  LDS row l = tile row l, 16 chunks of
 // 8 h values; chunk c of row l at position c ^ (l & 15).
-template <bool FP8>
 __device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4], uint8_t* lds,
                                                       uint16_t* __restrict__ C, int64_t ldc,
                                                       int64_t row0, int64_t row_end, int n0, int wm,
-                                                      int wn, int lane, int tid, const float* ssc) {
+                                                      int wn, int lane, int tid) {
   const int frow = lane & 31;
   const int half = lane >> 5;
   const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
@@ -352,28 +258,14 @@ __device__ __forceinline__ void store_tile_lds_swiglu(const f32x16 (&acc)[4][4],
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int l = wm * 128 + i * 32 + frow;
-    const float sa = FP8 ? ssc[l] : 1.0f;
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float h[4];
-        f32x4 sg, su;
-        if (FP8) {
-          sg = *reinterpret_cast<const f32x4*>(ssc + kBM + wn * 128 + 2 * p * 32 + g * 8 + half * 4);
-          su = *reinterpret_cast<const f32x4*>(ssc + kBM + wn * 128 + (2 * p + 1) * 32 + g * 8 +
-                                               half * 4);
-        }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float gv = acc[i][2 * p][g * 4 + q];
-          float uv = acc[i][2 * p + 1][g * 4 + q];
-          if (FP8) {
-            gv = gv * sa * sg[q];
-            uv = uv * sa * su[q];
-          }
-          h[q] = swiglu_bf16_points(gv, uv);
-        }
+        for (int q = 0; q < 4; ++q)
+          h[q] = swiglu_bf16_points(acc[i][2 * p][g * 4 + q], acc[i][2 * p + 1][g * 4 + q]);
         uint2 pk;
         pk.x = pack_bf16x2_rne(h[0], h[1]);
         pk.y = pack_bf16x2_rne(h[2], h[3]);
@@ -479,37 +371,69 @@ __device__ __forceinline__ void store_tile_lds_dswiglu(const f32x16 (&acc)[4][4]
   }
 }
 
-// Main loop with direct global -> LDS loads (used for the e4m3 operands,
-// whose 32-byte MFMA fragments leave no registers for load staging): the next
-// K step's A and B tiles (2 x 32 KB) go straight into the other LDS stage with
-// global_load_lds_dwordx4 while the current stage feeds the MFMAs; fragments
-// are double-buffered in registers and each sub-step's LDS reads and DMA
-// issues go out before its MFMAs.  With FP8, a_scale [a_rows] and b_scale
-// [n_experts * ncols] dequantise the float32 accumulators in the epilogue.
-template <bool SWIGLU, bool FP8>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+// ---- eight-wave e4m3 kernel ------------------------------------------------------
+// The e4m3 grouped GEMM with two waves per SIMD.  One workgroup of 8 waves
+// per CU loops over 256 x 256 tiles as grouped_gemm_regs does, each wave
+// owning a 128 x 64 block (4 x 2 fragments, 128 accumulator registers), so
+// that while one wave of a SIMD waits on LDS or a barrier the other keeps the
+// matrix core busy: with one wave per SIMD a CU draws ~67 B/clk of fragments
+// from LDS, with two ~170 B/clk, and the 256 x 256 tile's MFMAs need ~100.
+// A K step is 64 bytes of every A and B row (64 e4m3 values: one
+// v_mfma_scale_f32_32x32x64_f8f6f4 per fragment pair).  Four LDS stages of
+// 32 KB hold steps g .. g+3; the tiles go straight from global memory into
+// the stage of step g + 3 (buffer_load ... lds), the fragments of step g + 1
+// are read during step g (its stage completed at the previous barrier), and
+// the step ends with one barrier after which step g + 2 is complete.  The
+// tile's 256 row and 256 column scales are staged in LDS for the epilogue,
+// which dequantises (acc * s_row * s_col) and stores straight from the
+// accumulators.  GATHER: A is the per-token e4m3 matrix of x and row r of
+// the dispatched operand is its token perm_src[r] / top_k, whose scale is
+// the row scale (rows without a source read token 0).
+constexpr int kW8Threads = 512;
+constexpr int kW8StepBytes = 64;
+constexpr int kW8Stages = 4;
+constexpr int kW8StageBytes = 2 * kBM * kW8StepBytes;  // A 16 KB | B 16 KB
+constexpr int kW8Lds = kW8Stages * kW8StageBytes;       // 128 KB
+static_assert(kW8Lds <= 2 * kStageBytes, "allow_dynamic_lds grants 2 * kStageBytes");
+
+// 64-byte LDS rows: chunk c of row r sits at c ^ swz64(r), so the 16 lanes
+// of a fragment read served together (rows r .. r + 15) cover the 16
+// different 16-byte bank groups of the 256-byte bank space.
+__device__ __forceinline__ int swz64(int r) { return (r >> 2) & 3; }
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), expcnt left alone (gfx9 encoding: vmcnt bits
+// 0..3 and 14..15).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+}
+
+template <bool SWIGLU, bool GATHER>
+__global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
     const float* __restrict__ a_scale, const float* __restrict__ b_scale,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
-    uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n) {
-  typedef GemmElem<FP8> E;
-  // The two stages live in dynamic LDS.  With a static array the compiler
-  // cannot tell the stage being loaded from the stage being read and waits
-  // for every DMA load before the next LDS read; the stage protocol below
-  // (DMA into stage cur^1, read stage cur, vmcnt(0) + barrier at the end of
-  // each K step) already orders them.
+    uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n, const int32_t* __restrict__ gather_src,
+    int gather_k, int gather_rows) {
+  typedef GemmElem<true> E;
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int32_t tstart[kMaxExperts + 1];
-  __shared__ int32_t scan_tmp[kThreads];
-  // FP8: the current tile's row scales [0, 256) and column scales [256, 512)
-  __shared__ __attribute__((aligned(16))) float sscale[FP8 ? 2 * kBM : 4];
+  __shared__ int32_t scan_tmp[kW8Threads];
+  __shared__ __attribute__((aligned(16))) float sscale[2 * kBM];  // rows | columns
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const int total =
-      __builtin_amdgcn_readfirstlane(scan_tiles(offsets, n_experts, tstart, scan_tmp) * n_tiles_n);
+  const int total = __builtin_amdgcn_readfirstlane(
+      scan_tiles<kW8Threads>(offsets, n_experts, tstart, scan_tmp) * n_tiles_n);
   const int xcd = blockIdx.x % kNumXcd;
   const int per_xcd = gridDim.x / kNumXcd;
   const int slot = blockIdx.x / kNumXcd;
@@ -517,164 +441,278 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma(
   const int hi = static_cast<int>((static_cast<int64_t>(total) * (xcd + 1)) / kNumXcd);
   const int first = lo + slot;
   if (first >= hi) return;  // uniform per workgroup
-  const int row_bytes = kdim * E::kBytes;
-  const int ksteps = row_bytes / 128;
+  const int row_bytes = kdim;  // one byte per value
+  const int ks = row_bytes / kW8StepBytes;  // even: kdim % 128 == 0
+  const int n_my = (hi - first + per_xcd - 1) / per_xcd;
+  const int iters = n_my * ks;
 
-  // ---- global -> LDS loads ------------------------------------------------
-  // Round i (0..7) of a stage: this thread fills 16-byte slot i*256 + tid,
-  // i.e. row i*32 + tid/8 at position tid&7, which holds chunk
-  // (tid&7) ^ (row&7) = (tid&7) ^ ((tid>>3)&7).  One wave instruction writes
-  // 1 KB of contiguous LDS.
-  const int ld_r = tid >> 3;
-  const int ld_c = (tid & 7) ^ lds_swz(ld_r);
-  const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
-  uint32_t a_off[8];
-  const uint8_t* a_tile = A;
-  const uint8_t* b_tile = B;
-  auto set_load_tile = [&](int t) {
+  // ---- global -> LDS (DMA) ---------------------------------------------------
+  // Instruction j (0, 1) of wave w fills rows 32 w + 16 j + lane / 4 of the A
+  // and of the B stage (1 KB of contiguous LDS each); lane position lane & 3
+  // receives chunk (lane & 3) ^ swz64(row) = (lane & 3) ^ ((lane >> 4) & 3).
+  const int dma_row = wave * 32 + (lane >> 2);  // + 16 j
+  const int dma_byte = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
+  const int tile_bytes = kBM * row_bytes;
+  __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(A), 0, GATHER ? gather_rows * row_bytes : tile_bytes, kBufferWord3);
+  __amdgpu_buffer_rsrc_t b_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, tile_bytes, kBufferWord3);
+  const uint32_t b_voff0 = static_cast<uint32_t>(dma_row * row_bytes + dma_byte);
+  uint32_t a_voff[2];
+  int ld_kb = 0, ld_g = 0, ld_t = first;
+  int32_t pf_src[2];  // GATHER: sources of this lane's rows in the next tile
+  auto fetch_src = [&](int t) __attribute__((always_inline)) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
+    const int64_t lim = row_end - 1 - r0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int rr = dma_row + 16 * j;
+      rr = rr < lim ? rr : static_cast<int>(lim);
+      pf_src[j] = gather_src[r0 + rr];
+    }
+  };
+  auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
     decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
-    a_tile = A + static_cast<int64_t>(r0) * row_bytes;
-    b_tile = B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes;
-    // Rows past the expert's segment are clamped to its last row (repeated
-    // loads of one row hit the caches); their results are never stored.
-    const int64_t lim = row_end - 1 - r0;
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes), 0,
+        tile_bytes, kBufferWord3);
+    if (GATHER) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int rr = i * 32 + ld_r;
-      rr = rr < lim ? rr : static_cast<int>(lim);
-      a_off[i] = static_cast<uint32_t>(rr * row_bytes + ld_c * 16);
+      for (int j = 0; j < 2; ++j) {
+        int tk = pf_src[j] >= 0 ? pf_src[j] / gather_k : 0;
+        tk = tk < gather_rows ? tk : gather_rows - 1;
+        a_voff[j] = static_cast<uint32_t>(tk) * static_cast<uint32_t>(row_bytes) +
+                    static_cast<uint32_t>(dma_byte);
+      }
+      if (t + per_xcd < hi) fetch_src(t + per_xcd);
+    } else {
+      // rows past the segment repeat its last row; their results are never stored
+      a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(A + static_cast<int64_t>(r0) * row_bytes), 0, tile_bytes,
+          kBufferWord3);
+      const int64_t lim = row_end - 1 - r0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        int rr = dma_row + 16 * j;
+        rr = rr < lim ? rr : static_cast<int>(lim);
+        a_voff[j] = static_cast<uint32_t>(rr * row_bytes + dma_byte);
+      }
     }
   };
-  // Part p (0..3) issues rounds 2p and 2p+1 of A and of B for K step kb.
-  auto issue_loads = [&](int stage, int kb, int part) {
-    uint8_t* base = smem + stage * kStageBytes;
-    const uint8_t* ab = a_tile + kb * 128;
-    const uint8_t* bb = b_tile + kb * 128;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = part * 2 + q;
-      __builtin_amdgcn_global_load_lds(ab + a_off[i], (lds_ptr_t)(base + i * 4096 + wave * 1024),
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds(bb + b_off0 + static_cast<uint32_t>(i * 32 * row_bytes),
-                                       (lds_ptr_t)(base + 32768 + i * 4096 + wave * 1024), 16, 0,
-                                       0);
+  auto issue_dma = [&](int stage, int j) __attribute__((always_inline)) {
+    uint8_t* base = smem + stage * kW8StageBytes + (2 * wave + j) * 1024;
+    const int koff = ld_kb * kW8StepBytes;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)base, 16, a_voff[j], koff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kBM * kW8StepBytes), 16,
+                                             b_voff0 + static_cast<uint32_t>(16 * j * row_bytes),
+                                             koff, 0, 0);
+  };
+  // Once every step is loaded the load side repeats the last one (into a
+  // stage nothing reads), so every step issues the same DMA count.
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (ld_g + 1 < iters) {
+      ++ld_g;
+      if (++ld_kb == ks) {
+        ld_kb = 0;
+        ld_t += per_xcd;
+        set_load_tile(ld_t);
+      }
     }
   };
 
-  // ---- MFMA fragments -------------------------------------------------------
-  // The weight fragment is the first MFMA operand, so an accumulator lane
-  // holds one token row and groups of four consecutive output columns.
-  // Fragment i of the wave's 128 rows is 32 rows (4096 bytes) further down.
-  const int wm = wave >> 1, wn = wave & 1;
+  // ---- MFMA fragments ------------------------------------------------------
+  // Wave w: rows 128 (w & 1) .. +128, columns 64 (w >> 1) .. +64 of the tile.
+  // Lane L: row L & 31 of each 32-row fragment, bytes 32 (L / 32) .. + 32 of
+  // the step (chunks 2 (L / 32) and 2 (L / 32) + 1).
+  const int wm = wave & 1, wn = wave >> 1;
   const int frow = lane & 31;
   const int fhalf = lane >> 5;
-  const int fa_row = wm * 128 + frow;
-  const int fb_row = wn * 128 + frow;
-  typename E::frag_t fa[2][4], fb[2][4];
-  auto read_frags = [&](int buf, int stage, int s) {
-    const uint8_t* base = smem + stage * kStageBytes;
+  const int fsw = swz64(frow);
+  const int p0 = ((2 * fhalf) ^ fsw) * 16, p1 = ((2 * fhalf + 1) ^ fsw) * 16;
+  const int fa_off = (wm * 128 + frow) * kW8StepBytes;
+  const int fb_off = kBM * kW8StepBytes + (wn * 64 + frow) * kW8StepBytes;
+  E::frag_t fa[2][4], fb[2][2];
+  auto read_frag = [&](const uint8_t* row) __attribute__((always_inline)) {
+    const u32x4 lo4 = *reinterpret_cast<const u32x4*>(row + p0);
+    const u32x4 hi4 = *reinterpret_cast<const u32x4*>(row + p1);
+    E::frag_t f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[buf][i] = E::read(base, (fa_row + 32 * i) * 128, fa_row, s, fhalf);
-      fb[buf][i] = E::read(base + 32768, (fb_row + 32 * i) * 128, fb_row, s, fhalf);
+    for (int q = 0; q < 4; ++q) {
+      f[q] = static_cast<int>(lo4[q]);
+      f[4 + q] = static_cast<int>(hi4[q]);
     }
+    return f;
   };
-  f32x16 acc[4][4];
+  auto read_frags = [&](auto Bc, int stage) __attribute__((always_inline)) {
+    constexpr int b = decltype(Bc)::value;
+    const uint8_t* base = smem + stage * kW8StageBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[b][i] = read_frag(base + fa_off + i * 32 * kW8StepBytes);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[b][j] = read_frag(base + fb_off + j * 32 * kW8StepBytes);
+  };
+  f32x16 acc[4][2];
 
-  // One K step on stage `cur`: loads for the next step into stage cur^1 (when
-  // `load`; the four load parts are spread over the sub-steps), fragment
-  // double-buffering, 64 (bf16) or 32 (fp8) MFMAs, then a barrier (which also
-  // waits for this thread's DMA loads).
-  int cur = 0;
-  auto kstep = [&](bool load, int ld_kb) {
+  // Step g on fragment buffer B = g & 1: DMA of step g + 3, fragments of step
+  // g + 1 into buffer B ^ 1, the MFMAs of step g, one barrier.
+  auto step = [&](auto Bc, int g, auto Wc) __attribute__((always_inline)) {
+    constexpr int b = decltype(Bc)::value;
 #pragma unroll
-    for (int s = 0; s < E::kSub; ++s) {
-      if (load) {
-        if (E::kSub == 4) {
-          issue_loads(cur ^ 1, ld_kb, s);
-        } else {
-          issue_loads(cur ^ 1, ld_kb, 2 * s);
-          issue_loads(cur ^ 1, ld_kb, 2 * s + 1);
-        }
-      }
-      if (s + 1 < E::kSub) read_frags((s + 1) & 1, cur, s + 1);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < 2; ++j) issue_dma((g + 3) & 3, j);
+    advance();
+    read_frags(IntC<b ^ 1>{}, (g + 1) & 3);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < 2; ++j) acc[i][j] = E::mfma(fb[b][j], fa[b][i], acc[i][j]);
+    // per MFMA: a DMA or fragment reads
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // DMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS read
     }
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's DMA of step g + 2 landed (step g + 3's four may still fly);
+    // after the barrier every wave's has
+    wait_vm_lgkm0<decltype(Wc)::value>();
+    __builtin_amdgcn_s_barrier();
   };
 
+  // Prologue: steps 0, 1, 2 into stages 0, 1, 2; steps 0 and 1 complete.
+  if (GATHER) fetch_src(first);
   set_load_tile(first);
 #pragma unroll
-  for (int part = 0; part < 4; ++part) issue_loads(0, 0, part);
-  __syncthreads();
-  read_frags(0, 0, 0);
+  for (int st = 0; st < 3; ++st) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) issue_dma(st, j);
+    advance();
+  }
+  wait_vm_lgkm0<4>();
+  __builtin_amdgcn_s_barrier();
+  read_frags(IntC<0>{}, 0);
 
+  // GATHER: the source of tile row tid (tid < 256) of the current tile,
+  // loaded one tile ahead so that the scale lookup never waits on it
+  auto row_src = [&](int t) __attribute__((always_inline)) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    return gather_src[row0 + tid < row_end ? row0 + tid : row_end - 1];
+  };
+  int32_t my_src = 0;
+  if (GATHER && tid < kBM) my_src = row_src(first);
+
+  int g = 0;
   for (int t = first; t < hi; t += per_xcd) {
-    // FP8 with SwiGLU: this thread's row and column scale of the tile (rows
-    // past the buffer clamped), loaded now and written to LDS after the K loop
-    float sa_own = 0.0f, sb_own = 0.0f;
-    if (FP8 && SWIGLU) {
-      int e, n0;
-      int64_t row0, row_end;
-      decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
-      const int64_t r = row0 + tid < a_rows ? row0 + tid : a_rows - 1;
-      sa_own = a_scale[r];
-      sb_own = b_scale[static_cast<int64_t>(e) * ncols + n0 + tid];
+    int e, n0;
+    int64_t row0, row_end;
+    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    // this thread's row scale (tid < 256) or column scale (tid >= 256) of the
+    // tile, loaded now and staged in LDS after the K loop
+    float my_scale;
+    if (tid < kBM) {
+      if (GATHER) {
+        int tk = my_src >= 0 ? my_src / gather_k : 0;
+        tk = tk < gather_rows ? tk : gather_rows - 1;
+        my_scale = a_scale[tk];
+        if (t + per_xcd < hi) my_src = row_src(t + per_xcd);
+      } else {
+        my_scale = a_scale[row0 + tid < row_end ? row0 + tid : row_end - 1];
+      }
+    } else {
+      my_scale = b_scale[static_cast<int64_t>(e) * ncols + n0 + tid - kBM];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    for (int kb = 0; kb + 1 < ksteps; ++kb) {
-      kstep(true, kb + 1);
-      read_frags(0, cur ^ 1, 0);
-      cur ^= 1;
+    for (int kb = 0; kb < ks; kb += 2, g += 2) {
+      step(IntC<0>{}, g, IntC<4>{});
+      step(IntC<1>{}, g + 1, IntC<4>{});
     }
-    const bool next = t + per_xcd < hi;
-    if (next) set_load_tile(t + per_xcd);
-    kstep(next, 0);
-
-    int e, n0;
-    int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
-    if constexpr (SWIGLU) {
-      if (FP8) {
-        // the previous tile's epilogue read sscale before its last barrier
-        sscale[tid] = sa_own;
-        sscale[kBM + tid] = sb_own;
-        barrier_lds();
+    // the previous tile's epilogue read sscale before this tile's barriers
+    sscale[tid] = my_scale;
+    barrier_lds();
+    // Epilogue: lane L of acc[i][j] holds tile row 128 wm + 32 i + L % 32 and
+    // columns 64 wn + 32 j + 8 q + 4 (L / 32) + 0..3 (q = 0..3).  Each 32-column
+    // block is packed to bf16 (d[2q], d[2q + 1] = the 4 values of group q) and
+    // lanes L and L + 32 trade groups (v_permlane32_swap: lanes 32..63 of the
+    // first operand with lanes 0..31 of the second), after which lane L < 32
+    // holds columns 0..7 and 16..23 and lane L + 32 columns 8..15 and 24..31
+    // of its row: two 16-byte stores per block, each writing 32 contiguous
+    // bytes of every row.
+    const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
+    const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
+    auto store_block = [&](uint32_t (&d)[8], int r, int col) __attribute__((always_inline)) {
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const auto p01 = __builtin_amdgcn_permlane32_swap(d[w], d[2 + w], false, false);
+        d[w] = p01[0];
+        d[2 + w] = p01[1];
+        const auto p23 = __builtin_amdgcn_permlane32_swap(d[4 + w], d[6 + w], false, false);
+        d[4 + w] = p23[0];
+        d[6 + w] = p23[1];
       }
-      // Stage cur is idle here: the last step read it and the next tile's
-      // loads go into it only after the epilogue's last barrier.
-      store_tile_lds_swiglu<FP8>(acc, smem + cur * kStageBytes, C, ldc, row0, row_end, n0, wm, wn,
-                                 lane, tid, sscale);
-    } else {
-      // direct stores measured faster than LDS staging for this kernel's
-      // 256-column tiles
-      store_tile<false, FP8>(acc, C, ldc, a_scale, b_scale, ncols, e, row0, row_end, n0, wm, wn,
-                             lane);
+      const int off = static_cast<int>((r * ldc + col + fhalf * 8) * 2);
+      const u32x4 lo4 = {d[0], d[1], d[2], d[3]};
+      const u32x4 hi4 = {d[4], d[5], d[6], d[7]};
+      __builtin_amdgcn_raw_buffer_store_b128(lo4, c_rsrc, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(hi4, c_rsrc, off + 32, 0, 0);
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 128 + i * 32 + frow;
+      const float sa = sscale[r];
+      if (SWIGLU) {
+        // gate columns in acc[i][0], the up columns of the same h columns in acc[i][1]
+        uint32_t d[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 sg = *reinterpret_cast<const f32x4*>(sscale + kBM + wn * 64 + q * 8 + fhalf * 4);
+          const f32x4 su =
+              *reinterpret_cast<const f32x4*>(sscale + kBM + wn * 64 + 32 + q * 8 + fhalf * 4);
+          float h[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            h[k] = swiglu_bf16_points(acc[i][0][q * 4 + k] * sa * sg[k],
+                                      acc[i][1][q * 4 + k] * sa * su[k]);
+          d[2 * q] = pack_bf16x2_rne(h[0], h[1]);
+          d[2 * q + 1] = pack_bf16x2_rne(h[2], h[3]);
+        }
+        store_block(d, r, n0 / 2 + wn * 32);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          uint32_t d[8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 sb =
+                *reinterpret_cast<const f32x4*>(sscale + kBM + wn * 64 + j * 32 + q * 8 + fhalf * 4);
+            d[2 * q] = pack_bf16x2_rne(acc[i][j][q * 4] * sa * sb[0], acc[i][j][q * 4 + 1] * sa * sb[1]);
+            d[2 * q + 1] =
+                pack_bf16x2_rne(acc[i][j][q * 4 + 2] * sa * sb[2], acc[i][j][q * 4 + 3] * sa * sb[3]);
+          }
+          store_block(d, r, n0 + wn * 64 + j * 32);
+        }
+      }
     }
-    if (next) read_frags(0, cur ^ 1, 0);
-    cur ^= 1;
   }
+  // nothing may still be writing into LDS when the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
 }
-
-template <int V>
-struct IntC {
-  static constexpr int value = V;
-};
 
 // Main loop with register-staged loads (bf16): global loads run two K steps
 // ahead of the MFMAs.  ODD: the K dimension has an odd number of 64-element
@@ -934,11 +972,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
       store_tile_lds_dswiglu(acc, smem + kStageBytes, C, ldc, dh, row0, row_end, n0, wm, wn, lane,
                              tid);
     else if constexpr (SWIGLU)
-      store_tile_lds_swiglu<false>(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane,
-                                   tid, nullptr);
+      store_tile_lds_swiglu(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
     else
-      store_tile_lds<false>(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid,
-                            nullptr);
+      store_tile_lds(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
     if (g < iters) read_frags(0, 0, 0);
   }
 }
@@ -1221,10 +1257,11 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, false, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<false, false, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, true, true>),
-      reinterpret_cast<const void*>(grouped_gemm_dma<true, true>),
-      reinterpret_cast<const void*>(grouped_gemm_dma<false, true>),
       reinterpret_cast<const void*>(grouped_gemm_wgrad<false>),
       reinterpret_cast<const void*>(grouped_gemm_wgrad<true>),
+      reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, false>),
+      reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, true>),
+      reinterpret_cast<const void*>(grouped_gemm_w8_fp8<false, false>),
   };
   bool ok = true;
   for (const void* k : kernels) ok = ok && set_lds_limit(k, bytes);
@@ -1259,12 +1296,19 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
   uint16_t* c = static_cast<uint16_t*>(C);
   const bool odd = ((static_cast<int64_t>(kdim) * (fp8 ? 1 : 2) / 128) & 1) != 0;
   if (fp8) {
-    if (swiglu)
-      hipLaunchKernelGGL((grouped_gemm_dma<true, true>), dim3(grid), dim3(kThreads), lds, s, a, b,
-                         a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n);
-    else
-      hipLaunchKernelGGL((grouped_gemm_dma<false, true>), dim3(grid), dim3(kThreads), lds, s, a, b,
-                         a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc, n_tiles_n);
+    HMOE_REQUIRE(kdim % (2 * kW8StepBytes) == 0,
+                 "%s: reduction dimension must be a multiple of %d", what, 2 * kW8StepBytes);
+    HMOE_REQUIRE(static_cast<int64_t>(gather_rows) * kdim < (int64_t(1) << 31),
+                 "%s: gathered matrix too large", what);
+#define HMOE_LAUNCH_W8(SW, GA)                                                                    \
+  hipLaunchKernelGGL((grouped_gemm_w8_fp8<SW, GA>), dim3(grid), dim3(kW8Threads), kW8Lds, s, a,  \
+                     b, a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc,        \
+                     n_tiles_n, gather_src, gather_k, gather_rows)
+    HMOE_REQUIRE(swiglu || gather_src == nullptr, "%s: the fp8 down GEMM does not gather", what);
+    if (swiglu && gather_src != nullptr) HMOE_LAUNCH_W8(true, true);
+    else if (swiglu) HMOE_LAUNCH_W8(true, false);
+    else HMOE_LAUNCH_W8(false, false);
+#undef HMOE_LAUNCH_W8
   } else {
 #define HMOE_LAUNCH_REGS(SW, OD, GA, ...)                                                         \
   hipLaunchKernelGGL((grouped_gemm_regs<SW, OD, GA, ##__VA_ARGS__>), dim3(grid), dim3(kThreads),   \
@@ -1513,6 +1557,35 @@ extern "C" int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_sca
   return launch_grouped(true, true, xs_q, w_packed, xs_scale, w_scales, offsets, n_experts,
                         rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
                         "hmoe_grouped_gate_up_fp8");
+}
+
+extern "C" int hmoe_grouped_gate_up_fp8_gather(const uint8_t* x_q, const float* x_scale,
+                                               int64_t tokens, int top_k, const int32_t* perm_src,
+                                               const int32_t* offsets, int n_experts,
+                                               int64_t rows_cap, int d_model, int d_ff,
+                                               const uint8_t* w_packed, const float* w_scales,
+                                               void* h, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "grouped_gate_up_fp8_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
+               n_experts);
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
+               "grouped_gate_up_fp8_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE_CODE(d_model % 128 == 0 && d_model >= 128, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_fp8_gather: d_model must be a multiple of 128 (got %d)",
+                    d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "grouped_gate_up_fp8_gather: d_ff must be a multiple of %d (got %d)", kBN / 2,
+                    d_ff);
+  HMOE_REQUIRE(tokens * d_model < (int64_t(1) << 31),
+               "grouped_gate_up_fp8_gather: x_q must be smaller than 2 GiB");
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(x_q && x_scale && perm_src && offsets && w_packed && w_scales && h,
+               "grouped_gate_up_fp8_gather: null pointer argument");
+  return launch_grouped(true, true, x_q, w_packed, x_scale, w_scales, offsets, n_experts,
+                        rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
+                        "hmoe_grouped_gate_up_fp8_gather", perm_src, top_k,
+                        static_cast<int>(tokens));
 }
 
 extern "C" int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale,

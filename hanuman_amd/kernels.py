@@ -447,6 +447,28 @@ def grouped_gate_up_fp8(xs_q: torch.Tensor, xs_scale: torch.Tensor, offsets: tor
     return h
 
 
+def grouped_gate_up_fp8_gather(x_q: torch.Tensor, x_scale: torch.Tensor, plan: Plan,
+                               w_packed: torch.Tensor, w_scales: torch.Tensor) -> torch.Tensor:
+    """``h`` of :func:`grouped_gate_up_fp8` with the row permutation done by the
+    GEMM's loads: ``x_q, x_scale`` are the per-token codes and scales of ``x``
+    (:func:`quantize_rows_fp8` of ``x``) and row ``r`` of the dispatched operand
+    is token ``perm_src[r] // K`` (bit-identical to the permuted path)."""
+    for t, n in ((x_q, "x_q"), (x_scale, "x_scale"), (w_packed, "w_packed"),
+                 (w_scales, "w_scales")):
+        _check(t, n)
+    N, F2, D = w_packed.shape
+    T = x_q.shape[0]
+    if (x_q.dtype != torch.uint8 or w_packed.dtype != torch.uint8 or x_q.shape[1] != D
+            or x_scale.numel() != T or tuple(w_scales.shape) != (N, F2)
+            or plan.n_experts != N or plan.slot_pos.numel() != T * plan.top_k):
+        raise ValueError("grouped_gate_up_fp8_gather: inconsistent shapes or dtypes")
+    h = torch.empty((plan.rows_cap, F2 // 2), dtype=torch.bfloat16, device=x_q.device)
+    call("hmoe_grouped_gate_up_fp8_gather", _ptr(x_q), _ptr(x_scale), T, plan.top_k,
+         _ptr(plan.perm_src), _ptr(plan.offsets), N, plan.rows_cap, D, F2 // 2, _ptr(w_packed),
+         _ptr(w_scales), _ptr(h), _stream())
+    return h
+
+
 def grouped_down_fp8(h_q: torch.Tensor, h_scale: torch.Tensor, offsets: torch.Tensor,
                      w_packed: torch.Tensor, w_scales: torch.Tensor) -> torch.Tensor:
     """bf16 ``ys`` of the fp8 down GEMM (dequantised)."""

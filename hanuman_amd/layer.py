@@ -4,7 +4,8 @@
 and runs the layer (router -> plan -> permute -> grouped SwiGLU -> combine)
 entirely through ``libhanuman_moe.so``; ``forward`` is the step ``bench.py``
 times and the GPU tests check.  With bf16 tokens and SwiGLU experts the
-permutation is fused into the gate/up GEMM (``xs`` is then ``None``).
+permutation is fused into the gate/up GEMM (``xs`` is then ``None``); with
+fp8 experts on bf16 tokens the gate/up GEMM gathers from the per-token codes.
 """
 from __future__ import annotations
 
@@ -64,6 +65,10 @@ class DeviceLayer:
         # from x itself (hmoe_grouped_gate_up_gather), no dispatched copy.
         self.fused_dispatch = (wl.expert == "swiglu" and not self.fp8
                                and self.x.dtype == torch.bfloat16)
+        # fp8 experts on bf16 tokens: x is quantised per token and the gate/up
+        # GEMM gathers from its codes (hmoe_grouped_gate_up_fp8_gather).
+        self.fp8_gather = (wl.expert == "swiglu" and self.fp8
+                           and self.x.dtype == torch.bfloat16)
         ws = int(_lib.lib().hmoe_plan_workspace_bytes(wl.tokens, wl.top_k, wl.n_experts))
         self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
         self.out_dtype = _TORCH_DT[wl.out_dtype]
@@ -77,9 +82,18 @@ class DeviceLayer:
         return K.router(self.x, self.router_w, None, wl.top_k, self.mode)
 
     def experts_fp8(self, plan):
-        """e4m3 dispatch and expert GEMMs: (xs_q, xs_scale, h, h_q, h_scale, ys)."""
-        xs_q, xs_s = K.permute_rows_fp8(self.x, plan)
-        h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, self.w_gate_up, self.w_gate_up_scale)
+        """e4m3 dispatch and expert GEMMs: (xs_q, xs_scale, h, h_q, h_scale, ys).
+        With bf16 tokens x is quantised per token and the gate/up GEMM gathers
+        its rows from the codes (``xs_q``/``xs_scale`` are then per token,
+        ``[T, D]``/``[T]``); otherwise they are the dispatched rows."""
+        if self.fp8_gather:
+            xs_q, xs_s = K.quantize_rows_fp8(self.x)
+            h = K.grouped_gate_up_fp8_gather(xs_q, xs_s, plan, self.w_gate_up,
+                                             self.w_gate_up_scale)
+        else:
+            xs_q, xs_s = K.permute_rows_fp8(self.x, plan)
+            h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, self.w_gate_up,
+                                      self.w_gate_up_scale)
         h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
         ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, self.w_down, self.w_down_scale)
         return xs_q, xs_s, h, h_q, h_s, ys
@@ -92,7 +106,8 @@ class DeviceLayer:
         h = None
         if self.fp8:
             xs, xs_s, h, h_q, h_s, ys = self.experts_fp8(plan)
-            extra = {"xs_scale": xs_s, "h_q": h_q, "h_scale": h_s}
+            extra = {"xs_scale": xs_s, "h_q": h_q, "h_scale": h_s,
+                     "xs_per_token": self.fp8_gather}
         elif self.f32:
             xs = K.permute_rows(self.x, plan, torch.float32)
             h = K.grouped_gate_up_f32(xs, plan.offsets, self.w_gate, self.w_up)

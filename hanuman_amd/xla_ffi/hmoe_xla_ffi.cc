@@ -351,6 +351,32 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpFp8, GroupedGateUpFp8Impl,
                                   .Arg<ffi::Buffer<ffi::F32>>()
                                   .Ret<ffi::Buffer<ffi::BF16>>());
 
+// Per-token codes x_q [T, D] and scales [T], perm_src, offsets, packed gate/up
+// and scales -> h [rows_cap, F] bf16 (rows gathered by the GEMM's loads).
+static ffi::Error GroupedGateUpFp8GatherImpl(hipStream_t stream, ffi::Buffer<ffi::U8> x_q,
+                                             ffi::Buffer<ffi::F32> x_scale,
+                                             ffi::Buffer<ffi::S32> perm_src,
+                                             ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+                                             ffi::Buffer<ffi::F32> w_scales, int64_t top_k,
+                                             ffi::ResultBuffer<ffi::BF16> h) {
+  return Status(hmoe_grouped_gate_up_fp8_gather(
+      x_q.typed_data(), x_scale.typed_data(), Rows(x_q), static_cast<int>(top_k),
+      perm_src.typed_data(), offsets.typed_data(), static_cast<int>(offsets.element_count() - 1),
+      Rows(*h), static_cast<int>(Cols(x_q)), static_cast<int>(Cols(*h)), w.typed_data(),
+      w_scales.typed_data(), h->untyped_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpFp8Gather, GroupedGateUpFp8GatherImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Attr<int64_t>("top_k")
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
 static ffi::Error GroupedDownFp8Impl(hipStream_t stream, ffi::Buffer<ffi::U8> h_q,
                                      ffi::Buffer<ffi::F32> h_scale, ffi::Buffer<ffi::S32> offsets,
                                      ffi::Buffer<ffi::U8> w, ffi::Buffer<ffi::F32> w_scales,

@@ -215,6 +215,17 @@ int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_scale, const i
                              int n_experts, int64_t rows_cap, int d_model, int d_ff,
                              const uint8_t* w_packed, const float* w_scales, void* h,
                              hmoe_stream_t stream);
+/* The fp8 h with the row permutation done by the GEMM's loads, as
+ * hmoe_grouped_gate_up_gather does for bf16: x_q [tokens, D] and x_scale
+ * [tokens] are the per-token codes and scales of x (hmoe_quantize_rows_fp8
+ * of x, whose rule is hmoe_permute_rows_fp8's, so h is bit-identical to the
+ * permuted path) and row r of the dispatched operand is token
+ * perm_src[r] / top_k.  tokens * D < 2^31. */
+int hmoe_grouped_gate_up_fp8_gather(const uint8_t* x_q, const float* x_scale, int64_t tokens,
+                                    int top_k, const int32_t* perm_src, const int32_t* offsets,
+                                    int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                    const uint8_t* w_packed, const float* w_scales, void* h,
+                                    hmoe_stream_t stream);
 int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale, const int32_t* offsets,
                           int n_experts, int64_t rows_cap, int d_ff, int d_model,
                           const uint8_t* w_packed, const float* w_scales, void* ys,

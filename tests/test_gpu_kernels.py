@@ -453,6 +453,39 @@ FP8_GEMM_CASES = [
 ]
 
 
+FP8_GATHER_CASES = [
+    # T, D, N, K, F, capacity (rows per expert; small values drop slots)
+    (700, 256, 8, 2, 128, 10**6),
+    (1000, 384, 6, 4, 256, 300),
+    (333, 512, 16, 8, 128, 90),
+]
+
+
+@pytest.mark.parametrize("case", FP8_GATHER_CASES,
+                         ids=lambda c: f"T{c[0]}_D{c[1]}_N{c[2]}_K{c[3]}_cap{c[5]}")
+def test_grouped_gate_up_fp8_gather_matches_permuted(gpu, case):
+    """The fp8 gate/up GEMM that gathers its rows from the per-token codes of x
+    gives the same h, bit for bit, as the fp8 permutation followed by the
+    plain fp8 GEMM (the per-token codes are the dispatched codes)."""
+    T, D, N, Kk, F, cap = case
+    print(f"fp8 gather case {case}", flush=True)
+    rng = np.random.default_rng(17 + T)
+    x = dev_bf16(O.bf16_round(rng.standard_normal((T, D)).astype(np.float32)), gpu)
+    top = np.stack([rng.choice(N, Kk, replace=False) for _ in range(T)]).astype(np.int32)
+    plan = K.dispatch_plan(torch.from_numpy(top).to(gpu), N, cap)
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    w, ws = K.pack_fp8_gate_up(dev_f32(wg, gpu), dev_f32(wu, gpu))
+    x_q, x_s = K.quantize_rows_fp8(x)
+    h_fused = K.grouped_gate_up_fp8_gather(x_q, x_s, plan, w, ws)
+    xs_q, xs_s = K.permute_rows_fp8(x, plan)
+    h_ref = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, w, ws)
+    total = int(plan.offsets[-1].item())
+    assert total > 0
+    src = plan.perm_src[:total].long() // Kk
+    assert torch.equal(x_q[src], xs_q[:total]) and torch.equal(x_s[src], xs_s[:total])
+    assert torch.equal(h_fused[:total], h_ref[:total])
+
+
 @pytest.mark.parametrize("case", FP8_GEMM_CASES, ids=lambda c: c[0])
 def test_grouped_gemm_fp8(gpu, case):
     """fp8 GEMMs against float64 dot products of the same decoded operands and

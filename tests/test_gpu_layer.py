@@ -238,8 +238,13 @@ def test_fp8_workload_reduced_tokens(gpu):
     torch.cuda.synchronize()
     check_routing_and_plan(res, r8["top_idx"], r8["gates"], r8["plan"], r8["logits"])
     total = int(r8["plan"]["offsets"][-1])
-    assert np.array_equal(res["xs"].cpu().numpy()[:total], r8["xs"][:total]), "xs codes"
-    assert np.array_equal(res["xs_scale"].cpu().numpy()[:total], r8["xs_s"][:total]), "xs scales"
+    xs_q, xs_s = res["xs"].cpu().numpy(), res["xs_scale"].cpu().numpy()
+    if res["xs_per_token"]:
+        # per-token codes, gathered by the gate/up GEMM through perm_src
+        src = r8["plan"]["perm_src"][:total] // wl.top_k
+        xs_q, xs_s = xs_q[src], xs_s[src]
+    assert np.array_equal(xs_q[:total], r8["xs"][:total]), "xs codes"
+    assert np.array_equal(xs_s[:total], r8["xs_s"][:total]), "xs scales"
     out = host(res["out"])
     assert res["out"].dtype == torch.bfloat16
     err = O.normwise_rel_err(out, ref["out"])
