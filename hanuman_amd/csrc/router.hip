@@ -4,6 +4,8 @@
 // (see router_kernel for how the float64 matrix cores keep that order).
 // Top-k is K rounds of a wave-wide max over a packed (totalOrder key,
 // ~expert) 64-bit value, so equal keys resolve to the lower expert index.
+#include <atomic>
+
 #include "hmoe_common.h"
 
 namespace hmoe {
@@ -167,14 +169,13 @@ constexpr int kRTokWave = 16;
 constexpr int router_dc(int nt) { return nt <= 4 ? 64 : 32; }
 
 // ES waves share a group of 16 tokens and split its expert tiles, so a
-// workgroup of 4 waves takes 64 / ES tokens.  With ES = 2 twice as many
-// workgroups fit the token count, two waves run on every SIMD and each keeps
-// NT/2 independent accumulator chains.
-template <int NT, int ES>
+// workgroup of NW waves takes 16 NW / ES tokens.  With ES = 2 two waves run
+// on every SIMD and each keeps NT/2 independent accumulator chains.
+template <int NT, int ES, int NW>
 struct alignas(16) RouterLds {
   static constexpr int kNP = 16 * NT;
   static constexpr int kWPitch = kNP + 8;
-  static constexpr int kTB = 64 / ES;
+  static constexpr int kTB = 16 * NW / ES;
   static constexpr int kDc = router_dc(NT);
   static constexpr int kXPitch = kDc + 4;  // 16-byte aligned rows
   float x[2][kTB][kXPitch];
@@ -184,24 +185,25 @@ struct alignas(16) RouterLds {
 // WV: n_experts is a multiple of the W elements in 16 bytes, so a chunk of W
 // (kRDc consecutive rows of n_experts values, contiguous in memory) is staged
 // with 16-byte loads and LDS writes.
-template <int NT, int ES, typename XT, typename WT, bool WV>
-__global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, const WT* __restrict__ w,
+template <int NT, int ES, int NW, typename XT, typename WT, bool WV>
+__global__ __launch_bounds__(64 * NW) void router_kernel(const XT* __restrict__ x, const WT* __restrict__ w,
                                                      const float* __restrict__ bias, int64_t tokens,
                                                      int d_model, int n_experts, int top_k, int mode,
                                                      float rsf, float* __restrict__ logits,
                                                      int32_t* __restrict__ top_idx,
                                                      float* __restrict__ gates) {
   static_assert(NT % ES == 0, "expert tiles must split evenly");
-  constexpr int kNP = RouterLds<NT, ES>::kNP;
-  constexpr int kTB = RouterLds<NT, ES>::kTB;
-  constexpr int kRDc = RouterLds<NT, ES>::kDc;
+  constexpr int kThr = 64 * NW;
+  constexpr int kNP = RouterLds<NT, ES, NW>::kNP;
+  constexpr int kTB = RouterLds<NT, ES, NW>::kTB;
+  constexpr int kRDc = RouterLds<NT, ES, NW>::kDc;
   constexpr int kTG = kTB / kRTokWave;                // token groups per workgroup
   constexpr int kNTW = NT / ES;                       // expert tiles per wave
   constexpr int kEPL = (kNP + 63) / 64;
-  constexpr int kWPer = (kRDc * kNP + 255) / 256;     // w elements per thread per chunk
+  constexpr int kWPer = (kRDc * kNP + kThr - 1) / kThr;  // w elements per thread per chunk
   constexpr int kE16 = 16 / static_cast<int>(sizeof(WT));  // W elements per 16-byte load
-  constexpr int kWV = (kRDc * kNP / kE16 + 255) / 256;     // 16-byte W loads per thread per chunk
-  __shared__ RouterLds<NT, ES> lds;
+  constexpr int kWV = (kRDc * kNP / kE16 + kThr - 1) / kThr;  // 16-byte W loads per thread per chunk
+  __shared__ RouterLds<NT, ES, NW> lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -210,20 +212,20 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTB;
 
   // Staging assignment: x elements (tt, dd..dd+7) = (g / kXT, (g % kXT) * 8) for
-  // the groups g = tid + 256 r < kXT*kTB (kXT = kRDc / 8 groups per token
+  // the groups g = tid + kThr r < kXT*kTB (kXT = kRDc / 8 groups per token
   // row).  d_model is a multiple of 8, so a group of 8 is wholly inside or
   // outside the row.  Every load is unconditional from an
   // in-range address (clamped token row, d or expert 0) and masked
   // afterwards, so the loads of a chunk stay in flight together until they
   // are parked in LDS.
   constexpr int kXT = kRDc / 8;
-  constexpr int kXR = (kXT * kTB + 255) / 256;  // x groups per thread
+  constexpr int kXR = (kXT * kTB + kThr - 1) / kThr;  // x groups per thread
   int xs_tt[kXR], xs_dd[kXR];
   bool x_thread[kXR];
   int64_t xs_row[kXR];
 #pragma unroll
   for (int r = 0; r < kXR; ++r) {
-    const int g = tid + 256 * r;
+    const int g = tid + kThr * r;
     xs_tt[r] = g / kXT;
     x_thread[r] = xs_tt[r] < kTB;
     xs_dd[r] = (g % kXT) * 8;
@@ -237,12 +239,12 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   constexpr int kWRegs = WV ? 4 * kWV : kWPer;
   uint32_t wr0[kWRegs], wr1[kWRegs];
   auto w_ok = [&](int q, int d0) __attribute__((always_inline)) {
-    const int idx = q * 256 + tid;
+    const int idx = q * kThr + tid;
     return idx < kRDc * kNP && idx % kNP < n_experts && d0 + idx / kNP < d_model;
   };
-  // WV: vector q covers elements idx .. idx + kE16 - 1 (idx = (q*256 + tid) *
+  // WV: vector q covers elements idx .. idx + kE16 - 1 (idx = (q*kThr + tid) *
   // kE16) of the chunk, i.e. row idx / n_experts, experts idx % n_experts ...
-  auto wv_idx = [&](int q) __attribute__((always_inline)) { return (q * 256 + tid) * kE16; };
+  auto wv_idx = [&](int q) __attribute__((always_inline)) { return (q * kThr + tid) * kE16; };
   auto fetch = [&](X8<XT>* xr, uint32_t* wr, int d0) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < kXR; ++r) {
@@ -262,7 +264,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     } else {
 #pragma unroll
       for (int q = 0; q < kWPer; ++q) {
-        const int idx = q * 256 + tid;
+        const int idx = q * kThr + tid;
         const int64_t off = static_cast<int64_t>(d0 + idx / kNP) * n_experts + idx % kNP;
         wr[q] = __float_as_uint(load_w_f32(w, w_ok(q, d0) ? off : 0));
       }
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
     } else {
 #pragma unroll
       for (int q = 0; q < kWPer; ++q) {
-        const int idx = q * 256 + tid;
+        const int idx = q * kThr + tid;
         if (idx < kRDc * kNP) lds.w[buf][idx / kNP][idx % kNP] = w_ok(q, d0) ? __uint_as_float(wr[q]) : 0.0f;
       }
     }
@@ -325,7 +327,7 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
   if (WV && n_experts < kNP) {
     // Expert columns past n_experts are never written by the vector staging:
     // zero them once in both buffers.
-    for (int i = tid; i < 2 * kRDc * kNP; i += 256) {
+    for (int i = tid; i < 2 * kRDc * kNP; i += kThr) {
       const int n = i % kNP;
       if (n >= n_experts) lds.w[i / (kRDc * kNP)][(i / kNP) % kRDc][n] = 0.0f;
     }
@@ -383,8 +385,8 @@ __global__ __launch_bounds__(256) void router_kernel(const XT* __restrict__ x, c
           static_cast<float>(acc[t][r]);
   __syncthreads();
 
-  // Selection: wave w takes tokens w*kTB/4 .. (w+1)*kTB/4 - 1 of the workgroup.
-  constexpr int kSel = kTB / 4;
+  // Selection: wave w takes tokens w*kTB/NW .. (w+1)*kTB/NW - 1 of the workgroup.
+  constexpr int kSel = kTB / NW;
   static_assert(kSel % 2 == 0, "selection takes tokens in pairs");
 #pragma unroll 1
   for (int i = 0; i < kSel; i += 2) {
@@ -434,21 +436,54 @@ __global__ __launch_bounds__(256) void select_kernel(const float* __restrict__ l
   select_and_gate<EPL, 1>(l, st, bias, n_experts, top_k, mode, rsf, ti, gt);
 }
 
+// CU count of the stream's device (0 if it cannot be queried), cached per device.
+int stream_cus(hipStream_t s) {
+  int dev = 0;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess && hipGetDevice(&dev) != hipSuccess) return 0;
+  static std::atomic<int> cached[64];
+  int cus = dev >= 0 && dev < 64 ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (cus == 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      cus > 0 && dev >= 0 && dev < 64)
+    cached[dev].store(cus, std::memory_order_relaxed);
+  return cus > 0 ? cus : 0;
+}
+
+template <int NT, int NW, typename XT, typename WT>
+void launch_router_nw(const void* x, const void* w, const float* bias, int64_t tokens,
+                      int d_model, int n_experts, int top_k, int mode, float rsf, float* logits,
+                      int32_t* top_idx, float* gates, hipStream_t stream) {
+  constexpr int ES = NT >= 2 ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, RouterLds<NT, ES, NW>::kTB)));
+  if (n_experts % (16 / static_cast<int>(sizeof(WT))) == 0 &&
+      reinterpret_cast<uintptr_t>(w) % 16 == 0)
+    hipLaunchKernelGGL((router_kernel<NT, ES, NW, XT, WT, true>), grid, dim3(64 * NW), 0, stream,
+                       static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
+                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
+  else
+    hipLaunchKernelGGL((router_kernel<NT, ES, NW, XT, WT, false>), grid, dim3(64 * NW), 0, stream,
+                       static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
+                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
+}
+
+// From 64 experts up, workgroups of 8 waves (64 tokens) when they still give
+// every CU one: they stage each chunk of W once for twice the tokens.
+// Measured at 16384 tokens, d_model 2048, 64 experts: 112 -> 106 us; 65536
+// tokens, 128 experts: 703 -> 637 us; at 8192 tokens (half the CUs) 8 waves
+// were slower (72 -> 104 us), hence the token-count switch.
 template <int NT, typename XT, typename WT>
 void launch_router(const void* x, const void* w, const float* bias, int64_t tokens, int d_model,
                    int n_experts, int top_k, int mode, float rsf, float* logits, int32_t* top_idx,
                    float* gates, hipStream_t stream) {
-  constexpr int ES = NT >= 2 ? 2 : 1;
-  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, RouterLds<NT, ES>::kTB)));
-  if (n_experts % (16 / static_cast<int>(sizeof(WT))) == 0 &&
-      reinterpret_cast<uintptr_t>(w) % 16 == 0)
-    hipLaunchKernelGGL((router_kernel<NT, ES, XT, WT, true>), grid, dim3(256), 0, stream,
-                       static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
-                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
-  else
-    hipLaunchKernelGGL((router_kernel<NT, ES, XT, WT, false>), grid, dim3(256), 0, stream,
-                       static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
-                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
+  if constexpr (NT >= 4) {
+    const int cus = stream_cus(stream);
+    if (cus > 0 && ceil_div(tokens, RouterLds<NT, 2, 8>::kTB) >= cus) {
+      launch_router_nw<NT, 8, XT, WT>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf,
+                                      logits, top_idx, gates, stream);
+      return;
+    }
+  }
+  launch_router_nw<NT, 4, XT, WT>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits,
+                                  top_idx, gates, stream);
 }
 
 template <int NT>

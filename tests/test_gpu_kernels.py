@@ -61,6 +61,9 @@ ROUTER_CASES = [
     (300, 512, 200, 6, "bf16", "f32", "sigmoid", 2.5, True),
     (256, 4096, 32, 4, "bf16", "bf16", "softmax", 1.0, False),
     (129, 1536, 80, 8, "bf16", "f32", "sigmoid", 2.5, True),
+    # enough tokens for one 64-token workgroup per CU (8-wave router), last one partial
+    (16450, 512, 66, 6, "bf16", "f32", "sigmoid", 2.5, True),
+    (16400, 768, 64, 8, "bf16", "bf16", "softmax", 1.0, False),
 ]
 
 
