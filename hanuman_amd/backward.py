@@ -152,7 +152,8 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
                  w_gate_up: torch.Tensor, ops: BackwardOperands, dy: torch.Tensor, *,
                  mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0,
                  shared: SharedOperands | None = None, h_shared=None,
-                 aux: tuple | None = None, need: dict | None = None) -> dict:
+                 aux: tuple | None = None, need: dict | None = None,
+                 shared_promoted: tuple | None = None) -> dict:
     """The whole module's VJP (``moe.py:170-294``): every input and weight
     gradient for the cotangent ``dy`` (f32 ``[T, D]``) of ``out`` and, with
     ``aux = (batch, seq, d_losses)``, the cotangents ``d_losses`` (f32 ``[3]``:
@@ -166,6 +167,11 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
     ``dWg_shared``, ``dWu_shared``, ``dWd_shared`` when there is a shared
     expert.  ``need`` (``{"router", "experts", "shared"}`` -> bool, default
     all) skips the weight gradients not asked for; those entries are None.
+    ``shared_promoted = (w_gate, w_up, w_down, n_shared)`` (bf16-rounded
+    masters as float32) in place of ``shared``: float32 ``x``, whose shared
+    expert ran promoted to float32 (``moe.py:249``); its VJP runs on the
+    float32 kernels and the master gradients pass through bf16 (the VJP of
+    ``w.astype(bf16)``).
     """
     need = {"router": True, "experts": True, "shared": True, **(need or {})}
     plan = fwd["plan"]
@@ -173,6 +179,8 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
     xc = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)   # x.astype(dtype), moe.py:198
     n_sh = shared.n_shared if shared is not None else 0
     d_ys, d_gates, d_sh = K.combine_bwd(dy, fwd["ys"], plan, fwd["gates"], n_sh)
+    if shared_promoted is not None and shared is not None:
+        raise ValueError("moe_backward: shared and shared_promoted are exclusive")
     dh = K.grouped_dgrad_down(d_ys, plan.offsets, ops.w_down_dgrad)
     dgu = K.grouped_gate_up_swiglu_bwd_gather(xc, plan, w_gate_up, dh)
     del dh
@@ -183,6 +191,19 @@ def moe_backward(x: torch.Tensor, router_w: torch.Tensor | None, fwd: dict,
         sh = shared_backward(xc, d_sh, h_shared, shared, weights=need["shared"])
         residual = sh["dx"]
         res.update(dWg_shared=sh["dWg"], dWu_shared=sh["dWu"], dWd_shared=sh["dWd"])
+    elif shared_promoted is not None:
+        n_p = shared_promoted[3]
+        # each float32 SwiGLU's output cotangent is dy / n_shared (no bf16 cast)
+        d_sh32 = dy if n_p == 1 else dy / n_p
+        sh = _shared_backward_f32(x.float().contiguous(), d_sh32, h_shared, shared_promoted)
+        residual = sh["dx"]
+        if need["shared"]:
+            dws = [sh[k].to(torch.bfloat16).float() for k in ("dWg", "dWu", "dWd")]
+            if n_p == 1:
+                dws = [w[0] for w in dws]
+            res.update(dWg_shared=dws[0], dWu_shared=dws[1], dWd_shared=dws[2])
+        else:
+            res.update(dWg_shared=None, dWu_shared=None, dWd_shared=None)
     dx = K.gather_bwd(d_xs, plan, residual=residual)
     del d_xs, residual
     d_logits = K.router_bwd(fwd["logits"], fwd["top_idx"], fwd["gates"], d_gates, N, mode,

@@ -306,6 +306,22 @@ class MoE:
             acc += o.float()
         return acc / self.n_shared_experts
 
+    def _shared_ffn_promoted(self, x32: torch.Tensor, hs: list | None = None) -> torch.Tensor:
+        """Shared expert(s) for a float32 ``x`` under bf16 compute: ``moe.py:249``
+        passes ``x`` as given, so each SwiGLU's ``x @ w.astype(bf16)``
+        (``moe.py:23-29``) promotes to float32: a float32 SwiGLU on the
+        bf16-rounded weights, on the float32 grouped GEMMs, float32 output
+        (the mean over several)."""
+        wg, wu, wd = (w.to(torch.bfloat16).float()
+                      for w in (self.shared_w_gate.value, self.shared_w_up.value,
+                                self.shared_w_down.value))
+        if self.n_shared_experts == 1:
+            return _f32_swiglu_one(x32, wg, wu, wd, hs)
+        acc = torch.zeros((x32.shape[0], wd.shape[-1]), dtype=torch.float32, device=x32.device)
+        for i in range(self.n_shared_experts):
+            acc += _f32_swiglu_one(x32, wg[i], wu[i], wd[i], hs)
+        return acc / self.n_shared_experts
+
     def _params(self):
         return (self.router.value, self.expert_w_gate.value, self.expert_w_up.value,
                 self.expert_w_down.value, self.shared_w_gate.value, self.shared_w_up.value,
@@ -373,16 +389,19 @@ class MoE:
         else:
             h = K.grouped_gate_up(K.permute_rows(x2, plan, self.dtype), plan.offsets, wgu)
         ys = K.grouped_down(h, plan.offsets, wd)
-        xc = x2 if x2.dtype == self.dtype else x2.to(self.dtype)
         hs = [] if save else None
-        shared = self._shared_ffn(xc, hs)
+        promoted = x2.dtype == torch.float32 and self.n_shared_experts > 0
+        if promoted:
+            shared = self._shared_ffn_promoted(x2, hs)
+        else:
+            shared = self._shared_ffn(x2 if x2.dtype == self.dtype else x2.to(self.dtype), hs)
         out = K.combine(ys, plan, gates, shared, torch.float32)
         losses, counts = K.router_aux(logits, top_idx, B, S)
         saved = None
         if save:
             saved = {"x": x2, "logits": logits, "top_idx": top_idx, "gates": gates, "plan": plan,
                      "h": h, "ys": ys, "h_shared": hs, "mode": mode, "rsf": rsf,
-                     "batch": B, "seq": S}
+                     "batch": B, "seq": S, "shared_promoted": promoted}
         return out.reshape(B, S, D), losses, counts, saved
 
     def _backward_operands(self, masters):
@@ -421,7 +440,8 @@ class _MoEFunction(torch.autograd.Function):
         ctx.meta = {"capacity": plan.capacity, "rows_cap": plan.rows_cap,
                     "n_experts": plan.n_experts, "top_k": plan.top_k, "mode": saved["mode"],
                     "rsf": saved["rsf"], "batch": saved["batch"], "seq": saved["seq"],
-                    "n_hs": len(hs), "f32": "xs" in saved}
+                    "n_hs": len(hs), "f32": "xs" in saved,
+                    "shared_promoted": saved.get("shared_promoted", False)}
         ctx.x_shape, ctx.x_dtype = x.shape, x.dtype
         ctx.save_for_backward(saved["x"], saved["logits"], saved["top_idx"], saved["gates"],
                               *(getattr(plan, k) for k in _MoEFunction._PLAN),
@@ -467,9 +487,15 @@ class _MoEFunction(torch.autograd.Function):
         else:
             ops, shared = layer._backward_operands((wg, wu, wd, swg, swu, swd))
             wgu, _ = layer._packed_routed((wg, wu, wd))
+            promoted = None
+            if m["shared_promoted"]:
+                # float32 x: the shared expert ran promoted to float32 on bf16(w)
+                shared = None
+                promoted = tuple(t.to(torch.bfloat16).float() for t in (swg, swu, swd)) + (
+                    layer.n_shared_experts,)
             g = moe_backward(x2, router_w, fwd, wgu, ops, dy, mode=m["mode"],
                              routed_scaling_factor=m["rsf"], shared=shared, h_shared=hs,
-                             aux=aux, need=need)
+                             aux=aux, need=need, shared_promoted=promoted)
         dx = g["dx"].reshape(ctx.x_shape).to(ctx.x_dtype) if ng[1] else None
 
         def shaped(key, like, wanted):

@@ -292,7 +292,8 @@ def shared_forward64(x, w_gate, w_up, w_down, n_shared: int):
     return out / n_shared
 
 
-def shared_bwd(x, w_gate, w_up, w_down, n_shared: int, dy, precision: str = "bf16") -> dict:
+def shared_bwd(x, w_gate, w_up, w_down, n_shared: int, dy, precision: str = "bf16",
+               promoted: bool = False) -> dict:
     """VJP of the shared expert(s) (``moe.py:161-168``, added with weight 1 at
     ``:249-251``) for the float32 cotangent ``dy`` of the layer output.
 
@@ -301,9 +302,33 @@ def shared_bwd(x, w_gate, w_up, w_down, n_shared: int, dy, precision: str = "bf1
     with one segment holding every token.  Returns ``dx [T, D]`` and
     ``dWg``, ``dWu``, ``dWd`` in the parameter shapes (2-D for one shared
     expert, stacked for several), plus ``d_out`` (the per-expert cotangent).
+
+    ``promoted``: a float32 ``x`` under bf16 compute, whose SwiGLUs ran in
+    float32 on the bf16-rounded weights (``moe.py:249`` passes ``x`` as
+    given): the output cotangent is ``dy / n_shared`` (float32 outputs, no
+    cast), the VJP is the float32 one on ``bf16(w)``, and the master
+    gradients pass through bf16 (the VJP of ``w.astype(bf16)``).
     """
     x = np.asarray(x)
     T = x.shape[0]
+    if promoted:
+        d_out = np.asarray(dy, F32) / F32(n_shared)
+        stack = n_shared > 1
+        ws = [(w_gate[i], w_up[i], w_down[i]) for i in range(n_shared)] if stack \
+            else [(w_gate, w_up, w_down)]
+        dx = np.zeros(x.shape, F64)
+        grads = {"dWg": [], "dWu": [], "dWd": []}
+        for wg_, wu_, wd_ in ws:
+            r = expert_ffn_bwd(x, np.array([0, T]), bf16_round(np.asarray(wg_, F32))[None],
+                               bf16_round(np.asarray(wu_, F32))[None],
+                               bf16_round(np.asarray(wd_, F32))[None], d_out, "fp32")
+            dx = dx + r["d_xs"]
+            for k in grads:
+                grads[k].append(bf16_round(np.asarray(r[k][0], F32)))
+        res = {k: (np.stack(v) if stack else v[0]).astype(F32) for k, v in grads.items()}
+        res["dx"] = dx.astype(F32)
+        res["d_out"] = d_out
+        return res
     dy = np.asarray(dy, F32 if precision == "bf16" else F64)
     d_out = _r(dy / dy.dtype.type(n_shared), precision)
     stack = n_shared > 1
@@ -402,8 +427,10 @@ def moe_backward(x, params: dict, dy, fwd: dict, *, routing: str = "softmax",
     res = {}
     if n_shared > 0:
         xc = bf16_round(x) if precision == "bf16" else x
-        sh = shared_bwd(xc, params["shared_w_gate"], params["shared_w_up"],
-                        params["shared_w_down"], n_shared, dy, precision)
+        # a float32 x under bf16 compute reaches the shared expert as given (moe.py:249)
+        promoted = precision == "bf16" and not np.array_equal(xc, x)
+        sh = shared_bwd(x if promoted else xc, params["shared_w_gate"], params["shared_w_up"],
+                        params["shared_w_down"], n_shared, dy, precision, promoted=promoted)
         dx = dx + sh["dx"]
         res = {"dWg_shared": sh["dWg"], "dWu_shared": sh["dWu"], "dWd_shared": sh["dWd"],
                "dx_shared": sh["dx"], "d_shared_out": sh["d_out"]}

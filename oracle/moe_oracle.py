@@ -541,10 +541,20 @@ def combine_identity(x, slot_pos, gates, T: int, K: int) -> np.ndarray:
 
 def shared_expert(x_flat, w_gate, w_up, w_down, n_shared: int, precision: str = "fp32"):
     """``_shared_ffn`` (``moe.py:161-168``): one SwiGLU (2-D weights) or the
-    mean of ``n_shared`` SwiGLUs (3-D weights)."""
+    mean of ``n_shared`` SwiGLUs (3-D weights).  ``precision="bf16_promoted"``:
+    a float32 ``x`` under bf16 compute, which ``moe.py:249`` passes as given,
+    so ``x @ w.astype(bf16)`` (``moe.py:23-29``) promotes to float32: bf16
+    weights, every product and SwiGLU value a float32 result (float64
+    arithmetic rounded to float32 at each op)."""
     x = np.asarray(x_flat, F32)
 
     def one(wg, wu, wd):
+        if precision == "bf16_promoted":
+            x64 = x.astype(F64)
+            g = (x64 @ bf16_round(wg).astype(F64)).astype(F32)
+            u = (x64 @ bf16_round(wu).astype(F64)).astype(F32)
+            h = (silu(g.astype(F64)) * u.astype(F64)).astype(F32)
+            return (h.astype(F64) @ bf16_round(wd).astype(F64)).astype(F32)
         if precision == "f32":
             return ((silu(x @ np.asarray(wg, F32)) * (x @ np.asarray(wu, F32))).astype(F32)
                     @ np.asarray(wd, F32)).astype(F32)
@@ -686,8 +696,13 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
         raise ValueError(expert)
     residual = None
     if n_shared > 0:
-        residual = shared_expert(x_c, params["shared_w_gate"], params["shared_w_up"],
-                                 params["shared_w_down"], n_shared, precision=precision)
+        # moe.py:249 passes x as given (only the routed path casts, moe.py:198):
+        # a float32 x under bf16 compute promotes the shared SwiGLU to float32
+        promoted = dtype == "bf16" and not np.array_equal(x_c, x)
+        residual = shared_expert(x if promoted else x_c, params["shared_w_gate"],
+                                 params["shared_w_up"], params["shared_w_down"], n_shared,
+                                 precision="bf16_promoted" if promoted and precision == "bf16"
+                                 else precision)
     out = combine(ys, plan["slot_pos"], gates, T, K, residual=residual,
                   ys_dtype="f32" if (dtype == "f32" and expert == "swiglu") else "bf16")
     if out_dtype == "bf16":

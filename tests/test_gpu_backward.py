@@ -373,7 +373,7 @@ def test_gate_up_raw_matches_gather(gpu):
 
 
 @pytest.mark.parametrize("n_shared,cf,x_dtype,N,Kk", [(1, None, "bf16", 8, 2), (2, 1.0, "bf16", 8, 2),
-                                                      (1, 1.0, "f32", 8, 2),
+                                                      (1, 1.0, "f32", 8, 2), (2, None, "f32", 8, 2),
                                                       (1, None, "bf16", 66, 8)])
 def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype, N, Kk):
     """MoE.__call__ under torch autograd: loss = <dy, out> + c_z z_loss +

@@ -197,6 +197,37 @@ def test_moe_module_reference_mode(gpu, n_shared):
     assert np.array_equal(host(aux["expert_counts"]), a["expert_counts"])
 
 
+@pytest.mark.parametrize("n_shared", [1, 2])
+def test_moe_module_float32_input_promotes_shared_expert(gpu, n_shared):
+    """bf16 compute with a float32 x: the routed experts see bf16(x)
+    (moe.py:198), the shared expert x as given (moe.py:249), so its SwiGLU
+    runs in float32 on the bf16-rounded weights. The shared output matches
+    the oracle's promoted SwiGLU to float32 accuracy (the bf16 path would be
+    ~3e-3 away), the layer output the bf16-mode oracle."""
+    B, S, D, F, N, Kk = 2, 192, 256, 256, 8, 2
+    m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.bfloat16, rngs=3, device=gpu)
+    x = torch.randn(B, S, D, generator=torch.Generator(device=gpu).manual_seed(6), device=gpu)
+    print(f"module float32 x, n_shared={n_shared}", flush=True)
+    out, _ = m(x)
+    sh = m._shared_ffn_promoted(x.reshape(B * S, D).contiguous())
+    torch.cuda.synchronize()
+    p = _params_np(m)
+    xn = x.cpu().numpy().reshape(B * S, D)
+    sh_ref = O.shared_expert(xn, p["shared_w_gate"], p["shared_w_up"], p["shared_w_down"],
+                             n_shared, "bf16_promoted")
+    err_sh = O.normwise_rel_err(host(sh), sh_ref)
+    err_bf = O.normwise_rel_err(O.shared_expert(O.bf16_round(xn), p["shared_w_gate"],
+                                                p["shared_w_up"], p["shared_w_down"], n_shared,
+                                                "bf16"), sh_ref)
+    ref = O.moe_forward(xn, p, top_k=Kk, routing="sigmoid", routed_scaling_factor=2.5,
+                        n_shared=n_shared, dtype="bf16", precision="bf16")
+    err = O.normwise_rel_err(host(out).reshape(B * S, D), ref["out"])
+    print(f"  shared vs promoted oracle {err_sh:.2e} (bf16 path {err_bf:.2e}); out {err:.2e}",
+          flush=True)
+    assert err_sh < 1e-5 and err_bf > 1e-3
+    assert err < 5e-3
+
+
 def test_moe_module_capacity_softmax(gpu):
     B, S, D, F, N, Kk = 1, 512, 512, 256, 16, 4
     m = MoE(D, F, N, Kk, 1, 0.5, 1.0, "bfloat16", rngs=7, device=gpu, routing="softmax",

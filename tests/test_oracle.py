@@ -393,6 +393,38 @@ def test_shared_expert_is_one_segment_expert_ffn(precision):
     np.testing.assert_allclose(same, ones[0], rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("n_shared", [1, 2])
+def test_shared_expert_promoted_is_float32_swiglu_on_bf16_weights(n_shared):
+    """A float32 x under bf16 compute reaches the shared expert as given
+    (moe.py:249), so x @ w.astype(bf16) promotes to float32: the result is the
+    float64 SwiGLU on the bf16-rounded weights up to float32 roundings. Both
+    plausible mistakes, unrounded weights and the routed bf16 rounding points,
+    are 100x further away. moe_forward picks this mode for a float32 x."""
+    rng = np.random.default_rng(41 + n_shared)
+    T, D, F = 48, 64, 40
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    assert not np.array_equal(O.bf16_round(x), x)
+    sh = (lambda *s: s) if n_shared == 1 else (lambda *s: (n_shared,) + s)
+    wg, wu = (0.1 * rng.standard_normal((2,) + sh(D, F))).astype(np.float32)
+    wd = (0.1 * rng.standard_normal(sh(F, D))).astype(np.float32)
+    got = O.shared_expert(x, wg, wu, wd, n_shared, "bf16_promoted")
+    ref = O.shared_expert(x, O.bf16_round(wg), O.bf16_round(wu), O.bf16_round(wd), n_shared, "fp32")
+    assert O.normwise_rel_err(got, ref) < 1e-6
+    assert O.normwise_rel_err(O.shared_expert(x, wg, wu, wd, n_shared, "fp32"), got) > 1e-4
+    assert O.normwise_rel_err(O.shared_expert(x, wg, wu, wd, n_shared, "bf16"), got) > 1e-4
+    # the layer: out with the shared expert minus out without it is that residual
+    N, K = 4, 2
+    params = {"router": (0.1 * rng.standard_normal((D, N))).astype(np.float32),
+              "expert_w_gate": (0.1 * rng.standard_normal((N, D, F))).astype(np.float32),
+              "expert_w_up": (0.1 * rng.standard_normal((N, D, F))).astype(np.float32),
+              "expert_w_down": (0.1 * rng.standard_normal((N, F, D))).astype(np.float32),
+              "shared_w_gate": wg, "shared_w_up": wu, "shared_w_down": wd}
+    kw = dict(top_k=K, routing="softmax", dtype="bf16", precision="bf16")
+    with_sh = O.moe_forward(x, params, n_shared=n_shared, **kw)["out"]
+    without = O.moe_forward(x, params, n_shared=0, **kw)["out"]
+    assert O.normwise_rel_err(with_sh.astype(np.float64) - without, got) < 1e-5
+
+
 # ------------------------------------------------------------------- fp8 --
 
 def test_quantize_rows_e4m3_rule_matches_torch_conversion():

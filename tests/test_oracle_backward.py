@@ -276,6 +276,43 @@ def test_shared_bwd(n_shared):
         close((r[name] * v).sum(), fd(f, base[pos], v))
 
 
+@pytest.mark.parametrize("n_shared", [1, 2])
+def test_shared_bwd_promoted(n_shared):
+    """The shared expert of a float32 x under bf16 compute (moe.py:249: a
+    float32 SwiGLU on bf16(w)): dx against finite differences of the float64
+    forward on the rounded weights; the master gradients against the same
+    differences with respect to the rounded weights, to bf16 accuracy (they
+    pass through bf16, the VJP of w.astype(bf16))."""
+    rng = np.random.default_rng(30 + n_shared)
+    T, D, F = 7, 12, 10
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    shape = (lambda *s: s) if n_shared == 1 else (lambda *s: (n_shared,) + s)
+    wg = (0.3 * rng.standard_normal(shape(D, F))).astype(np.float32)
+    wu = (0.3 * rng.standard_normal(shape(D, F))).astype(np.float32)
+    wd = (0.3 * rng.standard_normal(shape(F, D))).astype(np.float32)
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    r = B.shared_bwd(x, wg, wu, wd, n_shared, dy, "bf16", promoted=True)
+    assert np.array_equal(r["d_out"], dy / np.float32(n_shared))
+    base = [x.astype(np.float64)] + [O.bf16_round(w).astype(np.float64) for w in (wg, wu, wd)]
+    for name, pos, rtol in (("dx", 0, 1e-5), ("dWg", 1, None), ("dWu", 2, None), ("dWd", 3, None)):
+        assert r[name].shape == base[pos].shape
+        if pos > 0:
+            assert np.array_equal(O.bf16_round(r[name]), r[name])
+        v = rng.standard_normal(base[pos].shape)
+
+        def f(p, pos=pos):
+            a = list(base)
+            a[pos] = p
+            return (dy * B.shared_forward64(*a, n_shared)).sum()
+
+        terms = r[name].astype(np.float64) * v
+        if pos == 0:
+            close(terms.sum(), fd(f, base[pos], v), rtol)
+        else:
+            # bf16 rounding moves each term by at most 2^-8 of itself
+            assert abs(terms.sum() - fd(f, base[pos], v)) <= 2.0 ** -8 * np.abs(terms).sum()
+
+
 def test_shared_forward64_matches_forward_oracle():
     rng = np.random.default_rng(12)
     T, D, F = 5, 8, 6
