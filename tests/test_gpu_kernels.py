@@ -116,6 +116,26 @@ def test_router_from_logits_ties_and_signed_zero(gpu):
     assert host(idx)[1].tolist() == list(range(Kk))      # all equal -> lowest indices
 
 
+@pytest.mark.parametrize("T,N,Kk,mode", [(1003, 200, 6, "sigmoid"), (77, 100, 4, "softmax"),
+                                         (18, 16, 2, "softmax")])
+def test_router_from_logits_ragged(gpu, T, N, Kk, mode):
+    """Token counts that leave the last wave's group of tokens partial."""
+    rng = np.random.default_rng(T + N)
+    logits = rng.standard_normal((T, N), dtype=np.float32)
+    if mode == "softmax":
+        idx_ref, g_ref = O.route_softmax(logits, Kk)
+        bias = None
+    else:
+        bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+        idx_ref, g_ref, _ = O.route_sigmoid(logits, bias, Kk, 2.5)
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    idx, g = K.router_from_logits(dev_f32(logits, gpu), dev_f32(bias, gpu) if bias is not None else None,
+                                  Kk, m, 2.5)
+    torch.cuda.synchronize()
+    assert_bits_equal(host(idx), idx_ref, "top_idx")
+    assert_bits_equal(host(g), g_ref, "gates")
+
+
 def test_router_from_logits_dispatch_workload_full_size(gpu):
     rng = np.random.default_rng(0)
     T, N, Kk = 32768, 64, 8
