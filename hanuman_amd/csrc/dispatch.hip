@@ -428,7 +428,7 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const TI* __restrict_
       if (c < chunks) v[u].load(src + static_cast<int64_t>(c) * 8);
     }
     for (int k = 0; k < top_k; ++k) {
-      const int32_t pos = __shfl(my_pos, k, 64);
+      const int32_t pos = lane_bcast(my_pos, k);
       if (pos < 0) continue;
       TO* dst = xs + static_cast<int64_t>(pos) * d_model;
 #pragma unroll
@@ -448,8 +448,7 @@ constexpr float kE4m3Max = 448.0f;
 
 // Scale and its inverse from the lane-partial amax (reduced over the wave).
 __device__ __forceinline__ void scales_from_amax(float amax, float& s, float& inv) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  amax = wave_max_f32(amax);
   s = amax > 0.0f ? amax / kE4m3Max : 1.0f;
   inv = amax > 0.0f ? kE4m3Max / amax : 1.0f;
 }
@@ -525,7 +524,7 @@ __global__ __launch_bounds__(256) void permute_rows_fp8_kernel(
       const int c = u * 64 + lane;
       const uint2 q = quant8_e4m3(v[u], inv);
       for (int k = 0; k < top_k; ++k) {
-        const int32_t pos = __shfl(my_pos, k, 64);
+        const int32_t pos = lane_bcast(my_pos, k);
         if (pos >= 0 && c < chunks)
           *reinterpret_cast<uint2*>(xs_q + static_cast<int64_t>(pos) * d_model + c * 8) = q;
       }
@@ -542,7 +541,7 @@ __global__ __launch_bounds__(256) void permute_rows_fp8_kernel(
     v.load(src + static_cast<int64_t>(ok ? c : 0) * 8);
     const uint2 q = quant8_e4m3(v, inv);
     for (int k = 0; k < top_k; ++k) {
-      const int32_t pos = __shfl(my_pos, k, 64);
+      const int32_t pos = lane_bcast(my_pos, k);
       if (pos >= 0 && ok)
         *reinterpret_cast<uint2*>(xs_q + static_cast<int64_t>(pos) * d_model + c * 8) = q;
     }

@@ -121,4 +121,37 @@ __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) {
   return (a + b - 1) / b;
 }
 
+// Lane `src` of v for the whole wave (src wave-uniform): v_readlane, no LDS
+// permute; the result is uniform, so addresses built from it are scalar.
+__device__ __forceinline__ int32_t lane_bcast(int32_t v, int src) {
+  return __builtin_amdgcn_readlane(v, src);
+}
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// fmaxf(v, v of the lane the DPP control CTRL names) in the rows ROW_MASK
+// enables (other lanes keep v).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_fmax(float v) {
+  const int t = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK,
+                                            0xF, false);
+  return fmaxf(v, __int_as_float(t));
+}
+
+// Wave-wide fmaxf, returned in every lane, with DPP moves on the VALU: within
+// each 16-lane row quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and
+// row_mirror leave the row's maximum in all its lanes; row_bcast15 into rows
+// 1 and 3 and row_bcast31 into rows 2 and 3 bring the wave's maximum to lane
+// 63, which is read out.
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = dpp_fmax<0xB1>(v);
+  v = dpp_fmax<0x4E>(v);
+  v = dpp_fmax<0x141>(v);
+  v = dpp_fmax<0x140>(v);
+  v = dpp_fmax<0x142, 0xA>(v);
+  v = dpp_fmax<0x143, 0xC>(v);
+  return lane_bcast(v, 63);
+}
+
 }  // namespace hmoe

@@ -55,9 +55,6 @@ __device__ __forceinline__ void wave_max_u64(uint64_t (&v)[NTOK]) {
   }
 }
 
-__device__ __forceinline__ float lane_value(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
 
 __device__ __forceinline__ uint64_t pack_key(float key, int e) {
   const uint32_t u = static_cast<uint32_t>(total_order_key(key)) ^ 0x80000000u;
@@ -126,14 +123,14 @@ __device__ __forceinline__ void select_and_gate(const float (&logit)[NTOK][EPL],
     float w;
     if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
       float denom = 0.0f;
-      for (int k = 0; k < top_k; ++k) denom = denom + lane_value(my_v, k);
+      for (int k = 0; k < top_k; ++k) denom = denom + lane_bcast(my_v, k);
       denom = denom + 1e-9f;
       w = (my_v / denom) * rsf;
     } else {
-      const float m = lane_value(my_v, 0);
+      const float m = lane_bcast(my_v, 0);
       const float ex = exp_det(my_v - m);
       float denom = 0.0f;
-      for (int k = 0; k < top_k; ++k) denom = denom + lane_value(ex, k);
+      for (int k = 0; k < top_k; ++k) denom = denom + lane_bcast(ex, k);
       w = ex / denom;
     }
     if (store[q] && lane < top_k) {
