@@ -650,8 +650,10 @@ int check_plan_args(const int32_t* top_idx, int64_t tokens, int top_k, int n_exp
   HMOE_REQUIRE(tokens >= 0 && top_k >= 1, "%s: need tokens >= 0 and top_k >= 1", what);
   HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
                "%s: n_experts must be in [1, %d] (got %d)", what, kMaxExperts, n_experts);
-  HMOE_REQUIRE(capacity >= 1, "%s: capacity must be >= 1 (got %lld)", what, (long long)capacity);
   const int64_t rows = tokens * top_k;
+  // (no slots: hmoe_capacity gives 0 and the plan is all zeros)
+  HMOE_REQUIRE(capacity >= 1 || rows == 0, "%s: capacity must be >= 1 (got %lld)", what,
+               (long long)capacity);
   HMOE_REQUIRE(rows < (int64_t(1) << 31), "%s: T*K must fit in int32 (got %lld)", what,
                (long long)rows);
   HMOE_REQUIRE(counts && offsets, "%s: null pointer argument", what);

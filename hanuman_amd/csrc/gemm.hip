@@ -1363,8 +1363,8 @@ extern "C" int hmoe_grouped_gate_up_gather(const void* x, int64_t tokens, int to
   HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
                "grouped_gate_up_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
                n_experts);
-  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
-               "grouped_gate_up_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
+               "grouped_gate_up_gather: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)");
   HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
                     "grouped_gate_up_gather: d_model must be a multiple of %d (got %d)", kBK,
                     d_model);
@@ -1410,8 +1410,8 @@ extern "C" int hmoe_grouped_gate_up_raw_gather(const void* x, int64_t tokens, in
   HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
                "grouped_gate_up_raw_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
                n_experts);
-  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
-               "grouped_gate_up_raw_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
+               "grouped_gate_up_raw_gather: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)");
   HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
                     "grouped_gate_up_raw_gather: d_model must be a multiple of %d (got %d)", kBK,
                     d_model);
@@ -1456,8 +1456,8 @@ extern "C" int hmoe_grouped_gate_up_swiglu_bwd_gather(
   HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
                "grouped_gate_up_swiglu_bwd_gather: n_experts must be in [1, %d] (got %d)",
                kMaxExperts, n_experts);
-  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
-               "grouped_gate_up_swiglu_bwd_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
+               "grouped_gate_up_swiglu_bwd_gather: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)");
   HMOE_REQUIRE_CODE(d_model % kBK == 0 && d_model >= kBK, HMOE_ERR_UNSUPPORTED,
                     "grouped_gate_up_swiglu_bwd_gather: d_model must be a multiple of %d (got %d)",
                     kBK, d_model);
@@ -1569,8 +1569,8 @@ extern "C" int hmoe_grouped_gate_up_fp8_gather(const uint8_t* x_q, const float* 
   HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
                "grouped_gate_up_fp8_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
                n_experts);
-  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 1 && top_k >= 1,
-               "grouped_gate_up_fp8_gather: need rows_cap >= 0, tokens >= 1, top_k >= 1");
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
+               "grouped_gate_up_fp8_gather: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)");
   HMOE_REQUIRE_CODE(d_model % 128 == 0 && d_model >= 128, HMOE_ERR_UNSUPPORTED,
                     "grouped_gate_up_fp8_gather: d_model must be a multiple of 128 (got %d)",
                     d_model);
