@@ -6,9 +6,9 @@
 // sigmoid scores, the normalised routing distribution p and its entropy; it
 // accumulates p per expert and lse^2 / entropy per wave, then the four waves
 // are summed in a fixed order.  The chunk's per-sequence expert histogram is
-// counted in LDS.  Pass 2: one workgroup reduces the chunk partials in chunk
-// order into the four outputs.  Every float reduction has a fixed order, so
-// results are identical from run to run.
+// counted in LDS.  Pass 2: one workgroup reduces the chunk partials into the
+// four outputs.  Every float reduction has a fixed order, so results are
+// identical from run to run.
 #include "hmoe_common.h"
 
 namespace hmoe {
@@ -112,56 +112,87 @@ __global__ __launch_bounds__(256) void aux_chunk_kernel(const float* __restrict_
   }
 }
 
-// One workgroup of 256 threads.
-__global__ __launch_bounds__(256) void aux_final_kernel(const float* __restrict__ parts, int batch,
-                                                        int seq, int n_experts, int top_k,
-                                                        int chunks_per_seq,
-                                                        float* __restrict__ losses,
-                                                        float* __restrict__ expert_counts) {
-  __shared__ float bal_terms[kMaxN];
-  __shared__ float bal_seq[1024];
-  const int tid = threadIdx.x;
+// One workgroup of 1024 threads, every loop over the chunk partials spread
+// over the threads (the serial version was bound by one dependent load per
+// chunk).  z and entropy: thread t sums chunks t, t + 1024, ... in order, then
+// the wave sums and the 16 wave totals in order.  Balance: sequences in
+// rounds of G, one thread per (sequence, expert) summing that sequence's
+// chunks in order; per sequence its expert terms are summed in a fixed order
+// and the sequences in order.  Counts are exact integers (LDS atomics).  Every
+// float reduction has a fixed order.
+constexpr int kFinalThreads = 1024;
+
+__global__ __launch_bounds__(kFinalThreads) void aux_final_kernel(
+    const float* __restrict__ parts, int batch, int seq, int n_experts, int top_k,
+    int chunks_per_seq, float* __restrict__ losses, float* __restrict__ expert_counts) {
+  __shared__ int32_t cnt_e[kMaxN];
+  __shared__ float terms[kFinalThreads];
+  __shared__ float wtot[2][kFinalThreads / 64];
+  __shared__ float bal_round[kFinalThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t stride = part_stride(n_experts);
   const int nchunks = batch * chunks_per_seq;
-  // expert_counts[n] = sum over all chunks (exact integers).
-  for (int e = tid; e < n_experts; e += 256) {
-    int64_t cnt = 0;
-    for (int ch = 0; ch < nchunks; ++ch)
-      cnt += reinterpret_cast<const int32_t*>(parts + ch * stride)[n_experts + e];
-    expert_counts[e] = static_cast<float>(cnt);
+  for (int e = tid; e < n_experts; e += kFinalThreads) cnt_e[e] = 0;
+
+  float z = 0.0f, ent = 0.0f;
+  for (int ch = tid; ch < nchunks; ch += kFinalThreads) {
+    z += parts[ch * stride + 2 * n_experts];
+    ent += parts[ch * stride + 2 * n_experts + 1];
   }
-  // balance: per sequence b, N * sum_n (count/(S*K)) * (sum_s p / S).
-  for (int b = 0; b < batch; ++b) {
-    for (int e = tid; e < n_experts; e += 256) {
+  z = wave_sum(z);
+  ent = wave_sum(ent);
+  if (lane == 0) {
+    wtot[0][wave] = z;
+    wtot[1][wave] = ent;
+  }
+  __syncthreads();
+
+  // threads per sequence: n_experts rounded up to whole waves
+  const int tps = (n_experts + 63) / 64 * 64;
+  const int per_round = kFinalThreads / tps;
+  const int bl = tid / tps, e = tid % tps;
+  float bal = 0.0f;
+  for (int b0 = 0; b0 < batch; b0 += per_round) {
+    const int b = b0 + bl;
+    float term = 0.0f;
+    if (bl < per_round && b < batch && e < n_experts) {
       float psum = 0.0f;
-      int64_t cnt = 0;
+      int32_t cnt = 0;
+#pragma unroll 8
       for (int c = 0; c < chunks_per_seq; ++c) {
         const float* pp = parts + static_cast<int64_t>(b * chunks_per_seq + c) * stride;
         psum += pp[e];
         cnt += reinterpret_cast<const int32_t*>(pp)[n_experts + e];
       }
+      atomicAdd(&cnt_e[e], cnt);
       const float frac = static_cast<float>(cnt) / static_cast<float>(seq * top_k);
-      bal_terms[e] = frac * (psum / static_cast<float>(seq));
+      term = frac * (psum / static_cast<float>(seq));
+    }
+    terms[tid] = term;
+    __syncthreads();
+    // the first wave of each sequence's group sums its expert terms
+    if (bl < per_round && e < 64) {
+      float acc = 0.0f;
+      for (int k = e; k < tps; k += 64) acc += terms[bl * tps + k];
+      acc = wave_sum(acc);
+      if (e == 0) bal_round[bl] = static_cast<float>(n_experts) * acc;
     }
     __syncthreads();
-    if (tid == 0) {
-      float acc = 0.0f;
-      for (int e = 0; e < n_experts; ++e) acc += bal_terms[e];
-      if (b < 1024) bal_seq[b] = static_cast<float>(n_experts) * acc;
-    }
+    if (tid == 0)
+      for (int q = 0; q < per_round && b0 + q < batch; ++q) bal += bal_round[q];
     __syncthreads();
   }
+  for (int k = tid; k < n_experts; k += kFinalThreads) expert_counts[k] = static_cast<float>(cnt_e[k]);
   if (tid == 0) {
-    float z = 0.0f, ent = 0.0f, bal = 0.0f;
-    for (int ch = 0; ch < nchunks; ++ch) {
-      z += parts[ch * stride + 2 * n_experts];
-      ent += parts[ch * stride + 2 * n_experts + 1];
+    float zt = 0.0f, et = 0.0f;
+    for (int w = 0; w < kFinalThreads / 64; ++w) {
+      zt += wtot[0][w];
+      et += wtot[1][w];
     }
-    for (int b = 0; b < batch && b < 1024; ++b) bal += bal_seq[b];
     const float tokens = static_cast<float>(batch) * static_cast<float>(seq);
-    losses[0] = z / tokens;
+    losses[0] = zt / tokens;
     losses[1] = bal / static_cast<float>(batch);
-    losses[2] = ent / tokens;
+    losses[2] = et / tokens;
   }
 }
 
@@ -317,8 +348,8 @@ extern "C" int hmoe_router_aux(const float* logits, const int32_t* top_idx, int 
   else
     hipLaunchKernelGGL(aux_chunk_kernel<4>, grid, dim3(256), 0, s, logits, top_idx, seq, n_experts, top_k, cps, parts);
   if (int rc = check_launch("router_aux/chunk")) return rc;
-  hipLaunchKernelGGL(aux_final_kernel, dim3(1), dim3(256), 0, s, parts, batch, seq, n_experts, top_k,
-                     cps, losses, expert_counts);
+  hipLaunchKernelGGL(aux_final_kernel, dim3(1), dim3(kFinalThreads), 0, s, parts, batch, seq,
+                     n_experts, top_k, cps, losses, expert_counts);
   return check_launch("router_aux/final");
 }
 
