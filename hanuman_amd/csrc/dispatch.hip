@@ -62,9 +62,21 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(int32_t* __restrict__ h
   const int L = (nblk + P - 1) / P;
   const int b0 = j * L;
   const int b1 = b0 + L < nblk ? b0 + L : nblk;
+  // Eight loads in flight per lane (a long block range otherwise costs one
+  // dependent global load per block).
+  constexpr int kU = 8;
   int32_t part = 0;
-  if (e < n_experts)
-    for (int b = b0; b < b1; ++b) part += hist[static_cast<int64_t>(b) * n_experts + e];
+  if (e < n_experts) {
+    int b = b0;
+    for (; b + kU <= b1; b += kU) {
+      int32_t v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = hist[static_cast<int64_t>(b + u) * n_experts + e];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) part += v[u];
+    }
+    for (; b < b1; ++b) part += hist[static_cast<int64_t>(b) * n_experts + e];
+  }
   // Inclusive scan of the partial sums within the group (P lanes, aligned).
   int32_t incl = part;
   for (int off = 1; off < P; off <<= 1) {
@@ -74,7 +86,18 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(int32_t* __restrict__ h
   const int32_t total = __shfl(incl, P - 1, P);
   if (e < n_experts) {
     int32_t run = incl - part;  // exclusive base of block b0
-    for (int b = b0; b < b1; ++b) {
+    int b = b0;
+    for (; b + kU <= b1; b += kU) {
+      int32_t v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = hist[static_cast<int64_t>(b + u) * n_experts + e];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        hist[static_cast<int64_t>(b + u) * n_experts + e] = run;
+        run += v[u];
+      }
+    }
+    for (; b < b1; ++b) {
       const int64_t idx = static_cast<int64_t>(b) * n_experts + e;
       const int32_t c = hist[idx];
       hist[idx] = run;
