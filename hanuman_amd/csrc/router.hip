@@ -2,8 +2,9 @@
 //
 // Logits are float32 roundings of float64 sums taken in ascending d from +0.0
 // (see router_kernel for how the float64 matrix cores keep that order).
-// Top-k is K rounds of a wave-wide max over a packed (totalOrder key,
-// ~expert) 64-bit value, so equal keys resolve to the lower expert index.
+// Top-k is K rounds of a wave-wide max over the totalOrder keys, each
+// followed by a ballot of the lanes at the maximum whose lowest expert wins,
+// so equal keys resolve to the lower expert index.
 #include <atomic>
 
 #include "hmoe_common.h"
@@ -14,14 +15,11 @@ namespace {
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 // max(v, v of the lane DPP control CTRL names), in the rows ROW_MASK enables
-// (other lanes keep v).  Both 32-bit halves move with the same control.
+// (other lanes keep v).
 template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
-  const int lo = static_cast<int>(static_cast<uint32_t>(v));
-  const int hi = static_cast<int>(static_cast<uint32_t>(v >> 32));
-  const uint32_t tlo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false));
-  const uint32_t thi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false));
-  const uint64_t t = (static_cast<uint64_t>(thi) << 32) | tlo;
+__device__ __forceinline__ int32_t dpp_max_i32(int32_t v) {
+  const int32_t t = ROW_MASK == 0xF ? __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false)
+                                    : __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
   return t > v ? t : v;
 }
 
@@ -32,37 +30,30 @@ __device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
 // rows 1 and 3 and row_bcast31 into rows 2 and 3 bring the wave's maximum to
 // lane 63, which is read out.
 template <int NTOK>
-__device__ __forceinline__ void wave_max_u64(uint64_t (&v)[NTOK]) {
+__device__ __forceinline__ void wave_max_i32(int32_t (&v)[NTOK]) {
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_u64<0xB1>(v[q]);
+  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_i32<0xB1>(v[q]);
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_u64<0x4E>(v[q]);
+  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_i32<0x4E>(v[q]);
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_u64<0x141>(v[q]);
+  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_i32<0x141>(v[q]);
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_u64<0x140>(v[q]);
+  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_i32<0x140>(v[q]);
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_u64<0x142, 0xA>(v[q]);
+  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_i32<0x142, 0xA>(v[q]);
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_u64<0x143, 0xC>(v[q]);
+  for (int q = 0; q < NTOK; ++q) v[q] = dpp_max_i32<0x143, 0xC>(v[q]);
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) {
-    const uint32_t lo = static_cast<uint32_t>(
-        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v[q])), 63));
-    const uint32_t hi = static_cast<uint32_t>(
-        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v[q] >> 32)), 63));
-    v[q] = (static_cast<uint64_t>(hi) << 32) | lo;
-  }
-}
-
-
-__device__ __forceinline__ uint64_t pack_key(float key, int e) {
-  const uint32_t u = static_cast<uint32_t>(total_order_key(key)) ^ 0x80000000u;
-  return (static_cast<uint64_t>(u) << 32) | static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(e));
+  for (int q = 0; q < NTOK; ++q) v[q] = __builtin_amdgcn_readlane(v[q], 63);
 }
 
 // Selection + gates for NTOK tokens whose logits are spread over the wave
 // (lane owns experts lane + 64*j); the tokens' reduction chains interleave.
+// Round k takes the wave maximum of the live totalOrder keys, then the
+// lowest expert holding it: the first j (ascending) whose ballot of live
+// entries at the maximum is non-empty, and that ballot's lowest lane -- the
+// lower-index tie-break of lax.top_k.  The winner's value is read from its
+// lane, and the gate denominators are summed from those values in k order.
 // Lane k < K writes slot k of every token q with store[q].
 template <int EPL, int NTOK>
 __device__ __forceinline__ void select_and_gate(const float (&logit)[NTOK][EPL],
@@ -73,65 +64,85 @@ __device__ __forceinline__ void select_and_gate(const float (&logit)[NTOK][EPL],
                                                 float* const (&gates_row)[NTOK]) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
+  constexpr int32_t kDead = INT32_MIN;
   float val[NTOK][EPL];  // value the gate is built from: sigmoid score or logit
-  uint64_t packed[NTOK][EPL];
+  int32_t key[NTOK][EPL];
+  uint64_t dead[NTOK][EPL];  // lanes whose entry j is retired or past n_experts (uniform)
 #pragma unroll
   for (int q = 0; q < NTOK; ++q)
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
       const int e = lane + 64 * j;
-      float key = logit[q][j];
+      float kf = logit[q][j];
       if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
         const float sg = sigmoid_det(logit[q][j]);
         val[q][j] = sg;
-        key = sg + ((bias != nullptr && e < n_experts) ? bias[e] : 0.0f);
+        kf = sg + ((bias != nullptr && e < n_experts) ? bias[e] : 0.0f);
       } else {
         val[q][j] = logit[q][j];
       }
-      packed[q][j] = e < n_experts ? pack_key(key, e) : 0ull;
+      key[q][j] = e < n_experts ? total_order_key(kf) : kDead;
+      dead[q][j] = __builtin_amdgcn_ballot_w64(e >= n_experts);
     }
   int my_e[NTOK];
+  float my_v[NTOK], denom[NTOK], vmax[NTOK];
 #pragma unroll
-  for (int q = 0; q < NTOK; ++q) my_e[q] = 0;
+  for (int q = 0; q < NTOK; ++q) {
+    my_e[q] = 0;
+    my_v[q] = 0.0f;
+    denom[q] = 0.0f;
+    vmax[q] = 0.0f;
+  }
   for (int k = 0; k < top_k; ++k) {
-    uint64_t best[NTOK];
+    int32_t best[NTOK];
 #pragma unroll
     for (int q = 0; q < NTOK; ++q) {
-      best[q] = packed[q][0];
+      best[q] = key[q][0];
 #pragma unroll
-      for (int j = 1; j < EPL; ++j) best[q] = packed[q][j] > best[q] ? packed[q][j] : best[q];
+      for (int j = 1; j < EPL; ++j) best[q] = key[q][j] > best[q] ? key[q][j] : best[q];
     }
-    wave_max_u64<NTOK>(best);
+    wave_max_i32<NTOK>(best);
 #pragma unroll
     for (int q = 0; q < NTOK; ++q) {
-      const int e_win = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best[q]));
-      if (lane == k) my_e[q] = e_win;
+      uint64_t mask = 0;
+      int jw = 0;
 #pragma unroll
-      for (int j = 0; j < EPL; ++j)
-        if (lane + 64 * j == e_win) packed[q][j] = 0ull;
+      for (int j = 0; j < EPL; ++j) {
+        const uint64_t mj = __builtin_amdgcn_ballot_w64(key[q][j] == best[q]) & ~dead[q][j];
+        if (mask == 0 && mj != 0) {
+          mask = mj;
+          jw = j;
+        }
+      }
+      // mask is non-empty: top_k <= n_experts keeps a live entry at the maximum
+      const int lw = __builtin_ctzll(mask);
+      float v_win = 0.0f;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        if (j == jw) {
+          v_win = lane_bcast(val[q][j], lw);
+          if (lane == lw) key[q][j] = kDead;
+          dead[q][j] |= 1ull << lw;
+        }
+      }
+      if (lane == k) {
+        my_e[q] = lw + 64 * jw;
+        my_v[q] = v_win;
+      }
+      if (mode == HMOE_ROUTE_SIGMOID_BIAS) denom[q] = denom[q] + v_win;
+      else if (k == 0) vmax[q] = v_win;
     }
   }
 #pragma unroll
   for (int q = 0; q < NTOK; ++q) {
-    // Fetch the selected experts' values from their owner lanes.
-    float my_v = 0.0f;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const float v = __shfl(val[q][j], my_e[q] & 63, 64);
-      if ((my_e[q] >> 6) == j) my_v = v;
-    }
     float w;
     if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
-      float denom = 0.0f;
-      for (int k = 0; k < top_k; ++k) denom = denom + lane_bcast(my_v, k);
-      denom = denom + 1e-9f;
-      w = (my_v / denom) * rsf;
+      w = (my_v[q] / (denom[q] + 1e-9f)) * rsf;
     } else {
-      const float m = lane_bcast(my_v, 0);
-      const float ex = exp_det(my_v - m);
-      float denom = 0.0f;
-      for (int k = 0; k < top_k; ++k) denom = denom + lane_bcast(ex, k);
-      w = ex / denom;
+      // exp of each slot in its lane, summed in k order
+      const float ex = exp_det(my_v[q] - vmax[q]);
+      for (int k = 0; k < top_k; ++k) denom[q] = denom[q] + lane_bcast(ex, k);
+      w = ex / denom[q];
     }
     if (store[q] && lane < top_k) {
       top_idx_row[q][lane] = my_e[q];

@@ -116,6 +116,38 @@ def test_router_from_logits_ties_and_signed_zero(gpu):
     assert host(idx)[1].tolist() == list(range(Kk))      # all equal -> lowest indices
 
 
+@pytest.mark.parametrize("N", [100, 200])
+def test_router_from_logits_ties_across_lanes(gpu, N):
+    """Experts past 64 share lanes with lower ones (lane = expert % 64): equal
+    keys on two experts of one lane, or on a low expert of a high lane and a
+    high expert of a low lane, must still go to the lower expert index."""
+    rng = np.random.default_rng(N)
+    T, Kk = 700, 8
+    logits = rng.integers(-2, 3, size=(T, N)).astype(np.float32)   # many exact ties
+    logits[0] = 0.0                        # all tied: the lowest K indices
+    logits[1] = 0.0
+    logits[1, [5, 69, 133 % N]] = 3.0      # one lane, several j
+    logits[2] = 0.0
+    logits[2, [70, 6]] = 2.0               # expert 6 (lane 6) before 70 (lane 6, j=1)
+    logits[3] = -1.0
+    logits[3, [N - 1, 63, 64]] = 1.0       # the last expert, lane 63 and lane 0 of j=1
+    for mode in (_lib.ROUTE_SOFTMAX, _lib.ROUTE_SIGMOID_BIAS):
+        bias = np.zeros(N, np.float32) if mode == _lib.ROUTE_SIGMOID_BIAS else None
+        if mode == _lib.ROUTE_SOFTMAX:
+            idx_ref, g_ref = O.route_softmax(logits, Kk)
+        else:
+            idx_ref, g_ref, _ = O.route_sigmoid(logits, bias, Kk, 2.5)
+        idx, g = K.router_from_logits(dev_f32(logits, gpu),
+                                      dev_f32(bias, gpu) if bias is not None else None, Kk, mode, 2.5)
+        torch.cuda.synchronize()
+        assert_bits_equal(host(idx), idx_ref, f"top_idx mode {mode}")
+        assert_bits_equal(host(g), g_ref, f"gates mode {mode}")
+    got = host(idx)
+    assert got[0].tolist() == list(range(Kk))
+    assert got[2][:2].tolist() == [6, 70]
+    assert got[3][:3].tolist() == [63, 64, N - 1]
+
+
 @pytest.mark.parametrize("T,N,Kk,mode", [(1003, 200, 6, "sigmoid"), (77, 100, 4, "softmax"),
                                          (18, 16, 2, "softmax")])
 def test_router_from_logits_ragged(gpu, T, N, Kk, mode):
