@@ -124,3 +124,17 @@ def test_pack_cache_rebuilds_on_identity_or_version():
     assert len(builds) == 3
     c.get((a2, b), lambda: builds.append(1) or len(builds))
     assert len(builds) == 3
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; asking for more exits with a message instead
+    of reporting a figure for a configuration it did not run."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], cwd=root,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
+    assert r.stdout.strip() == ""   # no JSON line
