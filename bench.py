@@ -11,7 +11,10 @@ input resident in HBM before the timed region.  One JSON line on stdout:
              dense bf16 (or fp8) MFMA peak; traffic = its measured HBM bytes per
              launch (profiles/hbm_traffic.json)
   grouped_gemm  gate/up + down together (6*R_kept*D*F FLOP)
-  kernels    every stage's HIP-event time and roofline fraction
+  kernels    every stage's HIP-event time and roofline fraction, and its fraction of
+             the ceiling measured on the box (frac_of_ceiling)
+  ceilings   a 1 GiB device copy and the vendor library's dense bf16 GEMM (8192^3),
+             timed in the same process after the timed steps
   cpu_baseline  the NumPy float32 restatement of the layer (oracle/) timed on
              this host's cores on up to 16384 tokens of the same workload (all of
              the headline workload)
@@ -98,6 +101,49 @@ def measured_traffic(workload: str) -> dict:
     except (OSError, ValueError):
         return {}
     return {k: v["total"] for k, v in data.get("workloads", {}).get(workload, {}).items()}
+
+
+def measured_ceilings(dev) -> dict:
+    """Ceilings measured on this GPU in this process, outside every timed
+    region: a 1 GiB device-to-device copy (GB/s counting the bytes read and
+    written) and the vendor library's dense bf16 GEMM at 8192^3 on random
+    operands (torch.matmul, hipBLASLt).  Each runs back to back for 200 ms,
+    then three batches of back-to-back calls are timed between two events;
+    the median batch gives the rate."""
+    import torch
+
+    def batch_ms(fn, calls):
+        t_end = time.perf_counter() + 0.2
+        while time.perf_counter() < t_end:
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(3):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(calls):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) / calls)
+        return float(np.median(times))
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    copy_ms = batch_ms(lambda: dst.copy_(src), 10)
+    del src, dst
+    n = 8192
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    gemm_ms = batch_ms(lambda: torch.matmul(a, b), 20)
+    del a, b
+    torch.cuda.empty_cache()
+    return {"hbm_copy_gbs": round(2 * (1 << 30) / (copy_ms / 1e3) / 1e9, 1),
+            "dense_bf16_gemm_tflops": round(2 * n ** 3 / (gemm_ms / 1e3) / 1e12, 1),
+            "how": "1 GiB device copy (bytes read + written), 10 back to back, and torch.matmul "
+                   "bf16 8192^3 on random operands (hipBLASLt), 20 back to back; 200 ms of "
+                   "spin-up each, median of 3 batches, same process, after the timed steps"}
 
 
 def cpu_baseline(wl_name: str, sample_tokens: int, seed: int) -> dict:
@@ -317,6 +363,7 @@ def main():
         ev_d[1].record()
         torch.cuda.synchronize()
         dispatch_ms = ev_d[0].elapsed_time(ev_d[1]) / args.steps
+    ceilings = measured_ceilings(dev)
     kernels = {}
     for st in stages:
         kind, amount, peak = work[st]
@@ -324,18 +371,22 @@ def main():
         if kind == "hbm":
             ach = amount / t / 1e9
             kernels[st] = {"ms": round(stage_ms[st], 4), "bound": "hbm", "achieved": round(ach, 1),
-                           "unit": "GB/s", "peak": peak, "frac": round(ach / peak, 4), "bytes": amount}
+                           "unit": "GB/s", "peak": peak, "frac": round(ach / peak, 4), "bytes": amount,
+                           "frac_of_ceiling": round(ach / ceilings["hbm_copy_gbs"], 4)}
         else:
             ach = amount / t / 1e12
             kernels[st] = {"ms": round(stage_ms[st], 4), "bound": kind, "achieved": round(ach, 1),
                            "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4),
                            "flop": amount}
+            if peak == BF16_PEAK_TFLOPS:
+                kernels[st]["frac_of_ceiling"] = round(ach / ceilings["dense_bf16_gemm_tflops"], 4)
     if dispatch_ms is not None:
         kind, amount, peak = work["permute"]
         ach = amount / (dispatch_ms / 1e3) / 1e9
         kernels["dispatch_permute"] = {
             "ms": round(dispatch_ms, 4), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
             "peak": peak, "frac": round(ach / peak, 4), "bytes": amount,
+            "frac_of_ceiling": round(ach / ceilings["hbm_copy_gbs"], 4),
             "note": "hmoe_permute_rows on the step's plan, timed after the layer and outside "
                     "its total (the layer fuses the gather into the gate/up GEMM)"}
     tokens_per_s = wl.tokens / (ms_per_step / 1e3)
@@ -409,6 +460,7 @@ def main():
                      "standalone hmoe_permute_rows on the same plan, timed outside the layer "
                      "total") if fused else "hmoe_permute_rows",
         "grouped_gemm_mfma_util": grouped_gemm["frac"] if grouped_gemm else None,
+        "ceilings": ceilings,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
