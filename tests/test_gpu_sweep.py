@@ -1,0 +1,95 @@
+"""Seeded sweep of small random layer shapes through the C ABI (needs an MI355X).
+
+Each case draws its own shape (tokens, d_model, experts, top-k, d_ff), routing
+mode (softmax, or sigmoid with a bias and a scaling factor), capacity factor
+(from heavy drops to none) and weight scale.  Routing (logits, indices, gates)
+and the dispatch plan (counts, offsets, slot map, permutation, keep mask) must
+be bit-exact against the oracle; the layer output of the bf16 path (router,
+plan, gathering gate/up GEMM with the SwiGLU epilogue, down GEMM, combine)
+must be within the bf16 tolerance of the oracle's float32 expert pass on the
+oracle's plan.  Shapes stay small so that the oracle's float64 router runs in
+well under a second per case.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from hanuman_amd import _lib
+from hanuman_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+N_CASES = 24
+
+
+def host(t):
+    return t.float().cpu().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    if a.dtype == np.float32:
+        a, b = a.view(np.uint32), np.asarray(b, np.float32).view(np.uint32)
+    return a.shape == b.shape and np.array_equal(a, b)
+
+
+def draw_case(i):
+    rng = np.random.default_rng(1000 + i)
+    T = int(rng.integers(1, 1200))
+    D = 256 * int(rng.integers(1, 3))             # multiples of the 256-column output tile
+    N = int(rng.choice([1, 3, 8, 17, 64, 70, 96]))
+    Kk = int(rng.integers(1, min(N, 8) + 1))
+    F = 128 * int(rng.integers(1, 5))
+    mode = "softmax" if rng.random() < 0.5 else "sigmoid"
+    cf = [None, 0.5, 1.0, 1.25, 2.0][int(rng.integers(0, 5))]
+    wstd = float(rng.choice([0.02, 0.2]))
+    return rng, T, D, N, Kk, F, mode, cf, wstd
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_layer_matches_oracle(gpu, i):
+    rng, T, D, N, Kk, F, mode, cf, wstd = draw_case(i)
+    print(f"sweep case {i}: T={T} D={D} N={N} K={Kk} F={F} {mode} cf={cf} wstd={wstd}", flush=True)
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    router_w = (wstd * rng.standard_normal((D, N))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32) if mode == "sigmoid" else None
+    rsf = 2.5 if mode == "sigmoid" else 1.0
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    xt = dev(x).to(torch.bfloat16)
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    logits, idx, gates = K.router(xt, dev(router_w), dev(bias) if bias is not None else None, Kk,
+                                  m, rsf)
+    cap = K.capacity(T, Kk, N, cf)
+    plan = K.dispatch_plan(idx, N, cap)
+    h = K.grouped_gate_up_gather(xt, plan, K.pack_gate_up(dev(wg), dev(wu)))
+    ys = K.grouped_down(h, plan.offsets, K.pack_down(dev(wd)))
+    out = K.combine(ys, plan, gates, None, torch.float32)
+    torch.cuda.synchronize()
+
+    ref_logits = O.router_logits(x, router_w)
+    if mode == "softmax":
+        ref_idx, ref_gates = O.route_softmax(ref_logits, Kk)
+    else:
+        ref_idx, ref_gates, _ = O.route_sigmoid(ref_logits, bias, Kk, rsf)
+    assert cap == O.capacity_of(T, Kk, N, cf)
+    ref_plan = O.dispatch_plan(ref_idx, N, cap)
+    assert bits_equal(host(logits), ref_logits), "logits"
+    assert bits_equal(host(idx), ref_idx), "top_idx"
+    assert bits_equal(host(gates), ref_gates), "gates"
+    for k in ("counts", "offsets", "slot_pos", "perm_src", "keep"):
+        assert np.array_equal(host(getattr(plan, k)), ref_plan[k]), k
+    xs = O.permute_rows(x, ref_plan["perm_src"], Kk)
+    ys_ref = O.expert_ffn(xs, ref_plan["offsets"], wg, wu, wd, precision="fp32")
+    ref = O.combine(ys_ref, ref_plan["slot_pos"], ref_gates, T, Kk, ys_dtype="bf16")
+    kept = int(ref_plan["offsets"][-1])
+    if kept == 0:
+        assert not np.any(host(out)), "a layer with every slot dropped returns zeros"
+        return
+    err = O.normwise_rel_err(host(out), ref)
+    print(f"  kept {kept} of {T * Kk} slots, output normwise err {err:.2e}", flush=True)
+    assert err < BF16_TOL
