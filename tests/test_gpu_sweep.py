@@ -7,8 +7,9 @@ and the dispatch plan (counts, offsets, slot map, permutation, keep mask) must
 be bit-exact against the oracle; the layer output of the bf16 path (router,
 plan, gathering gate/up GEMM with the SwiGLU epilogue, down GEMM, combine)
 must be within the bf16 tolerance of the oracle's float32 expert pass on the
-oracle's plan.  Shapes stay small so that the oracle's float64 router runs in
-well under a second per case.
+oracle's plan.  The e4m3 expert path is swept the same way against the
+oracle's e4m3 emulation.  Shapes stay small so that the oracle's float64
+router runs in well under a second per case.
 """
 import numpy as np
 import pytest
@@ -93,3 +94,59 @@ def test_random_layer_matches_oracle(gpu, i):
     err = O.normwise_rel_err(host(out), ref)
     print(f"  kept {kept} of {T * Kk} slots, output normwise err {err:.2e}", flush=True)
     assert err < BF16_TOL
+
+
+FP8_TOL = 5e-2
+N_FP8_CASES = 12
+
+
+@pytest.mark.parametrize("i", range(N_FP8_CASES))
+def test_random_fp8_layer_matches_oracle(gpu, i):
+    """The e4m3 expert path on random shapes: routing, plan and the per-token
+    codes and scales of x bit-exact; the bf16 output within 1e-2 of the
+    oracle's e4m3 emulation and within 5e-2 of the float32 layer on the
+    dequantised weights."""
+    rng, T, D, N, Kk, F, mode, cf, wstd = draw_case(500 + i)
+    print(f"fp8 sweep case {i}: T={T} D={D} N={N} K={Kk} F={F} {mode} cf={cf} wstd={wstd}",
+          flush=True)
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    router_w = (wstd * rng.standard_normal((D, N))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32) if mode == "sigmoid" else None
+    rsf = 2.5 if mode == "sigmoid" else 1.0
+    wg, wu = (0.02 * rng.standard_normal((2, N, D, F))).astype(np.float32)
+    wd = (0.02 * rng.standard_normal((N, F, D))).astype(np.float32)
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    xt = dev(x).to(torch.bfloat16)
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    logits, idx, gates = K.router(xt, dev(router_w), dev(bias) if bias is not None else None, Kk,
+                                  m, rsf)
+    plan = K.dispatch_plan(idx, N, K.capacity(T, Kk, N, cf))
+    fgu, sgu = K.pack_fp8_gate_up(dev(wg), dev(wu))
+    fd, sd = K.pack_fp8_down(dev(wd))
+    x_q, x_s = K.quantize_rows_fp8(xt)
+    h8 = K.grouped_gate_up_fp8_gather(x_q, x_s, plan, fgu, sgu)
+    h_q, h_s = K.quantize_rows_fp8(h8, plan.offsets)
+    ys8 = K.grouped_down_fp8(h_q, h_s, plan.offsets, fd, sd)
+    out = K.combine(ys8, plan, gates, None, torch.bfloat16)
+    torch.cuda.synchronize()
+
+    params = {"router": router_w, "expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd}
+    if bias is not None:
+        params["bias"] = bias
+    kw = dict(top_k=Kk, routing=mode, routed_scaling_factor=rsf, capacity_factor=cf)
+    r8 = O.moe_forward(x, params, expert="swiglu_fp8", out_dtype="bf16", **kw)
+    ref = O.moe_forward(x, {**params, **O.dequantized_weights(r8["fp8"])}, precision="fp32", **kw)
+    assert bits_equal(host(logits), r8["logits"]), "logits"
+    assert bits_equal(host(idx), r8["top_idx"]), "top_idx"
+    assert bits_equal(host(gates), r8["gates"]), "gates"
+    for k in ("counts", "offsets", "slot_pos", "perm_src", "keep"):
+        assert np.array_equal(host(getattr(plan, k)), r8["plan"][k]), k
+    assert np.array_equal(x_q.cpu().numpy(), r8["x_q"]), "x codes"
+    assert bits_equal(host(x_s), r8["x_s"]), "x scales"
+    got = host(out)
+    err_emul = O.normwise_rel_err(got, r8["out"])
+    err = O.normwise_rel_err(got, ref["out"])
+    print(f"  output normwise err {err:.2e} (vs the e4m3 emulation {err_emul:.2e})", flush=True)
+    assert err_emul < 1e-2
+    assert err < FP8_TOL
