@@ -150,3 +150,88 @@ def test_random_fp8_layer_matches_oracle(gpu, i):
     print(f"  output normwise err {err:.2e} (vs the e4m3 emulation {err_emul:.2e})", flush=True)
     assert err_emul < 1e-2
     assert err < FP8_TOL
+
+
+N_BWD_CASES = 8
+
+
+@pytest.mark.parametrize("i", range(N_BWD_CASES))
+def test_random_module_backward_matches_oracle(gpu, i):
+    """MoE.__call__ under torch autograd on random shapes (with 1-2 shared
+    experts, the z and balance losses in the loss): every gradient against the
+    bf16-mode VJP oracle fed with the forward's own routing, normwise 2e-2."""
+    from hanuman_amd.moe import MoE
+    from oracle import moe_backward as B
+
+    rng = np.random.default_rng(2000 + i)
+    Bq = int(rng.integers(1, 4))
+    Sq = int(rng.integers(16, 300))
+    D = 256 * int(rng.integers(1, 3))
+    F = 256 * int(rng.integers(1, 3))    # the bf16 backward's dh GEMM takes whole 256-column tiles
+    N = int(rng.choice([2, 8, 17, 64, 70]))
+    Kk = int(rng.integers(1, min(N, 8) + 1))
+    n_shared = int(rng.integers(1, 3))   # the reference divides by the count (moe.py:168)
+    cf = [None, 0.75, 1.25][int(rng.integers(0, 3))]
+    seed = int(rng.integers(0, 1 << 30))
+    print(f"bwd sweep case {i}: B={Bq} S={Sq} D={D} F={F} N={N} K={Kk} shared={n_shared} cf={cf}",
+          flush=True)
+    m = MoE(D, F, N, Kk, n_shared, 0.05, 2.5, torch.bfloat16, rngs=seed, device=gpu,
+            capacity_factor=cf)
+    m.bias.value.copy_(torch.from_numpy((0.02 * rng.standard_normal(N)).astype(np.float32)))
+    names = ["router", "expert_w_gate", "expert_w_up", "expert_w_down",
+             "shared_w_gate", "shared_w_up", "shared_w_down"]
+    for n in names:
+        getattr(m, n).value.requires_grad_(True)
+    x = torch.from_numpy(rng.standard_normal((Bq, Sq, D)).astype(np.float32)).to(gpu)
+    x = x.to(torch.bfloat16).requires_grad_(True)
+    dy = torch.from_numpy(rng.standard_normal((Bq, Sq, D)).astype(np.float32)).to(gpu)
+    c_z, c_b = 0.37, 0.81
+    out, aux = m(x)
+    (((out * dy).sum()) + c_z * aux["router_z_loss"] + c_b * aux["balance_loss"]).backward()
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        _, _, _, sv = m._forward(x.detach(), save=True)
+    T = Bq * Sq
+    idx = host(sv["top_idx"])
+    ref_plan = O.dispatch_plan(idx, N, O.capacity_of(T, Kk, N, cf))
+    xn = host(x.detach()).reshape(T, D)
+    p = {n: getattr(m, n).value.detach().float().cpu().numpy() for n in names}
+    ref_fwd = {"logits": host(sv["logits"]), "top_idx": idx, "gates": host(sv["gates"]),
+               "plan": ref_plan, "xs": O.permute_rows(xn, ref_plan["perm_src"], Kk),
+               "ys": host(sv["ys"])}
+    ref = B.moe_backward(xn, p, host(dy).reshape(T, D), ref_fwd, routing="sigmoid", rsf=2.5,
+                         precision="bf16", n_shared=n_shared, batch_shape=(Bq, Sq),
+                         d_aux=(c_z, c_b, 0.0))
+    pairs = [("dx", x.grad, "dx"), ("d_router", m.router.value.grad, "d_router"),
+             ("dWg", m.expert_w_gate.value.grad, "dWg"), ("dWu", m.expert_w_up.value.grad, "dWu"),
+             ("dWd", m.expert_w_down.value.grad, "dWd"),
+             ("dWg_shared", m.shared_w_gate.value.grad, "dWg_shared"),
+             ("dWu_shared", m.shared_w_up.value.grad, "dWu_shared"),
+             ("dWd_shared", m.shared_w_down.value.grad, "dWd_shared")]
+    for name, got, key in pairs:
+        want = ref[key]
+        if not np.any(want):
+            # an expert set that received no kept rows has an exactly zero gradient
+            assert not torch.any(got), name
+            continue
+        err = O.normwise_rel_err(host(got).reshape(np.shape(want)), want)
+        print(f"  {name}: normwise {err:.2e}", flush=True)
+        assert err < 2e-2, (name, err)
+
+
+def test_module_backward_needs_d_ff_multiple_of_256(gpu):
+    """d_ff = 384 runs forward (gate/up columns come in 256-column tiles of
+    the packed [gate | up] pairs, so d_ff % 128 suffices), and the backward
+    refuses it with the library's error instead of computing on partial
+    tiles (its dh = d_ys Wd^T GEMM has d_ff output columns)."""
+    from hanuman_amd._lib import HmoeError
+    from hanuman_amd.moe import MoE
+
+    m = MoE(256, 384, 8, 2, 1, 0.05, 2.5, torch.bfloat16, rngs=3, device=gpu)
+    m.expert_w_gate.value.requires_grad_(True)
+    x = torch.randn(1, 64, 256, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    out, _ = m(x)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    with pytest.raises(HmoeError, match="multiple of 256"):
+        out.sum().backward()
