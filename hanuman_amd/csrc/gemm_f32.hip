@@ -20,7 +20,11 @@
 // one GEMM over [dg | du] (K = 2F).
 //
 // Tiles of 64 rows x 64 columns, one per workgroup of 4 waves (wave (wm, wn)
-// owns a 32 x 32 block); K runs in steps of 16 through LDS.  Row tiles are
+// owns a 32 x 32 block); K runs in steps of 16 through LDS.  A single-matrix
+// GEMM sums in two interleaved accumulator chains through two LDS stages,
+// each step's loads issued two steps ahead; the g/u GEMMs (two chains
+// already) load each step at its start through one stage, which keeps more
+// workgroups on a CU.  Row tiles are
 // numbered per expert segment (ceil(rows / 64) each), found from offsets by
 // each workgroup (an LDS scan over the experts); workgroups past the last
 // tile exit.  Rows past a segment are never stored.
@@ -55,10 +59,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_f32_kernel(
   __shared__ int32_t mstart[kF32MaxExperts + 1];
   __shared__ int32_t scan[256];
   // A tile [64 rows][16 k] and B tiles [16 k][64 n], +1 float of padding per
-  // row so that the operand reads below hit distinct banks
-  __shared__ float sa[kF32Tile][kF32K + 1];
-  __shared__ float sb0[kF32K][kF32Tile + 1];
-  __shared__ float sb1[kDual ? kF32K : 1][kF32Tile + 1];
+  // row so that the operand reads below hit distinct banks; two stages for a
+  // single matrix, one for g and u (whose kernels keep more workgroups per CU)
+  constexpr int kStages = kDual ? 1 : 2;
+  __shared__ float sa[kStages][kF32Tile][kF32K + 1];
+  __shared__ float sb0[kStages][kF32K][kF32Tile + 1];
+  __shared__ float sb1[1][kDual ? kF32K : 1][kF32Tile + 1];
   const int tid = threadIdx.x;
   // per-expert row-tile starts (exclusive scan of ceil(rows_e / 64))
   const int per = (n_experts + 255) / 256;
@@ -105,11 +111,14 @@ __global__ __launch_bounds__(256) void grouped_gemm_f32_kernel(
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, hi2 = lane >> 5;
-  f32x16 acc0, acc1;
+  // A single matrix sums in two accumulator chains (the K pairs of a step
+  // alternate between them), added before the epilogue.
+  f32x16 acc0, acc1, acc0b;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     acc0[r] = 0.0f;
     acc1[r] = 0.0f;
+    acc0b[r] = 0.0f;
   }
   // loader: A 64 x 16 = 1024 floats, 4 per thread (row tid / 4, k 4 (tid % 4)
   // .. +4); B 16 x 64, 4 per thread: k tid / 16, n 4 (tid % 16) .. +4, or,
@@ -122,36 +131,70 @@ __global__ __launch_bounds__(256) void grouped_gemm_f32_kernel(
     return BT ? *reinterpret_cast<const f32x4*>(be + static_cast<int64_t>(n0 + b_n) * ksplit + kk0 + b_k)
               : *reinterpret_cast<const f32x4*>(be + static_cast<int64_t>(kk0 + b_k) * ncols + n0 + b_n);
   };
-  for (int k0 = 0; k0 < kdim; k0 += kF32K) {
-    const f32x4 av = *reinterpret_cast<const f32x4*>(A + ar * kdim + k0 + a_k);
-    f32x4 bv0, bv1 = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 av, bv0, bv1 = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+    av = *reinterpret_cast<const f32x4*>(A + ar * kdim + k0 + a_k);
     if (kDual) {
       bv0 = load_b(be0, k0);
       bv1 = load_b(be1, k0);
     } else {
       bv0 = k0 < ksplit ? load_b(be0, k0) : load_b(be1, k0 - ksplit);  // uniform branch
     }
-    __syncthreads();
+  };
+  auto park = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      sa[a_r][a_k + q] = av[q];
+      sa[buf][a_r][a_k + q] = av[q];
       if (BT) {
-        sb0[b_k + q][b_n] = bv0[q];
-        if (kDual) sb1[b_k + q][b_n] = bv1[q];
+        sb0[buf][b_k + q][b_n] = bv0[q];
+        if (kDual) sb1[buf][b_k + q][b_n] = bv1[q];
       } else {
-        sb0[b_k][b_n + q] = bv0[q];
-        if (kDual) sb1[b_k][b_n + q] = bv1[q];
+        sb0[buf][b_k][b_n + q] = bv0[q];
+        if (kDual) sb1[buf][b_k][b_n + q] = bv1[q];
       }
     }
-    __syncthreads();
-    // D[m][n] += A[m][k] B[k][n]: lane supplies A[m = l32][k = hi2] (here the
-    // weights, so that a lane ends with one token row) and B[k = hi2][n = l32]
+  };
+  const int nsteps = kdim / kF32K;
+  if constexpr (kDual) {
+    // g and u: one stage, each step's loads at its start; two chains already
+    for (int st = 0; st < nsteps; ++st) {
+      fetch(st * kF32K);
+      __syncthreads();
+      park(0);
+      __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < kF32K; kk += 2) {
-      const float x = sa[wm * 32 + l32][kk + hi2];
-      acc0 = mfma32x2(sb0[kk + hi2][wn * 32 + l32], x, acc0);
-      if (kDual) acc1 = mfma32x2(sb1[kk + hi2][wn * 32 + l32], x, acc1);
+      for (int kk = 0; kk < kF32K; kk += 2) {
+        const float x = sa[0][wm * 32 + l32][kk + hi2];
+        acc0 = mfma32x2(sb0[0][kk + hi2][wn * 32 + l32], x, acc0);
+        acc1 = mfma32x2(sb1[0][kk + hi2][wn * 32 + l32], x, acc1);
+      }
     }
+  } else {
+    // K step s goes global -> registers during step s - 2 and registers ->
+    // LDS stage s & 1 at the end of step s - 1.
+    fetch(0);
+    park(0);
+    if (nsteps > 1) fetch(kF32K);
+    __syncthreads();
+    for (int st = 0; st < nsteps; ++st) {
+      const int buf = st & 1;
+      // D[m][n] += A[m][k] B[k][n]: lane supplies A[m = l32][k = hi2] (here the
+      // weights, so that a lane ends with one token row) and B[k = hi2][n = l32]
+#pragma unroll
+      for (int kk = 0; kk < kF32K; kk += 4) {
+        const float x0 = sa[buf][wm * 32 + l32][kk + hi2];
+        const float x1 = sa[buf][wm * 32 + l32][kk + 2 + hi2];
+        acc0 = mfma32x2(sb0[buf][kk + hi2][wn * 32 + l32], x0, acc0);
+        acc0b = mfma32x2(sb0[buf][kk + 2 + hi2][wn * 32 + l32], x1, acc0b);
+      }
+      if (st + 1 < nsteps) park(buf ^ 1);
+      if (st + 2 < nsteps) fetch((st + 2) * kF32K);
+      __syncthreads();
+    }
+  }
+  if (!kDual) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc0[r] += acc0b[r];
   }
   // lane holds row wm*32 + l32 and columns wn*32 + 8 (r/4) + 4 hi2 + r%4
   const int64_t row = row0 + wm * 32 + l32;
