@@ -194,7 +194,7 @@ __device__ __forceinline__ float load_w_f32<uint16_t>(const uint16_t* p, int64_t
 //
 // A workgroup of 4 waves takes 64 tokens; each wave 16 tokens against all
 // experts (NT tiles of 16 experts, zero-padded past n_experts).  x and W are
-// staged in LDS as float32, 64 (or 32) d at a time, double-buffered through registers
+// staged in LDS as float32, a chunk of d at a time (router_dc), double-buffered through registers
 // (the next chunk's global loads are issued before the current chunk's
 // MFMAs).  The float32-rounded logits go through LDS to the wave-per-token
 // selection.
@@ -204,19 +204,24 @@ struct IntC {
 };
 
 constexpr int kRTokWave = 16;
-// d per LDS chunk (one barrier per chunk): 64 while the staging of up to 64
-// experts fits two workgroups per CU, 32 beyond.
-constexpr int router_dc(int nt) { return nt <= 4 ? 64 : 32; }
+// d per LDS chunk (one barrier per chunk): as many as keep the staging
+// within one 8-wave workgroup per CU (up to 64 experts: 128 d, 141 KB) or two
+// 4-wave ones (up to 32 experts: 128 d; up to 64: 64 d), 32 beyond.  Halving
+// the barriers took 1.5-2 us off 62-93 us.  The scalar W staging (WV false)
+// keeps 64 d, whose registers 128 d would spill.
+constexpr int router_dc(int nt, int nw, bool wv) {
+  return wv && (nt <= 2 || (nt <= 4 && nw == 8)) ? 128 : (nt <= 4 ? 64 : 32);
+}
 
 // ES waves share a group of 16 tokens and split its expert tiles, so a
 // workgroup of NW waves takes 16 NW / ES tokens.  With ES = 2 two waves run
 // on every SIMD and each keeps NT/2 independent accumulator chains.
-template <int NT, int ES, int NW>
+template <int NT, int ES, int NW, bool WV = true>
 struct alignas(16) RouterLds {
   static constexpr int kNP = 16 * NT;
   static constexpr int kWPitch = kNP + 8;
   static constexpr int kTB = 16 * NW / ES;
-  static constexpr int kDc = router_dc(NT);
+  static constexpr int kDc = router_dc(NT, NW, WV);
   static constexpr int kXPitch = kDc + 4;  // 16-byte aligned rows
   float x[2][kTB][kXPitch];
   float w[2][kDc][kWPitch];
@@ -234,16 +239,16 @@ __global__ __launch_bounds__(64 * NW) void router_kernel(const XT* __restrict__ 
                                                      float* __restrict__ gates) {
   static_assert(NT % ES == 0, "expert tiles must split evenly");
   constexpr int kThr = 64 * NW;
-  constexpr int kNP = RouterLds<NT, ES, NW>::kNP;
-  constexpr int kTB = RouterLds<NT, ES, NW>::kTB;
-  constexpr int kRDc = RouterLds<NT, ES, NW>::kDc;
+  constexpr int kNP = RouterLds<NT, ES, NW, WV>::kNP;
+  constexpr int kTB = RouterLds<NT, ES, NW, WV>::kTB;
+  constexpr int kRDc = RouterLds<NT, ES, NW, WV>::kDc;
   constexpr int kTG = kTB / kRTokWave;                // token groups per workgroup
   constexpr int kNTW = NT / ES;                       // expert tiles per wave
   constexpr int kEPL = (kNP + 63) / 64;
   constexpr int kWPer = (kRDc * kNP + kThr - 1) / kThr;  // w elements per thread per chunk
   constexpr int kE16 = 16 / static_cast<int>(sizeof(WT));  // W elements per 16-byte load
   constexpr int kWV = (kRDc * kNP / kE16 + kThr - 1) / kThr;  // 16-byte W loads per thread per chunk
-  __shared__ RouterLds<NT, ES, NW> lds;
+  __shared__ RouterLds<NT, ES, NW, WV> lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
