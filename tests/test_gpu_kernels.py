@@ -64,6 +64,13 @@ ROUTER_CASES = [
     # enough tokens for one 64-token workgroup per CU (8-wave router), last one partial
     (16450, 512, 66, 6, "bf16", "f32", "sigmoid", 2.5, True),
     (16400, 768, 64, 8, "bf16", "bf16", "softmax", 1.0, False),
+    # 128-d LDS chunks with a partial last chunk: 8-wave, 4-wave up to 32
+    # experts, and float32 x
+    (16384, 1000, 64, 8, "bf16", "f32", "softmax", 1.0, False),
+    (600, 520, 32, 4, "bf16", "f32", "sigmoid", 2.5, True),
+    (700, 200, 20, 3, "f32", "f32", "softmax", 1.0, False),
+    # 62 experts: W rows not a multiple of 16 bytes (scalar W staging, 64-d chunks)
+    (16400, 648, 62, 8, "bf16", "f32", "sigmoid", 2.5, True),
 ]
 
 
