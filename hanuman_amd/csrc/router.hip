@@ -2,9 +2,11 @@
 //
 // Logits are float32 roundings of float64 sums taken in ascending d from +0.0
 // (see router_kernel for how the float64 matrix cores keep that order).
-// Top-k is K rounds of a wave-wide max over the totalOrder keys, each
-// followed by a ballot of the lanes at the maximum whose lowest expert wins,
-// so equal keys resolve to the lower expert index.
+// Top-k is K rounds of a max over the totalOrder keys that resolves equal
+// keys to the lower expert index: up to 64 experts eight tokens per wave (8
+// lanes per token, 64-bit (key, expert) composites, select_group8); beyond,
+// one token per wave (a wave-wide max, then a ballot of the lanes at the
+// maximum whose lowest expert wins, select_and_gate).
 #include <atomic>
 
 #include "hmoe_common.h"
@@ -147,6 +149,110 @@ __device__ __forceinline__ void select_and_gate(const float (&logit)[NTOK][EPL],
     if (store[q] && lane < top_k) {
       top_idx_row[q][lane] = my_e[q];
       gates_row[q][lane] = w;
+    }
+  }
+}
+
+// max over the 8 lanes of each aligned lane group of the 64-bit (key, value)
+// pair with the larger key: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror.
+template <int CTRL>
+__device__ __forceinline__ void dpp_max_kv(int64_t& k, float& v) {
+  const int32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int32_t>(k), CTRL, 0xF, 0xF, false);
+  const int32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int32_t>(k >> 32), CTRL, 0xF, 0xF, false);
+  const int32_t vv = __builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false);
+  const int64_t t = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                         static_cast<uint32_t>(lo));
+  if (t > k) {
+    k = t;
+    v = __int_as_float(vv);
+  }
+}
+
+// Selection + gates for 8 tokens per wave: lane group g = lane / 8 takes one
+// token, lane p = lane % 8 of the group its experts p*E .. p*E + E - 1.  Every
+// entry is a 64-bit composite, the totalOrder key in the high bits above
+// 0xFFFF - expert, so the larger composite is the larger key and on equal
+// keys the lower expert (the lax.top_k order); retired entries and those past
+// n_experts hold INT64_MIN, below every live one.  Round k: each lane's
+// largest entry, then the group's largest (three DPP stages, carrying the
+// entry's value); the lane that holds it retires it.  Lane p records slots
+// p, p + 8, p + 16, p + 24; the gate denominators are summed in k order.
+template <int E>
+__device__ __forceinline__ void select_group8(const float (&logit)[E], bool store,
+                                              const float* __restrict__ bias, int n_experts,
+                                              int top_k, int mode, float rsf,
+                                              int32_t* __restrict__ top_idx_row,
+                                              float* __restrict__ gates_row) {
+#pragma clang fp contract(off)
+  const int p = threadIdx.x & 7;
+  constexpr int64_t kGone = INT64_MIN;
+  int64_t ck[E];
+  float val[E];  // value the gate is built from: sigmoid score or logit
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const int e = p * E + j;
+    float kf = logit[j];
+    if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
+      const float sg = sigmoid_det(logit[j]);
+      val[j] = sg;
+      kf = sg + ((bias != nullptr && e < n_experts) ? bias[e] : 0.0f);
+    } else {
+      val[j] = logit[j];
+    }
+    const uint64_t key = static_cast<uint64_t>(static_cast<int64_t>(total_order_key(kf)));
+    ck[j] = e < n_experts ? static_cast<int64_t>((key << 16) | static_cast<uint64_t>(0xFFFF - e)) : kGone;
+  }
+  int my_e[4] = {0, 0, 0, 0};
+  float my_v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float denom = 0.0f, vmax = 0.0f;
+  for (int k = 0; k < top_k; ++k) {
+    int64_t best = ck[0];
+    float bv = val[0];
+    int barg = 0;
+#pragma unroll
+    for (int j = 1; j < E; ++j) {
+      if (ck[j] > best) {
+        best = ck[j];
+        bv = val[j];
+        barg = j;
+      }
+    }
+    int64_t gb = best;
+    float gv = bv;
+    dpp_max_kv<0xB1>(gb, gv);
+    dpp_max_kv<0x4E>(gb, gv);
+    dpp_max_kv<0x141>(gb, gv);
+    // composites are unique, so exactly one lane of the group holds gb
+    const bool owner = gb == best;
+#pragma unroll
+    for (int j = 0; j < E; ++j)
+      if (owner && barg == j) ck[j] = kGone;
+    const int w = 0xFFFF - static_cast<int>(gb & 0xFFFF);
+    float rec = gv;
+    if (mode == HMOE_ROUTE_SIGMOID_BIAS) {
+      denom = denom + gv;
+    } else {
+      if (k == 0) vmax = gv;
+      rec = exp_det(gv - vmax);
+      denom = denom + rec;
+    }
+    if ((k & 7) == p) {
+      const int r = k >> 3;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q == r) {
+          my_e[q] = w;
+          my_v[q] = rec;
+        }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k = 8 * q + p;
+    if (store && k < top_k) {
+      top_idx_row[k] = my_e[q];
+      gates_row[k] = mode == HMOE_ROUTE_SIGMOID_BIAS ? (my_v[q] / (denom + 1e-9f)) * rsf
+                                                     : my_v[q] / denom;
     }
   }
 }
@@ -430,32 +536,58 @@ __global__ __launch_bounds__(64 * NW) void router_kernel(const XT* __restrict__ 
           static_cast<float>(acc[t][r]);
   __syncthreads();
 
-  // Selection: wave w takes tokens w*kTB/NW .. (w+1)*kTB/NW - 1 of the workgroup.
-  constexpr int kSel = kTB / NW;
-  static_assert(kSel % 2 == 0, "selection takes tokens in pairs");
+  if constexpr (NT <= 4) {
+    // Selection: wave w takes tokens w*kTB/NW .. (w+1)*kTB/NW - 1 of the
+    // workgroup, eight at a time (lane group lane / 8 one token).
+    constexpr int kSel = kTB / NW;
+    static_assert(kSel % 8 == 0, "selection takes tokens in groups of eight");
+    constexpr int kE8 = kNP / 8;
+    const int p8 = lane & 7;
 #pragma unroll 1
-  for (int i = 0; i < kSel; i += 2) {
-    const int row = wave * kSel + i;
-    const int64_t tok = t0 + row;
-    if (tok >= tokens) break;
-    float l[2][kEPL];
-    bool st[2];
-    int32_t* ti[2];
-    float* gt[2];
+    for (int i = 0; i < kSel; i += 8) {
+      if (t0 + wave * kSel + i >= tokens) break;
+      const int row = wave * kSel + i + (lane >> 3);
+      const int64_t tok = t0 + row;
+      const bool st = tok < tokens;
+      const int64_t tq = st ? tok : tokens - 1;
+      float l[kE8];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      st[q] = tok + q < tokens;
-      const int64_t tq = st[q] ? tok + q : tok;
-      ti[q] = top_idx + tq * top_k;
-      gt[q] = gates + tq * top_k;
-#pragma unroll
-      for (int j = 0; j < kEPL; ++j) {
-        const int e = lane + 64 * j;
-        l[q][j] = e < kNP ? lg[(row + q) * kNP + e] : 0.0f;
-        if (st[q] && e < n_experts) logits[tq * n_experts + e] = l[q][j];
+      for (int j = 0; j < kE8; ++j) {
+        const int e = p8 * kE8 + j;
+        l[j] = lg[row * kNP + e];
+        if (st && e < n_experts) logits[tq * n_experts + e] = l[j];
       }
+      select_group8<kE8>(l, st, bias, n_experts, top_k, mode, rsf, top_idx + tq * top_k,
+                         gates + tq * top_k);
     }
-    select_and_gate<kEPL, 2>(l, st, bias, n_experts, top_k, mode, rsf, ti, gt);
+  } else {
+    // Selection: wave w takes tokens w*kTB/NW .. (w+1)*kTB/NW - 1 of the workgroup.
+    constexpr int kSel = kTB / NW;
+    static_assert(kSel % 2 == 0, "selection takes tokens in pairs");
+#pragma unroll 1
+    for (int i = 0; i < kSel; i += 2) {
+      const int row = wave * kSel + i;
+      const int64_t tok = t0 + row;
+      if (tok >= tokens) break;
+      float l[2][kEPL];
+      bool st[2];
+      int32_t* ti[2];
+      float* gt[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        st[q] = tok + q < tokens;
+        const int64_t tq = st[q] ? tok + q : tok;
+        ti[q] = top_idx + tq * top_k;
+        gt[q] = gates + tq * top_k;
+#pragma unroll
+        for (int j = 0; j < kEPL; ++j) {
+          const int e = lane + 64 * j;
+          l[q][j] = e < kNP ? lg[(row + q) * kNP + e] : 0.0f;
+          if (st[q] && e < n_experts) logits[tq * n_experts + e] = l[q][j];
+        }
+      }
+      select_and_gate<kEPL, 2>(l, st, bias, n_experts, top_k, mode, rsf, ti, gt);
+    }
   }
 }
 
@@ -491,6 +623,31 @@ __global__ __launch_bounds__(256) void select_kernel(const float* __restrict__ l
     }
   }
   select_and_gate<EPL, kSelTok>(l, st, bias, n_experts, top_k, mode, rsf, ti, gt);
+}
+
+// Selection and gates from given logits for up to 64 experts, eight tokens
+// per wave (lane group lane / 8 one token, lane p its experts 8p .. 8p + 7).
+__global__ __launch_bounds__(256) void select_kernel_g8(const float* __restrict__ logits,
+                                                        const float* __restrict__ bias,
+                                                        int64_t tokens, int n_experts, int top_k,
+                                                        int mode, float rsf,
+                                                        int32_t* __restrict__ top_idx,
+                                                        float* __restrict__ gates) {
+  const int lane = threadIdx.x & 63;
+  const int p = lane & 7;
+  const int64_t tok0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8;
+  if (tok0 >= tokens) return;  // uniform per wave
+  const int64_t tok = tok0 + (lane >> 3);
+  const bool st = tok < tokens;
+  const int64_t tq = st ? tok : tokens - 1;
+  float l[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = p * 8 + j;
+    l[j] = e < n_experts ? logits[tq * n_experts + e] : 0.0f;
+  }
+  select_group8<8>(l, st, bias, n_experts, top_k, mode, rsf, top_idx + tq * top_k,
+                   gates + tq * top_k);
 }
 
 // CU count of the stream's device (0 if it cannot be queried), cached per device.
@@ -610,7 +767,8 @@ extern "C" int hmoe_router_from_logits(const float* logits, const float* bias, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(ceil_div(tokens, 4 * kSelTok)));
   if (n_experts <= 64)
-    hipLaunchKernelGGL(select_kernel<1>, grid, dim3(256), 0, s, logits, bias, tokens, n_experts, top_k, mode, routed_scaling_factor, top_idx, gates);
+    hipLaunchKernelGGL(select_kernel_g8, dim3(static_cast<unsigned>(ceil_div(tokens, 32))), dim3(256), 0, s,
+                       logits, bias, tokens, n_experts, top_k, mode, routed_scaling_factor, top_idx, gates);
   else if (n_experts <= 128)
     hipLaunchKernelGGL(select_kernel<2>, grid, dim3(256), 0, s, logits, bias, tokens, n_experts, top_k, mode, routed_scaling_factor, top_idx, gates);
   else

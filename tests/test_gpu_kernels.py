@@ -102,6 +102,38 @@ def test_router_bit_exact(gpu, case):
     assert_bits_equal(host(g), g_ref, "gates")
 
 
+@pytest.mark.parametrize("T,N,Kk,mode", [(16400, 64, 8, "softmax"), (700, 64, 8, "sigmoid"),
+                                         (333, 50, 6, "softmax"), (16390, 40, 4, "sigmoid")])
+def test_router_ties_through_logits(gpu, T, N, Kk, mode):
+    """Experts with identical router columns get identical logits for every
+    token; the lower expert index must come first (within one lane, across
+    lanes and across lane groups), and all-zero columns tie at exactly 0."""
+    print(f"router ties T={T} N={N} K={Kk} {mode}", flush=True)
+    rng = np.random.default_rng(T + 7 * N)
+    D = 512
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    w = (0.02 * rng.standard_normal((D, N))).astype(np.float32)
+    for a, b in [(5, 9), (0, N - 1), (32 % N, 33 % N), (7, 8), (3, 20)]:
+        w[:, b] = w[:, a]
+    w[:, [1, 2, N - 2]] = 0.0
+    bias = None
+    if mode == "sigmoid":
+        bias = np.zeros(N, np.float32)
+        bias[[5, 9, 0, N - 1]] = 0.25
+    logits_ref = O.router_logits(x, w)
+    if mode == "softmax":
+        idx_ref, g_ref = O.route_softmax(logits_ref, Kk)
+    else:
+        idx_ref, g_ref, _ = O.route_sigmoid(logits_ref, bias, Kk, 2.5)
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    logits, idx, g = K.router(dev_bf16(x, gpu), dev_f32(w, gpu),
+                              dev_f32(bias, gpu) if bias is not None else None, Kk, m, 2.5)
+    torch.cuda.synchronize()
+    assert_bits_equal(host(logits), logits_ref, "logits")
+    assert_bits_equal(host(idx), idx_ref, "top_idx")
+    assert_bits_equal(host(g), g_ref, "gates")
+
+
 def test_router_from_logits_ties_and_signed_zero(gpu):
     rng = np.random.default_rng(21)
     T, N, Kk = 512, 64, 8
