@@ -153,8 +153,10 @@ __device__ __forceinline__ void select_and_gate(const float (&logit)[NTOK][EPL],
   }
 }
 
-// max over the 8 lanes of each aligned lane group of the 64-bit (key, value)
-// pair with the larger key: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror.
+// One stage of a max over each aligned group of 8 lanes of a (64-bit key,
+// value) pair: the pair of the lane the DPP control CTRL names replaces this
+// lane's if its key is larger.  quad_perm [1,0,3,2], then [2,3,0,1], then
+// row_half_mirror leave the group's largest pair in all 8 lanes.
 template <int CTRL>
 __device__ __forceinline__ void dpp_max_kv(int64_t& k, float& v) {
   const int32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int32_t>(k), CTRL, 0xF, 0xF, false);
