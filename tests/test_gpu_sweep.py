@@ -235,3 +235,54 @@ def test_module_backward_needs_d_ff_multiple_of_256(gpu):
     assert torch.isfinite(out).all()
     with pytest.raises(HmoeError, match="multiple of 256"):
         out.sum().backward()
+
+
+N_ROUTER_CASES = 20
+
+
+@pytest.mark.parametrize("i", range(N_ROUTER_CASES))
+def test_random_router_with_ties_matches_oracle(gpu, i):
+    """Routing alone on tie-heavy inputs: the fused router on router weights
+    whose columns repeat (every token then has equal logits on those experts),
+    and the logits-given selection on small-integer logits.  Shapes span the
+    eight-tokens-per-wave selection (up to 64 experts) and the one-token-per-
+    wave one (beyond), partial groups of eight tokens and top-k up to 32."""
+    rng = np.random.default_rng(5000 + i)
+    T = int(rng.integers(1, 3000))
+    D = 8 * int(rng.integers(1, 65))
+    N = int(rng.choice([1, 2, 7, 8, 9, 31, 33, 50, 63, 64, 65, 100, 256]))
+    Kk = int(rng.integers(1, min(N, 32) + 1))
+    mode = "softmax" if rng.random() < 0.5 else "sigmoid"
+    rsf = 2.5 if mode == "sigmoid" else 1.0
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    print(f"router sweep case {i}: T={T} D={D} N={N} K={Kk} {mode}", flush=True)
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    w = (0.05 * rng.standard_normal((D, N))).astype(np.float32)
+    for _ in range(min(N // 2, 6)):
+        a, b = rng.choice(N, 2, replace=False)
+        w[:, b] = w[:, a]
+    bias = None
+    if mode == "sigmoid":
+        bias = (0.1 * rng.integers(-2, 3, size=N)).astype(np.float32)   # ties in the bias too
+    logits_ref = O.router_logits(x, w)
+    if mode == "softmax":
+        idx_ref, g_ref = O.route_softmax(logits_ref, Kk)
+    else:
+        idx_ref, g_ref, _ = O.route_sigmoid(logits_ref, bias, Kk, rsf)
+    dev_bias = torch.from_numpy(bias).to(gpu) if bias is not None else None
+    logits, idx, g = K.router(torch.from_numpy(x).to(gpu).to(torch.bfloat16),
+                              torch.from_numpy(w).to(gpu), dev_bias, Kk, m, rsf)
+    torch.cuda.synchronize()
+    assert bits_equal(host(logits), logits_ref), "fused router logits"
+    assert bits_equal(host(idx), idx_ref), "fused router top_idx"
+    assert bits_equal(host(g), g_ref), "fused router gates"
+
+    lg = rng.integers(-3, 4, size=(T, N)).astype(np.float32)
+    if mode == "softmax":
+        idx_ref, g_ref = O.route_softmax(lg, Kk)
+    else:
+        idx_ref, g_ref, _ = O.route_sigmoid(lg, bias, Kk, rsf)
+    idx, g = K.router_from_logits(torch.from_numpy(lg).to(gpu), dev_bias, Kk, m, rsf)
+    torch.cuda.synchronize()
+    assert bits_equal(host(idx), idx_ref), "logits-given top_idx"
+    assert bits_equal(host(g), g_ref), "logits-given gates"
