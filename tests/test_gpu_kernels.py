@@ -155,6 +155,45 @@ def test_router_from_logits_ties_and_signed_zero(gpu):
     assert host(idx)[1].tolist() == list(range(Kk))      # all equal -> lowest indices
 
 
+@pytest.mark.parametrize("N", [20, 60, 100])
+def test_router_from_logits_nan_and_infinities(gpu, N):
+    """NaNs, infinities and signed zeros order by IEEE totalOrder; the
+    negative NaN with every payload bit set has the lowest key of all, which
+    must still rank above the padding past n_experts (top-k = N selects
+    every expert)."""
+    rng = np.random.default_rng(N + 1)
+    T, Kk = 16, min(N, 32)
+    bits = rng.standard_normal((T, N)).astype(np.float32).view(np.uint32)
+    bits[0] = 0xFFFFFFFF                       # all the lowest key: index order
+    bits[1, [3, 17, N - 1]] = 0xFFFFFFFF       # negative NaN, full payload
+    bits[1, 5] = 0xFF800000                    # -inf
+    bits[1, 6] = 0x7F800000                    # +inf
+    bits[1, 7] = 0x7FC00000                    # +NaN: above +inf
+    bits[1, 8] = 0x80000000                    # -0.0 below +0.0
+    bits[1, 9] = 0x00000000
+    bits[2:, ::7] = 0xFFFFFFFF
+    logits = bits.view(np.float32)
+    # softmax selects on the logits' own bits; the sigmoid keys are computed,
+    # and a NaN's payload after arithmetic is not fixed, so that mode gets -inf
+    # where the logits hold NaNs
+    finite_or_inf = np.where(np.isnan(logits), np.float32(-np.inf), logits)
+    for mode, lg in ((_lib.ROUTE_SOFTMAX, logits), (_lib.ROUTE_SIGMOID_BIAS, finite_or_inf)):
+        bias = np.zeros(N, np.float32) if mode == _lib.ROUTE_SIGMOID_BIAS else None
+        if mode == _lib.ROUTE_SOFTMAX:
+            idx_ref, g_ref = O.route_softmax(lg, Kk)
+        else:
+            idx_ref, g_ref, _ = O.route_sigmoid(lg, bias, Kk, 2.5)
+        idx, g = K.router_from_logits(dev_f32(lg, gpu),
+                                      dev_f32(bias, gpu) if bias is not None else None, Kk, mode, 2.5)
+        torch.cuda.synchronize()
+        assert_bits_equal(host(idx), idx_ref, f"top_idx mode {mode}")
+        g, g_ref = host(g), np.asarray(g_ref, np.float32)
+        assert np.array_equal(np.isnan(g), np.isnan(g_ref)), f"gate NaNs mode {mode}"
+        ok = ~np.isnan(g_ref)
+        assert_bits_equal(g[ok], g_ref[ok], f"gates mode {mode}")
+        assert host(idx)[0].tolist() == list(range(Kk)), f"row of equal keys, mode {mode}"
+
+
 @pytest.mark.parametrize("N", [100, 200])
 def test_router_from_logits_ties_across_lanes(gpu, N):
     """Experts past 64 share lanes with lower ones (lane = expert % 64): equal
