@@ -84,21 +84,28 @@ class _PackCache:
     """Packed bf16 operands of fp32 master weights, rebuilt when a master
     changes: a different tensor object (held by weak reference and compared
     by identity, so a new tensor at a freed address is not mistaken for the
-    old one) or an in-place update (the tensor's version counter)."""
+    old one), an in-place update (the tensor's version counter), or new
+    storage under the same object (``t.data = other``, which keeps both the
+    identity and the version counter: caught by the data pointer, shape,
+    stride and dtype)."""
 
     def __init__(self):
         self._refs = None
-        self._versions = None
+        self._keys = None
         self._val = None
+
+    @staticmethod
+    def _key(t):
+        return (t._version, t.data_ptr(), tuple(t.shape), t.stride(), t.dtype, t.device)
 
     def get(self, tensors, build):
         same = (self._refs is not None and len(self._refs) == len(tensors)
                 and all(r() is t for r, t in zip(self._refs, tensors))
-                and all(t._version == v for t, v in zip(tensors, self._versions)))
+                and all(self._key(t) == k for t, k in zip(tensors, self._keys)))
         if not same:
             self._val = build()
             self._refs = tuple(weakref.ref(t) for t in tensors)
-            self._versions = tuple(t._version for t in tensors)
+            self._keys = tuple(self._key(t) for t in tensors)
         return self._val
 
 

@@ -392,7 +392,7 @@ def routed_forward64(x, router_w, wg, wu, wd, top_idx, slot_pos, perm_src, offse
 
 def moe_backward(x, params: dict, dy, fwd: dict, *, routing: str = "softmax",
                  rsf: float = 1.0, precision: str = "bf16", n_shared: int = 0,
-                 batch_shape=None, d_aux=None) -> dict:
+                 batch_shape=None, d_aux=None, x_dtype: str | None = None) -> dict:
     """VJP of the MoE layer (``moe.py:170-294``) for the cotangent ``dy`` of
     ``out`` and, optionally, ``d_aux = (d_z, d_bal, d_ent)`` of the aux losses
     (with ``batch_shape = (B, S)``; ``:253-283``).
@@ -403,8 +403,12 @@ def moe_backward(x, params: dict, dy, fwd: dict, *, routing: str = "softmax",
     shared), ``d_router [D, N]``, ``dWg``, ``dWu [N, D, F]``, ``dWd [N, F, D]``,
     ``dWg_shared``/``dWu_shared``/``dWd_shared`` when there is a shared expert,
     and the intermediates ``d_ys``, ``d_gates``, ``d_logits``, ``d_xs``,
-    ``dx_experts``, ``dx_router``.
+    ``dx_experts``, ``dx_router``.  ``x_dtype`` is the dtype ``x`` arrived in
+    (``"f32"`` under bf16 compute promotes the shared expert, as in
+    :func:`moe_oracle.moe_forward`; default: the compute dtype).
     """
+    if x_dtype not in (None, "bf16", "f32"):
+        raise ValueError(x_dtype)
     x = np.asarray(x, F32)
     T = x.shape[0]
     K = np.asarray(fwd["top_idx"]).shape[1]
@@ -427,8 +431,9 @@ def moe_backward(x, params: dict, dy, fwd: dict, *, routing: str = "softmax",
     res = {}
     if n_shared > 0:
         xc = bf16_round(x) if precision == "bf16" else x
-        # a float32 x under bf16 compute reaches the shared expert as given (moe.py:249)
-        promoted = precision == "bf16" and not np.array_equal(xc, x)
+        # a float32 x under bf16 compute reaches the shared expert as given
+        # (moe.py:249); decided by x's dtype, never by its values
+        promoted = precision == "bf16" and x_dtype == "f32"
         sh = shared_bwd(x if promoted else xc, params["shared_w_gate"], params["shared_w_up"],
                         params["shared_w_down"], n_shared, dy, precision, promoted=promoted)
         dx = dx + sh["dx"]

@@ -641,7 +641,7 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
                 routed_scaling_factor: float = 2.5, capacity_factor=None,
                 expert: str = "swiglu", n_shared: int = 0, dtype: str = "bf16",
                 precision: str = "fp32", logits=None, fast_router: bool = False,
-                batch_shape=None, out_dtype: str = "f32") -> dict:
+                batch_shape=None, out_dtype: str = "f32", x_dtype: str | None = None) -> dict:
     """Whole-layer forward (``MoE.__call__``, ``moe.py:170-294``).
 
     ``x`` [T,D] float32 values (bf16-representable when ``dtype="bf16"``).
@@ -652,8 +652,18 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
     ``expert``: ``"swiglu"``, ``"identity"`` or ``"swiglu_fp8"`` (e4m3 operands,
     :func:`expert_ffn_fp8`; quantised weights from ``params["fp8"]`` or
     :func:`quantize_expert_weights`).  ``out_dtype="bf16"`` rounds the output.
+    ``x_dtype``: the dtype ``x`` arrives in (``"bf16"`` or ``"f32"``; default
+    the compute ``dtype``, as ``model/transformer.py`` passes it).  The
+    routed path casts ``x`` to the compute dtype (``moe.py:198``); the shared
+    expert sees it as given (``moe.py:249``), so a float32 ``x`` under bf16
+    compute promotes the shared SwiGLU to float32.  The promotion follows the
+    dtype, never ``x``'s values: a float32 ``x`` whose values happen to be
+    bf16-exact is still promoted.
     Returns a dict with every intermediate the kernels produce.
     """
+    x_dtype = dtype if x_dtype is None else x_dtype
+    if x_dtype not in ("bf16", "f32"):
+        raise ValueError(x_dtype)
     x = np.asarray(x, dtype=F32)
     T, D = x.shape
     if logits is None:
@@ -698,7 +708,7 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
     if n_shared > 0:
         # moe.py:249 passes x as given (only the routed path casts, moe.py:198):
         # a float32 x under bf16 compute promotes the shared SwiGLU to float32
-        promoted = dtype == "bf16" and not np.array_equal(x_c, x)
+        promoted = dtype == "bf16" and x_dtype == "f32"
         residual = shared_expert(x if promoted else x_c, params["shared_w_gate"],
                                  params["shared_w_up"], params["shared_w_down"], n_shared,
                                  precision="bf16_promoted" if promoted and precision == "bf16"

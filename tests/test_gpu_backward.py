@@ -415,7 +415,7 @@ def test_module_autograd_matches_oracle(gpu, n_shared, cf, x_dtype, N, Kk):
                "ys": host(sv["ys"])}
     ref = B.moe_backward(xn, p, host(dy).reshape(T, D), ref_fwd, routing="sigmoid", rsf=2.5,
                          precision="bf16", n_shared=n_shared, batch_shape=(Bq, Sq),
-                         d_aux=(c_z, c_b, 0.0))
+                         d_aux=(c_z, c_b, 0.0), x_dtype=x_dtype)
     pairs = [("dx", x.grad, ref["dx"]), ("d_router", m.router.value.grad, ref["d_router"]),
              ("dWg", m.expert_w_gate.value.grad, ref["dWg"]),
              ("dWu", m.expert_w_up.value.grad, ref["dWu"]),

@@ -16,6 +16,10 @@ from hanuman_amd.moe import MoE
 pytestmark = pytest.mark.gpu
 
 BF16_TOL = 2e-2
+# Worst single token (normwise over its d_model values) at the full-size
+# workloads, against the float32 layer on the weights the kernels use.
+WORST_TOKEN_TOL_BF16 = 1.5e-2   # measured 5.4e-3 (full_bf16), 6.0e-3 (skewed_bf16)
+WORST_TOKEN_TOL_FP8 = 7e-2     # measured 5.4e-2 (fp8_experts)
 
 
 def host(t):
@@ -143,6 +147,10 @@ def test_workload_full_size(gpu, name):
           f"worst token {tok.max():.3e}, max abs / max |ref| "
           f"{np.abs(out - ref).max() / np.abs(ref).max():.3e}", flush=True)
     assert err < BF16_TOL
+    # every token, not only the whole output: one wrong K step in one of the
+    # thousands of persistent tiles moves the normwise figure by ~1e-3 but
+    # puts that tile's tokens far above this bound
+    assert tok.max() < WORST_TOKEN_TOL_BF16, f"worst token {tok.max():.3e}"
     # size-independent property: the fused gate/up (rows gathered from x by
     # the GEMM) equals the unfused permute + gate/up on the kept rows, bit for bit
     import hanuman_amd.kernels as K
@@ -220,7 +228,7 @@ def test_moe_module_float32_input_promotes_shared_expert(gpu, n_shared):
                                                 p["shared_w_up"], p["shared_w_down"], n_shared,
                                                 "bf16"), sh_ref)
     ref = O.moe_forward(xn, p, top_k=Kk, routing="sigmoid", routed_scaling_factor=2.5,
-                        n_shared=n_shared, dtype="bf16", precision="bf16")
+                        n_shared=n_shared, dtype="bf16", precision="bf16", x_dtype="f32")
     err = O.normwise_rel_err(host(out).reshape(B * S, D), ref["out"])
     print(f"  shared vs promoted oracle {err_sh:.2e} (bf16 path {err_bf:.2e}); out {err:.2e}",
           flush=True)
@@ -314,6 +322,7 @@ def test_fp8_workload_full_size(gpu):
           f"against the float32 layer on the dequantised weights; {err32:.3e} against the "
           f"unquantised float32 weights", flush=True)
     assert err < FP8_TOL
+    assert tok.max() < WORST_TOKEN_TOL_FP8, f"worst token {tok.max():.3e}"
 
 
 @pytest.mark.parametrize("n_shared,routing,cf", [(1, "sigmoid", None), (2, "softmax", 1.25)])

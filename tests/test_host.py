@@ -106,7 +106,9 @@ def test_moe_state_round_trip(tmp_path):
 
 def test_pack_cache_rebuilds_on_identity_or_version():
     """The packed-operand cache rebuilds for a different tensor object (even
-    with equal contents) and after an in-place update, and not otherwise."""
+    with equal contents), after an in-place update and after new storage is
+    assigned under the same object (``t.data = other``, which keeps identity
+    and version counter), and not otherwise."""
     import torch
     from hanuman_amd.moe import _PackCache
     builds = []
@@ -124,6 +126,13 @@ def test_pack_cache_rebuilds_on_identity_or_version():
     assert len(builds) == 3
     c.get((a2, b), lambda: builds.append(1) or len(builds))
     assert len(builds) == 3
+    v = a2._version
+    a2.data = torch.full((6,), 5.0)          # new storage and shape, same object
+    assert a2._version == v
+    assert c.get((a2, b), lambda: builds.append(1) or len(builds)) == 4
+    a2.data = torch.full((6,), 7.0)          # same shape, new storage
+    assert c.get((a2, b), lambda: builds.append(1) or len(builds)) == 5
+    assert c.get((a2, b), lambda: builds.append(1) or len(builds)) == 5
 
 
 def test_bench_refuses_more_than_one_gpu():

@@ -419,10 +419,44 @@ def test_shared_expert_promoted_is_float32_swiglu_on_bf16_weights(n_shared):
               "expert_w_up": (0.1 * rng.standard_normal((N, D, F))).astype(np.float32),
               "expert_w_down": (0.1 * rng.standard_normal((N, F, D))).astype(np.float32),
               "shared_w_gate": wg, "shared_w_up": wu, "shared_w_down": wd}
-    kw = dict(top_k=K, routing="softmax", dtype="bf16", precision="bf16")
+    kw = dict(top_k=K, routing="softmax", dtype="bf16", precision="bf16", x_dtype="f32")
     with_sh = O.moe_forward(x, params, n_shared=n_shared, **kw)["out"]
     without = O.moe_forward(x, params, n_shared=0, **kw)["out"]
     assert O.normwise_rel_err(with_sh.astype(np.float64) - without, got) < 1e-5
+
+
+@pytest.mark.parametrize("n_shared", [1, 2])
+def test_shared_expert_promotion_follows_x_dtype_not_values(n_shared):
+    """The promotion is decided by x's dtype (moe.py:249 against :198), not by
+    its values: a float32 x whose values are all bf16-exact is still promoted
+    (the float32 SwiGLU on bf16 weights, which keeps h and the output
+    unrounded), and the same values declared bf16 take the bf16 path.  The two
+    results differ, so a value-based rule fails one of the asserts."""
+    rng = np.random.default_rng(77 + n_shared)
+    T, D, F, N, K = 40, 64, 48, 4, 2
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))   # bf16-exact values
+    sh = (lambda *s: s) if n_shared == 1 else (lambda *s: (n_shared,) + s)
+    params = {"router": (0.1 * rng.standard_normal((D, N))).astype(np.float32),
+              "expert_w_gate": (0.1 * rng.standard_normal((N, D, F))).astype(np.float32),
+              "expert_w_up": (0.1 * rng.standard_normal((N, D, F))).astype(np.float32),
+              "expert_w_down": (0.1 * rng.standard_normal((N, F, D))).astype(np.float32),
+              "shared_w_gate": (0.1 * rng.standard_normal(sh(D, F))).astype(np.float32),
+              "shared_w_up": (0.1 * rng.standard_normal(sh(D, F))).astype(np.float32),
+              "shared_w_down": (0.1 * rng.standard_normal(sh(F, D))).astype(np.float32)}
+    kw = dict(top_k=K, routing="softmax", dtype="bf16", precision="bf16", n_shared=n_shared)
+    base = O.moe_forward(x, params, **{**kw, "n_shared": 0})["out"].astype(np.float64)
+    f32 = O.moe_forward(x, params, x_dtype="f32", **kw)["out"] - base
+    b16 = O.moe_forward(x, params, x_dtype="bf16", **kw)["out"] - base
+    default = O.moe_forward(x, params, **kw)["out"] - base
+    args = (params["shared_w_gate"], params["shared_w_up"], params["shared_w_down"], n_shared)
+    promoted = O.shared_expert(x, *args, "bf16_promoted")
+    plain = O.shared_expert(x, *args, "bf16")
+    assert O.normwise_rel_err(promoted, plain) > 1e-4
+    assert O.normwise_rel_err(f32, promoted) < 1e-5
+    assert O.normwise_rel_err(b16, plain) < 1e-5
+    assert np.array_equal(default, b16)
+    with pytest.raises(ValueError):
+        O.moe_forward(x, params, x_dtype="f16", **kw)
 
 
 # ------------------------------------------------------------------- fp8 --

@@ -374,3 +374,33 @@ def test_moe_backward_module_with_shared_and_aux(n_shared):
             return L(*a)
 
         close((g[name] * v).sum(), fd(f, base[pos], v), rtol=1e-5)
+
+
+def test_moe_backward_promotion_follows_x_dtype():
+    """moe_backward takes the shared expert's promoted VJP for a float32 x
+    (x_dtype="f32") even when every value of x is bf16-exact, and the bf16
+    VJP for the same values declared bf16 (the default): the choice follows
+    the dtype moe.py:249 sees, not the values."""
+    rng = np.random.default_rng(91)
+    T, D, F, N, K = 24, 16, 12, 4, 2
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    params = {"router": (0.2 * rng.standard_normal((D, N))).astype(np.float32),
+              "expert_w_gate": (0.2 * rng.standard_normal((N, D, F))).astype(np.float32),
+              "expert_w_up": (0.2 * rng.standard_normal((N, D, F))).astype(np.float32),
+              "expert_w_down": (0.2 * rng.standard_normal((N, F, D))).astype(np.float32),
+              "shared_w_gate": (0.2 * rng.standard_normal((D, F))).astype(np.float32),
+              "shared_w_up": (0.2 * rng.standard_normal((D, F))).astype(np.float32),
+              "shared_w_down": (0.2 * rng.standard_normal((F, D))).astype(np.float32)}
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    fwd = O.moe_forward(x, params, top_k=K, routing="softmax", dtype="bf16", precision="bf16")
+    sw = (params["shared_w_gate"], params["shared_w_up"], params["shared_w_down"], 1, dy, "bf16")
+    want_p = B.shared_bwd(x, *sw, promoted=True)
+    want_b = B.shared_bwd(x, *sw, promoted=False)
+    assert not np.array_equal(want_p["dWd"], want_b["dWd"])
+    got_p = B.moe_backward(x, params, dy, fwd, precision="bf16", n_shared=1, x_dtype="f32")
+    got_b = B.moe_backward(x, params, dy, fwd, precision="bf16", n_shared=1)
+    for k in ("dWg", "dWu", "dWd", "dx"):
+        assert np.array_equal(got_p[k + "_shared"] if k != "dx" else got_p["dx_shared"], want_p[k])
+        assert np.array_equal(got_b[k + "_shared"] if k != "dx" else got_b["dx_shared"], want_b[k])
+    with pytest.raises(ValueError):
+        B.moe_backward(x, params, dy, fwd, precision="bf16", n_shared=1, x_dtype="fp16")
