@@ -51,6 +51,9 @@ SIGNATURES = {
     "hmoe_grouped_gate_up_gather": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32, _i32, _vp,
                                            _vp, _vp]),
     "hmoe_grouped_down": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "hmoe_grouped_swiglu_fused_workspace_bytes": (_sz, [_i64, _i32]),
+    "hmoe_grouped_swiglu_fused": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32, _i32, _vp,
+                                         _vp, _vp, _vp, _vp, _sz, _i64, _i32, _vp]),
     "hmoe_combine": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp]),
     "hmoe_permute_rows_fp8": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hmoe_quantize_rows_fp8": (_i32, [_vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp]),

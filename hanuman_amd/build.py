@@ -44,9 +44,18 @@ def hipcc() -> str:
     return path
 
 
+# Per-file flags.  gemm.hip: no wave-level aggregation of atomics (the fused
+# launch's claims are made by one lane and their results are read a K step
+# later; the aggregation would read the result, and wait for every memory
+# operation in flight, right after the atomic).
+FILE_FLAGS = {
+    "gemm.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

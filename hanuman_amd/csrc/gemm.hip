@@ -1210,6 +1210,431 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
   }
 }
 
+// ---- gate/up and down in one persistent launch -----------------------------------
+// The layer's two bf16 GEMMs (moe.py:70-74) as one launch: neither leaves a
+// partial last round of tiles, there is one launch gap instead of two, and
+// the store-heavy down tiles run beside other CUs' load-heavy gate/up tiles.
+// The m-tiles (256-row blocks of the experts' segments) are split evenly
+// over the XCDs, and each XCD keeps one work list: the gate/up tiles of its
+// m-tiles (m-major, n fastest), then their down tiles.  The XCD of a
+// workgroup is the hardware XCC id of the CU it runs on, not its block
+// index, so the h rows a down tile reads were written by gate/up tiles of
+// the same XCD, into that XCD's L2 (whose lines for h rows are only ever
+// written or read by this XCD during the launch): no L2 write-back or
+// invalidation is needed between them.  Workgroups claim list positions one
+// at a time from the XCD's counter, three tiles ahead of the tile they
+// compute (so the load pipeline and the gather's source prefetch can look
+// ahead), and compute their claims in order.  A down tile of m-tile m waits
+// until ready[m] counts every gate/up tile of m: a gate/up tile adds one
+// once all its waves' stores have completed (s_waitcnt vmcnt(0) and a
+// barrier, in the first K step of the workgroup's next tile, or at the end
+// of its gate/up tiles).  No deadlock: a workgroup claims a down tile only
+// after every gate/up position of its XCD has been claimed, by workgroups
+// that are running and never wait inside a gate/up tile.  The wait is
+// bounded by a wall-clock limit: a wait that gives up sets status bit 0 and
+// its tile is computed from whatever h holds (every access stays in bounds),
+// so every workgroup always exits.
+// Sync words of the workspace.  The launch leaves every counter at zero when
+// it ends (the last workgroup to finish clears them), so a workspace that
+// was zero before its first call needs no clearing between calls.
+constexpr int kFusedStatus = 8;   // status of the last completed call (bit 0: a wait gave up)
+constexpr int kFusedError = 9;    // status bits of the running call
+constexpr int kFusedDone = 10;    // workgroups finished in the running call
+// The claim ring lives in LDS; volatile, so that every read after a barrier
+// sees what thread 0 wrote before it.
+typedef __attribute__((address_space(3))) volatile int32_t lds_ring_t;
+constexpr int kFusedReady = 16;   // sync words from here: ready count per m-tile
+                                  // (words 0..7: claim counter per XCD)
+
+// HW_REG_XCC_ID (hardware register 20), bits 3:0: the XCD this wave runs on.
+__device__ __forceinline__ int hw_xcc_id() {
+  return static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (kNumXcd - 1));
+}
+
+// One XCD's work list.  Position p < n_gu is gate/up tile (m_lo + p / nt_gu,
+// p % nt_gu); n_gu <= p < total is down tile (m_lo + q / nt_dn, q % nt_dn),
+// q = p - n_gu; -1 is no tile.
+struct FusedList {
+  int m_lo, n_gu, total, nt_gu, nt_dn;
+  __device__ bool gate_up(int p) const { return p >= 0 && p < n_gu; }
+  __device__ bool down(int p) const { return p >= n_gu; }
+  __device__ int mtile(int p) const {
+    return p < n_gu ? m_lo + p / nt_gu : m_lo + (p - n_gu) / nt_dn;
+  }
+  // Logical tile index of decode_tile (m * n_tiles + n).
+  __device__ int tile(int p) const {
+    if (p < n_gu) return (m_lo + p / nt_gu) * nt_gu + p % nt_gu;
+    const int q = p - n_gu;
+    return (m_lo + q / nt_dn) * nt_dn + q % nt_dn;
+  }
+};
+
+// Waits (thread 0 only) until ready[m] >= need or the wall clock has run
+// wait_ticks past the first failed look; v is a value already loaded.
+__device__ __forceinline__ void fused_wait_ready(uint32_t v, const uint32_t* ready, int m,
+                                                 uint32_t need, uint64_t wait_ticks,
+                                                 uint32_t* status) {
+  if (v >= need) return;
+  const uint64_t t0 = static_cast<uint64_t>(wall_clock64());
+  for (;;) {
+    __builtin_amdgcn_s_sleep(2);
+    v = __hip_atomic_load(ready + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v >= need) return;
+    if (static_cast<uint64_t>(wall_clock64()) - t0 > wait_ticks) {
+      __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+  }
+}
+
+// The tiles of one phase of the fused launch (GATE_UP: gate/up with the
+// gather and the SwiGLU epilogue; else down), the claims ring[k], ring[k+1],
+// ... of this workgroup while they belong to the phase.  The pipeline is the
+// one of grouped_gemm_regs (even number of K steps, at least 4).
+template <bool GATE_UP>
+__device__ __forceinline__ void fused_phase(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int kdim, int ncols,
+    uint16_t* __restrict__ C, int64_t ldc, const int32_t* __restrict__ gather_src, int gather_k,
+    int gather_rows, const int32_t* __restrict__ offsets, int n_experts, const int32_t* tstart,
+    uint8_t* smem, lds_ring_t* ring, int& k, const FusedList& L,
+    uint32_t* __restrict__ claim_ctr, uint32_t* __restrict__ status, uint32_t* __restrict__ ready,
+    uint32_t need, uint64_t wait_ticks) {
+  constexpr bool GATHER = GATE_UP;
+  typedef GemmElem<false> E;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n_tiles_n = GATE_UP ? L.nt_gu : L.nt_dn;
+  auto ring_at = [&](int j) __attribute__((always_inline)) {
+    return __builtin_amdgcn_readfirstlane(ring[j & 3]);
+  };
+  auto mine = [&](int p) __attribute__((always_inline)) {
+    return GATE_UP ? L.gate_up(p) : L.down(p);
+  };
+  if (!mine(ring_at(k))) return;  // uniform
+  auto decode = [&](int p, int& e, int64_t& row0, int64_t& row_end, int& n0)
+      __attribute__((always_inline)) {
+    decode_tile(L.tile(p), n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+  };
+
+  if (!GATE_UP) {
+    // The first down tile: nothing of it is loaded before its m-tile is ready.
+    const int p0 = ring_at(k);
+    if (tid == 0)
+      fused_wait_ready(__hip_atomic_load(ready + L.mtile(p0), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT),
+                       ready, L.mtile(p0), need, wait_ticks, status);
+    __syncthreads();
+  }
+
+  const int row_bytes = kdim * E::kBytes;
+  const int kpad = row_bytes / 128;
+  const int ld_r = tid >> 3;
+  const int ld_c = tid & 7;
+  const int st_pos = (ld_c ^ lds_swz(ld_r)) * 16;
+  const uint32_t b_off0 = static_cast<uint32_t>(ld_r * row_bytes + ld_c * 16);
+  uint32_t a_off[8];
+  const uint8_t* a_tile = A;
+  const int b_tile_bytes = 256 * row_bytes;
+  __amdgpu_buffer_rsrc_t b_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, b_tile_bytes, kBufferWord3);
+  int ld_k = k, ld_kb = 0;
+  bool ld_done = false;
+  int32_t pf_src[8];
+  auto fetch_src = [&](int p) __attribute__((always_inline)) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode(p, e, row0, row_end, n0);
+    const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
+    const int64_t lim = row_end - 1 - r0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int rr = i * 32 + ld_r;
+      rr = rr < lim ? rr : static_cast<int>(lim);
+      pf_src[i] = gather_src[r0 + rr];
+    }
+  };
+  // The load side enters tile p; p_next is the claim after it (prefetched
+  // gather sources when it belongs to the phase).
+  auto set_load_tile = [&](int p, int p_next) __attribute__((always_inline)) {
+    int e, n0;
+    int64_t row0, row_end;
+    decode(p, e, row0, row_end, n0);
+    e = __builtin_amdgcn_readfirstlane(e);
+    n0 = __builtin_amdgcn_readfirstlane(n0);
+    const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(B + (static_cast<int64_t>(e) * ncols + n0) * row_bytes), 0,
+        b_tile_bytes, kBufferWord3);
+    const int64_t lim = row_end - 1 - r0;
+    if (GATHER) {
+      a_tile = A;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int tk = pf_src[i] >= 0 ? pf_src[i] / gather_k : 0;
+        tk = tk < gather_rows ? tk : gather_rows - 1;
+        a_off[i] = static_cast<uint32_t>(tk) * static_cast<uint32_t>(row_bytes) +
+                   static_cast<uint32_t>(ld_c * 16);
+      }
+      if (mine(p_next)) fetch_src(p_next);
+    } else {
+      a_tile = A + static_cast<int64_t>(r0) * row_bytes;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int rr = i * 32 + ld_r;
+        rr = rr < lim ? rr : static_cast<int>(lim);
+        a_off[i] = static_cast<uint32_t>(rr * row_bytes + ld_c * 16);
+      }
+    }
+  };
+  auto issue_part = [&](u32x4* ra, u32x4* rb, int p) __attribute__((always_inline)) {
+    const uint8_t* ab = a_tile + ld_kb * 128;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * p + q;
+      ra[i] = *reinterpret_cast<const u32x4*>(ab + a_off[i]);
+      rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            b_rsrc, b_off0, ld_kb * 128 + i * 32 * row_bytes, 0));
+    }
+  };
+  // After the phase's last claimed tile the load side repeats its last step.
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (ld_done) return;
+    if (++ld_kb == kpad) {
+      const int np = ring_at(ld_k + 1);
+      if (!mine(np)) {
+        ld_done = true;
+        ld_kb = kpad - 1;
+        return;
+      }
+      ld_kb = 0;
+      ++ld_k;
+      set_load_tile(np, ring_at(ld_k + 1));
+    }
+  };
+  auto park_part = [&](const u32x4* ra, const u32x4* rb, int stage, int p)
+      __attribute__((always_inline)) {
+    uint8_t* base = smem + stage * kStageBytes;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * p + q;
+      const int row = i * 32 + ld_r;
+      *reinterpret_cast<u32x4*>(base + row * 128 + st_pos) = ra[i];
+      *reinterpret_cast<u32x4*>(base + 32768 + row * 128 + st_pos) = rb[i];
+    }
+  };
+  u32x4 ra0[8], rb0[8], ra1[8], rb1[8];
+
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31;
+  const int fhalf = lane >> 5;
+  const int fa_row = wm * 128 + frow;
+  const int fb_row = wn * 128 + frow;
+  typename E::frag_t fa[2][4], fb[2][4];
+  auto read_frags = [&](int buf, int stage, int s) __attribute__((always_inline)) {
+    const uint8_t* base = smem + stage * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[buf][i] = E::read(base, (fa_row + 32 * i) * 128, fa_row, s, fhalf);
+      fb[buf][i] = E::read(base + 32768, (fb_row + 32 * i) * 128, fb_row, s, fhalf);
+    }
+  };
+  f32x16 acc[4][4];
+
+  // Per tile: thread 0 claims the position of tile k + 3 when the tile
+  // starts and publishes it in the ring at the end of K step hook_step; in
+  // the down phase it also resolves the readiness of tile k + 1 there, before
+  // the barrier, and the load side enters tile k + 1 only after that barrier
+  // (at the end of step kpad - 3 > hook_step).  In the gate/up phase the
+  // previous tile's stores are waited for (vmcnt(0)) before that barrier and
+  // counted in ready[] right after it.
+  int m_pending = -1;
+  uint32_t claimed = 0;
+  // K step (even) whose end runs the hook: the third when the tile has at
+  // least six, so the claim and the probe have two more steps to return
+  // (under the operand stream's load an atomic can outlast one K step, and
+  // the barrier would wait for it); the first otherwise.
+  const int hook_step = kpad >= 6 ? 2 : 0;
+  uint32_t probe = 0;
+  int probe_m = 0;
+  auto first_step_hook = [&]() __attribute__((always_inline)) {
+    if (GATE_UP && m_pending >= 0) wait_vm_lgkm0<0>();
+    if (tid == 0) {
+      // The empty asm pins the first read of the claim (and of the probe)
+      // here: the compiler would otherwise hoist the comparisons to the tile
+      // start, and with them the wait for the atomics' results.
+      uint32_t c = claimed;
+      asm volatile("" : "+v"(c));
+      ring[(k + 3) & 3] = c < static_cast<uint32_t>(L.total) ? static_cast<int>(c) : -1;
+      if (!GATE_UP && probe_m >= 0) {
+        uint32_t v = probe;
+        asm volatile("" : "+v"(v));
+        fused_wait_ready(v, ready, probe_m, need, wait_ticks, status);
+      }
+    }
+  };
+  auto step = [&](auto Pc, bool first) __attribute__((always_inline)) {
+    constexpr int P = decltype(Pc)::value;
+    u32x4* ld_a = P == 0 ? ra0 : ra1;
+    u32x4* ld_b = P == 0 ? rb0 : rb1;
+    const u32x4* pk_a = P == 0 ? ra1 : ra0;
+    const u32x4* pk_b = P == 0 ? rb1 : rb0;
+#pragma unroll
+    for (int s = 0; s < E::kSub; ++s) {
+      issue_part(ld_a, ld_b, s);
+      park_part(pk_a, pk_b, P ^ 1, s);
+      if (s + 1 < E::kSub) read_frags((s + 1) & 1, P, s + 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    advance();
+    if (first) first_step_hook();
+    barrier_lds();
+  };
+
+  if (GATHER) fetch_src(ring_at(k));
+  set_load_tile(ring_at(k), ring_at(k + 1));
+#pragma unroll
+  for (int p = 0; p < 4; ++p) issue_part(ra0, rb0, p);
+  advance();
+#pragma unroll
+  for (int p = 0; p < 4; ++p) issue_part(ra1, rb1, p);
+  advance();
+#pragma unroll
+  for (int p = 0; p < 4; ++p) park_part(ra0, rb0, 0, p);
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  for (;;) {
+    const int p = ring_at(k);
+    if (tid == 0) {
+      // the result is first read in the first K step's hook, so the wait for
+      // it does not hold up the step's loads
+      claimed = __hip_atomic_fetch_add(claim_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      probe_m = -1;
+      if (!GATE_UP) {
+        const int pn = ring_at(k + 1);
+        if (L.down(pn)) {
+          probe_m = L.mtile(pn);
+          probe = __hip_atomic_load(ready + probe_m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int kb = 0; kb < kpad; kb += 2) {
+      step(IntC<0>{}, kb == hook_step);
+      if (GATE_UP && kb == hook_step && m_pending >= 0) {
+        if (tid == 0)
+          __hip_atomic_fetch_add(ready + m_pending, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        m_pending = -1;
+      }
+      read_frags(0, 1, 0);
+      step(IntC<1>{}, false);
+      if (kb + 2 < kpad) read_frags(0, 0, 0);
+    }
+
+    int e, n0;
+    int64_t row0, row_end;
+    decode(p, e, row0, row_end, n0);
+    if constexpr (GATE_UP)
+      store_tile_lds_swiglu(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
+    else
+      store_tile_lds(acc, smem + kStageBytes, C, ldc, row0, row_end, n0, wm, wn, lane, tid);
+    if (GATE_UP) m_pending = L.mtile(p);
+    const bool more = mine(ring_at(k + 1));
+    ++k;
+    if (!more) break;
+    read_frags(0, 0, 0);
+  }
+  if (GATE_UP && m_pending >= 0) {
+    wait_vm_lgkm0<0>();
+    barrier_lds();
+    if (tid == 0)
+      __hip_atomic_fetch_add(ready + m_pending, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void grouped_swiglu_fused(
+    const uint8_t* __restrict__ x, const uint8_t* __restrict__ w_gu,
+    const uint8_t* __restrict__ w_dn, const int32_t* __restrict__ offsets, int n_experts,
+    int d_model, int d_ff, uint16_t* __restrict__ h, uint16_t* __restrict__ ys,
+    const int32_t* __restrict__ perm_src, int top_k, int tokens, uint32_t* __restrict__ sync,
+    uint32_t need, uint64_t wait_ticks) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int32_t tstart[kMaxExperts + 1];
+  __shared__ int32_t scan_tmp[kThreads];
+  __shared__ int32_t ring_s[4];
+  lds_ring_t* ring = (lds_ring_t*)ring_s;
+  const int tid = threadIdx.x;
+  const int m_total = __builtin_amdgcn_readfirstlane(scan_tiles(offsets, n_experts, tstart, scan_tmp));
+  const int xcc = __builtin_amdgcn_readfirstlane(hw_xcc_id());
+  FusedList L;
+  L.nt_gu = 2 * d_ff / kBN;
+  L.nt_dn = d_model / kBN;
+  L.m_lo = static_cast<int>((static_cast<int64_t>(m_total) * xcc) / kNumXcd);
+  const int m_hi = static_cast<int>((static_cast<int64_t>(m_total) * (xcc + 1)) / kNumXcd);
+  L.n_gu = (m_hi - L.m_lo) * L.nt_gu;
+  L.total = L.n_gu + (m_hi - L.m_lo) * L.nt_dn;
+  uint32_t* claim_ctr = sync + xcc;
+  uint32_t* error = sync + kFusedError;
+  uint32_t* ready = sync + kFusedReady;
+  if (tid == 0) {
+    // three claims in flight together; their results are read after all
+    // three are issued
+    uint32_t c[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      c[j] = __hip_atomic_fetch_add(claim_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) ring[j] = c[j] < static_cast<uint32_t>(L.total) ? static_cast<int>(c[j]) : -1;
+  }
+  __syncthreads();
+  int k = 0;
+  fused_phase<true>(x, w_gu, d_model, 2 * d_ff, h, d_ff, perm_src, top_k, tokens, offsets,
+                    n_experts, tstart, smem, ring, k, L, claim_ctr, error, ready, need, wait_ticks);
+  fused_phase<false>(reinterpret_cast<const uint8_t*>(h), w_dn, d_ff, d_model, ys, d_model,
+                     nullptr, 1, 1, offsets, n_experts, tstart, smem, ring, k, L, claim_ctr,
+                     error, ready, need, wait_ticks);
+  // The last workgroup to finish publishes the status and clears every
+  // counter for the next call.  Thread 0 waits for its own atomics first
+  // (vmcnt(0)), so no count of this workgroup can land after the clearing.
+  wait_vm_lgkm0<0>();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t d =
+        __hip_atomic_fetch_add(sync + kFusedDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ring[0] = d == gridDim.x - 1 ? 1 : 0;
+  }
+  __syncthreads();
+  if (ring[0]) {
+    for (int i = tid; i < m_total; i += kThreads) ready[i] = 0u;
+    if (tid < kNumXcd) sync[tid] = 0u;
+    if (tid == 0) {
+      sync[kFusedStatus] =
+          __hip_atomic_exchange(error, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sync[kFusedDone] = 0u;
+    }
+  }
+}
+
 // Workgroups per launch: one per CU, a multiple of the XCD count.
 int persistent_grid(hipStream_t s, int* grid, int* dev_out) {
   int dev = 0;
@@ -1262,6 +1687,7 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, false>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<false, false>),
+      reinterpret_cast<const void*>(grouped_swiglu_fused),
   };
   bool ok = true;
   for (const void* k : kernels) ok = ok && set_lds_limit(k, bytes);
@@ -1397,6 +1823,81 @@ extern "C" int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_ex
   return launch_grouped(false, false, h, w_down_packed, nullptr, nullptr, offsets, n_experts,
                         rows_cap, d_ff, d_model, ys, d_model, static_cast<hipStream_t>(stream),
                         "hmoe_grouped_down");
+}
+
+namespace hmoe {
+namespace {
+// Ticks of the wall clock (s_memrealtime) per microsecond, once per device.
+int wall_ticks_per_us(int dev, int64_t* out) {
+  static std::atomic<int64_t> cached[64];
+  int64_t v = dev >= 0 && dev < 64 ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (v == 0) {
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) {
+      set_error("grouped_swiglu_fused: cannot query the wall clock rate of device %d", dev);
+      return HMOE_ERR_HIP;
+    }
+    v = (khz + 999) / 1000;
+    if (dev >= 0 && dev < 64) cached[dev].store(v, std::memory_order_relaxed);
+  }
+  *out = v;
+  return HMOE_OK;
+}
+}  // namespace
+}  // namespace hmoe
+
+extern "C" size_t hmoe_grouped_swiglu_fused_workspace_bytes(int64_t rows_cap, int n_experts) {
+  using namespace hmoe;
+  if (rows_cap < 0 || n_experts < 1) return 0;
+  return static_cast<size_t>(kFusedReady + ceil_div(rows_cap, kBM) + n_experts) * sizeof(uint32_t);
+}
+
+extern "C" int hmoe_grouped_swiglu_fused(const void* x, int64_t tokens, int top_k,
+                                         const int32_t* perm_src, const int32_t* offsets,
+                                         int n_experts, int64_t rows_cap, int d_model, int d_ff,
+                                         const void* w_gate_up_packed, const void* w_down_packed,
+                                         void* h, void* ys, void* workspace,
+                                         size_t workspace_bytes, int64_t wait_timeout_us,
+                                         int extra_ready_needed, hmoe_stream_t stream) {
+  using namespace hmoe;
+  const char* what = "hmoe_grouped_swiglu_fused";
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "%s: n_experts must be in [1, %d] (got %d)", what, kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
+               "%s: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)", what);
+  HMOE_REQUIRE_CODE(d_model % kBN == 0 && d_model >= kBN, HMOE_ERR_UNSUPPORTED,
+                    "%s: d_model must be a multiple of %d (got %d)", what, kBN, d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff >= kBN,
+                    HMOE_ERR_UNSUPPORTED,
+                    "%s: d_ff must be a multiple of %d and at least %d (got %d)", what, kBN / 2,
+                    kBN, d_ff);
+  HMOE_REQUIRE(extra_ready_needed >= 0, "%s: extra_ready_needed must be >= 0", what);
+  HMOE_REQUIRE(tokens * d_model * 2 < (int64_t(1) << 31), "%s: x must be smaller than 2 GiB", what);
+  HMOE_REQUIRE(rows_cap < (int64_t(1) << 31), "%s: rows_cap must fit in int32", what);
+  HMOE_REQUIRE(static_cast<int64_t>(kBM) * d_model * 2 < (int64_t(1) << 31),
+               "%s: output rows too wide", what);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && perm_src && offsets && w_gate_up_packed && w_down_packed && h && ys && workspace,
+               "%s: null pointer argument", what);
+  const size_t need_ws = hmoe_grouped_swiglu_fused_workspace_bytes(rows_cap, n_experts);
+  HMOE_REQUIRE_CODE(workspace_bytes >= need_ws, HMOE_ERR_WORKSPACE,
+                    "%s: workspace of %zu bytes, %zu needed", what, workspace_bytes, need_ws);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = 0, grid = 0;
+  if (int rc = persistent_grid(s, &grid, &dev)) return rc;
+  if (int rc = allow_dynamic_lds(dev)) return rc;
+  int64_t tpu = 0;
+  if (int rc = wall_ticks_per_us(dev, &tpu)) return rc;
+  const int64_t us = wait_timeout_us > 0 ? wait_timeout_us : 200000;  // default 0.2 s
+  const uint64_t ticks = static_cast<uint64_t>(us) * static_cast<uint64_t>(tpu);
+  uint32_t* sync = static_cast<uint32_t*>(workspace);
+  const uint32_t need = static_cast<uint32_t>(2 * d_ff / kBN + extra_ready_needed);
+  hipLaunchKernelGGL(grouped_swiglu_fused, dim3(grid), dim3(kThreads), 2 * kStageBytes, s,
+                     static_cast<const uint8_t*>(x), static_cast<const uint8_t*>(w_gate_up_packed),
+                     static_cast<const uint8_t*>(w_down_packed), offsets, n_experts, d_model, d_ff,
+                     static_cast<uint16_t*>(h), static_cast<uint16_t*>(ys), perm_src, top_k,
+                     static_cast<int>(tokens), sync, need, ticks);
+  return check_launch(what);
 }
 
 // ---- backward (the VJP of moe.py:70-74) -------------------------------------

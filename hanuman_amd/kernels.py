@@ -289,6 +289,53 @@ def grouped_down(h: torch.Tensor, offsets: torch.Tensor, w_down: torch.Tensor,
     return ys
 
 
+FUSED_STATUS_WORD = 8   # uint32 word of the fused launch's workspace: bit 0 = a wait gave up
+
+
+def grouped_swiglu_fused_workspace(plan: Plan) -> torch.Tensor:
+    """Workspace of :func:`grouped_swiglu_fused` for plans of this shape."""
+    n = int(_lib.lib().hmoe_grouped_swiglu_fused_workspace_bytes(plan.rows_cap, plan.n_experts))
+    # zero before the first call; every call leaves it zeroed again
+    return torch.zeros(max(n, 4 * (FUSED_STATUS_WORD + 1)), dtype=torch.uint8,
+                       device=plan.offsets.device)
+
+
+def grouped_swiglu_fused(x: torch.Tensor, plan: Plan, w_gate_up: torch.Tensor,
+                         w_down: torch.Tensor, workspace: torch.Tensor | None = None,
+                         wait_timeout_us: int = 0, extra_ready_needed: int = 0):
+    """``h`` and ``ys`` of :func:`grouped_gate_up_gather` then :func:`grouped_down`
+    in one persistent launch (``moe.py:56,70-74``), bit-identical.  Returns
+    ``(h, ys, workspace)``; word :data:`FUSED_STATUS_WORD` of the workspace
+    (uint32) is 0 when every down tile's wait for its gate/up tiles was met.
+    A workspace passed in must have been zero before its first call (as
+    :func:`grouped_swiglu_fused_workspace` makes it); each call leaves it so."""
+    _check(x, "x", 2)
+    _check(w_gate_up, "w_gate_up", 3)
+    _check(w_down, "w_down", 3)
+    if x.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:
+        raise TypeError("grouped_swiglu_fused takes bf16 operands")
+    T, D = x.shape
+    N, F2, D2 = w_gate_up.shape
+    if (D2 != D or plan.n_experts != N or plan.slot_pos.numel() != T * plan.top_k
+            or tuple(w_down.shape) != (N, D, F2 // 2)):
+        raise ValueError("grouped_swiglu_fused: inconsistent shapes")
+    if workspace is None:
+        workspace = grouped_swiglu_fused_workspace(plan)
+    _check(workspace, "workspace", 1)
+    h = torch.empty((plan.rows_cap, F2 // 2), dtype=torch.bfloat16, device=x.device)
+    ys = torch.empty((plan.rows_cap, D), dtype=torch.bfloat16, device=x.device)
+    call("hmoe_grouped_swiglu_fused", _ptr(x), T, plan.top_k, _ptr(plan.perm_src),
+         _ptr(plan.offsets), N, plan.rows_cap, D, F2 // 2, _ptr(w_gate_up), _ptr(w_down), _ptr(h),
+         _ptr(ys), _ptr(workspace), workspace.numel() * workspace.element_size(),
+         int(wait_timeout_us), int(extra_ready_needed), _stream())
+    return h, ys, workspace
+
+
+def fused_status(workspace: torch.Tensor) -> int:
+    """Status word of a fused launch's workspace (synchronises with the device)."""
+    return int(workspace[4 * FUSED_STATUS_WORD:4 * FUSED_STATUS_WORD + 4].view(torch.int32).item())
+
+
 def grouped_gate_up_f32(xs: torch.Tensor, offsets: torch.Tensor, w_gate: torch.Tensor,
                         w_up: torch.Tensor) -> torch.Tensor:
     """Float32 ``h = silu(xs Wg[e]) * (xs Wu[e])`` per expert segment

@@ -19,7 +19,8 @@ _TORCH_DT = {"bf16": torch.bfloat16, "f32": torch.float32}
 
 
 class DeviceLayer:
-    def __init__(self, inp: Inputs, device: str | torch.device = "cuda"):
+    def __init__(self, inp: Inputs, device: str | torch.device = "cuda",
+                 fused_ffn: bool | None = None):
         wl: Workload = inp.wl
         if wl.expert_dtype not in ("bf16", "fp8", "f32"):
             raise NotImplementedError(f"{wl.name}: expert dtype {wl.expert_dtype} is not built")
@@ -71,6 +72,17 @@ class DeviceLayer:
                            and self.x.dtype == torch.bfloat16)
         ws = int(_lib.lib().hmoe_plan_workspace_bytes(wl.tokens, wl.top_k, wl.n_experts))
         self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
+        # The gathered gate/up GEMM and the down GEMM in one persistent launch
+        # (hmoe_grouped_swiglu_fused) where its shape rules hold; fused_ffn=False
+        # keeps the two launches.
+        can_fuse = (self.fused_dispatch and wl.d_model % 256 == 0 and wl.d_ff % 128 == 0
+                    and wl.d_ff >= 256)
+        self.fused_ffn = can_fuse if fused_ffn is None else (bool(fused_ffn) and can_fuse)
+        self.fused_ws = None
+        if self.fused_ffn:
+            rc = K.rows_cap(wl.tokens, wl.top_k, wl.n_experts, self.capacity)
+            n = int(_lib.lib().hmoe_grouped_swiglu_fused_workspace_bytes(rc, wl.n_experts))
+            self.fused_ws = torch.zeros(max(n, 64), dtype=torch.uint8, device=dev)
         self.out_dtype = _TORCH_DT[wl.out_dtype]
 
     # ---- stages (each enqueues on the current stream) ----------------------
@@ -112,6 +124,10 @@ class DeviceLayer:
             xs = K.permute_rows(self.x, plan, torch.float32)
             h = K.grouped_gate_up_f32(xs, plan.offsets, self.w_gate, self.w_up)
             ys = K.grouped_down_f32(h, plan.offsets, self.w_down_f32)
+        elif self.fused_ffn:
+            xs = None
+            h, ys, _ = K.grouped_swiglu_fused(self.x, plan, self.w_gate_up, self.w_down,
+                                              self.fused_ws)
         elif self.fused_dispatch:
             xs = None
             h = K.grouped_gate_up_gather(self.x, plan, self.w_gate_up)

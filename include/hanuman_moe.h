@@ -205,6 +205,32 @@ int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
                       int64_t rows_cap, int d_ff, int d_model,
                       const void* w_down_packed, void* ys, hmoe_stream_t stream);
 
+/* The layer's whole expert FFN in one persistent launch (moe.py:56,70-74:
+ * the gathered gate/up GEMM with the SwiGLU, then the down GEMM): h and ys
+ * are bit-identical to hmoe_grouped_gate_up_gather followed by
+ * hmoe_grouped_down.  Each XCD of the GPU takes an even share of the 256-row
+ * m-tiles and runs their gate/up tiles, then their down tiles; a down tile
+ * starts once the gate/up tiles of its m-tile are stored (per-m-tile counts
+ * in the workspace).  A wait that runs past wait_timeout_us (<= 0: 200 ms)
+ * gives up and sets bit 0 of the workspace's uint32 word 8 (status; 0 when
+ * every wait was met), and that tile's ys is not meaningful; every launch
+ * exits.  extra_ready_needed > 0 raises the count a down tile waits for
+ * past what the gate/up tiles can reach, so that every wait gives up (it
+ * exists to test that path; pass 0).  Workspace: at least
+ * hmoe_grouped_swiglu_fused_workspace_bytes(rows_cap, n_experts) bytes,
+ * zero-filled before its first call; every call leaves its counters at zero
+ * again (and word 8 holding its status), so no clearing is needed between
+ * calls.  Calls that overlap in time must not share one.  D % 256 == 0,
+ * F % 128 == 0 and F >= 256, tokens * D * 2 < 2^31. */
+size_t hmoe_grouped_swiglu_fused_workspace_bytes(int64_t rows_cap, int n_experts);
+int hmoe_grouped_swiglu_fused(const void* x, int64_t tokens, int top_k,
+                              const int32_t* perm_src, const int32_t* offsets, int n_experts,
+                              int64_t rows_cap, int d_model, int d_ff,
+                              const void* w_gate_up_packed, const void* w_down_packed, void* h,
+                              void* ys, void* workspace, size_t workspace_bytes,
+                              int64_t wait_timeout_us, int extra_ready_needed,
+                              hmoe_stream_t stream);
+
 /* fp8 expert GEMMs (workload rule): e4m3 operands on the CDNA4 32x32x64
  * fp8 MFMA with float32 accumulation; the accumulators are dequantised with
  * the row scale times the column scale, then (gate/up) g and u are rounded to
