@@ -52,6 +52,7 @@ SIGNATURES = {
                                            _vp, _vp]),
     "hmoe_grouped_down": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "hmoe_grouped_swiglu_fused_workspace_bytes": (_sz, [_i64, _i32]),
+    "hmoe_zero_fill": (_i32, [_vp, _sz, _vp]),
     "hmoe_grouped_swiglu_fused": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32, _i32, _vp,
                                          _vp, _vp, _vp, _vp, _sz, _i64, _i32, _vp]),
     "hmoe_combine": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp]),

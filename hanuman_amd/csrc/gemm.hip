@@ -1846,6 +1846,28 @@ int wall_ticks_per_us(int dev, int64_t* out) {
 }  // namespace
 }  // namespace hmoe
 
+namespace hmoe {
+namespace {
+__global__ void zero_fill_kernel(uint32_t* __restrict__ p, int64_t words) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+}  // namespace
+}  // namespace hmoe
+
+extern "C" int hmoe_zero_fill(void* buffer, size_t bytes, hmoe_stream_t stream) {
+  using namespace hmoe;
+  HMOE_REQUIRE(bytes % 4 == 0, "zero_fill: byte count must be a multiple of 4 (got %zu)", bytes);
+  if (bytes == 0) return HMOE_OK;
+  HMOE_REQUIRE(buffer != nullptr, "zero_fill: null buffer");
+  const int64_t words = static_cast<int64_t>(bytes / 4);
+  const int blocks = static_cast<int>(ceil_div(words, 256) < 1024 ? ceil_div(words, 256) : 1024);
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint32_t*>(buffer), words);
+  return check_launch("hmoe_zero_fill");
+}
+
 extern "C" size_t hmoe_grouped_swiglu_fused_workspace_bytes(int64_t rows_cap, int n_experts) {
   using namespace hmoe;
   if (rows_cap < 0 || n_experts < 1) return 0;

@@ -223,6 +223,11 @@ int hmoe_grouped_down(const void* h, const int32_t* offsets, int n_experts,
  * calls.  Calls that overlap in time must not share one.  D % 256 == 0,
  * F % 128 == 0 and F >= 256, tokens * D * 2 < 2^31. */
 size_t hmoe_grouped_swiglu_fused_workspace_bytes(int64_t rows_cap, int n_experts);
+/* Sets `bytes` (a multiple of 4) of device memory to zero with a kernel
+ * (graph-capturable, unlike a memset node): the first-use clearing of a
+ * fused workspace that a caller allocates afresh per call (an XLA result
+ * buffer).  No counterpart in the reference. */
+int hmoe_zero_fill(void* buffer, size_t bytes, hmoe_stream_t stream);
 int hmoe_grouped_swiglu_fused(const void* x, int64_t tokens, int top_k,
                               const int32_t* perm_src, const int32_t* offsets, int n_experts,
                               int64_t rows_cap, int d_model, int d_ff,
