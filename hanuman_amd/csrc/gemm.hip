@@ -995,9 +995,11 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
 // the 32x32x16 operand.  Tiles: every expert (an empty one too, whose
 // gradient is zero) x (M / 256) x (N / 256), persistent as in the forward.
 // Rows past the segment read zeros: the loads are raw buffer loads whose
-// range ends at the segment's last row (the row offset is in the
-// range-checked VGPR offset), so a tile runs max(2, ceil(rows / 64)) steps,
-// rounded up to even, with no masking.  The output is float32; SPLIT: B's
+// resource starts at the K step's first row and ends at the segment's last
+// row (the row within the step is in the range-checked VGPR offset), so a
+// tile runs max(2, ceil(rows / 64)) steps, rounded up to even, with no
+// masking, and neither a segment nor the operand buffers are limited to
+// 2 GiB.  The output is float32; SPLIT: B's
 // columns are in the gate/up order (blocks of 32 gate columns, then the 32 up
 // columns of the same h columns) and C goes to out0 (gate) and out1 (up) as
 // [e][m][F].
@@ -1051,24 +1053,32 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
   auto swz = [](int k, int byte) __attribute__((always_inline)) {
     return (((byte >> 5) ^ (2 * (k & 3))) << 5) | (byte & 31);
   };
+  // The buffer resources of a K step start at its first row and end at the
+  // segment's last row (or hold nothing past it), so every offset is within
+  // 64 rows of the base and no segment or buffer size limits the kernel.
   __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, 0, kBufferWord3);
   __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, 0, kBufferWord3);
   Tile lt = decode(first);
   int ld_t = first, ld_kb = 0;
   bool ld_more = true;
+  auto set_step_rsrc = [&]() __attribute__((always_inline)) {
+    const int64_t r0 = lt.seg0 + static_cast<int64_t>(ld_kb) * 64;
+    int left = lt.rows - ld_kb * 64;
+    left = left < 0 ? 0 : (left > 64 ? 64 : left);
+    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A + r0 * M + lt.m0), 0,
+                                               left * a_row_bytes, kBufferWord3);
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B + r0 * N + lt.n0), 0,
+                                               left * b_row_bytes, kBufferWord3);
+  };
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     lt = decode(t);
-    const uint32_t nr = static_cast<uint32_t>(lt.rows);
-    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(A + lt.seg0 * M + lt.m0), 0, static_cast<int>(nr * a_row_bytes), kBufferWord3);
-    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(B + lt.seg0 * N + lt.n0), 0, static_cast<int>(nr * b_row_bytes), kBufferWord3);
+    set_step_rsrc();
   };
   auto issue_part = [&](u32x4* ra, u32x4* rb, int p) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int i = 2 * p + q;
-      const int k = ld_kb * 64 + 8 * i + ld_r;
+      const int k = 8 * i + ld_r;
       ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             a_rsrc, k * a_row_bytes + ld_c * 16, 0, 0));
       rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -1085,6 +1095,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
         ld_kb = lt.kpad - 1;
         ld_more = false;
       }
+    } else if (ld_more) {
+      set_step_rsrc();
     }
   };
   auto park_part = [&](const u32x4* ra, const u32x4* rb, int stage, int p) __attribute__((always_inline)) {
@@ -2137,6 +2149,10 @@ namespace hmoe {
 namespace {
 int launch_wgrad(bool split, const void* A, const void* B, const int32_t* offsets, int n_experts,
                  int M, int N, float* out0, float* out1, hipStream_t s, const char* what) {
+  HMOE_REQUIRE(static_cast<int64_t>(64) * (M > N ? M : N) * 2 < (int64_t(1) << 31),
+               "%s: rows too wide", what);
+  HMOE_REQUIRE(static_cast<int64_t>(n_experts) * (M / kBM) * (N / kBN) < (int64_t(1) << 31),
+               "%s: too many tiles", what);
   int dev = 0;
   int grid = 0;
   if (int rc = persistent_grid(s, &grid, &dev)) return rc;
@@ -2165,9 +2181,8 @@ extern "C" int hmoe_grouped_wgrad_down(const void* h, const void* d_ys, const in
                     HMOE_ERR_UNSUPPORTED,
                     "grouped_wgrad_down: d_ff and d_model must be multiples of 256 (got %d, %d)",
                     d_ff, d_model);
-  HMOE_REQUIRE(rows_cap >= 0 && rows_cap * static_cast<int64_t>(d_model) * 2 < (int64_t(1) << 31) &&
-                   rows_cap * static_cast<int64_t>(d_ff) * 2 < (int64_t(1) << 31),
-               "grouped_wgrad_down: h and d_ys must be smaller than 2 GiB");
+  HMOE_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31),
+               "grouped_wgrad_down: rows_cap must fit in int32");
   HMOE_REQUIRE(h && d_ys && offsets && dw_down, "grouped_wgrad_down: null pointer argument");
   return launch_wgrad(false, h, d_ys, offsets, n_experts, d_ff, d_model, dw_down, nullptr,
                       static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_down");
@@ -2184,9 +2199,8 @@ extern "C" int hmoe_grouped_wgrad_gate_up(const void* xs, const void* dgu, const
                     HMOE_ERR_UNSUPPORTED,
                     "grouped_wgrad_gate_up: d_model must be a multiple of 256 and d_ff of 128 "
                     "(got %d, %d)", d_model, d_ff);
-  HMOE_REQUIRE(rows_cap >= 0 && rows_cap * static_cast<int64_t>(d_model) * 2 < (int64_t(1) << 31) &&
-                   rows_cap * static_cast<int64_t>(d_ff) * 4 < (int64_t(1) << 31),
-               "grouped_wgrad_gate_up: xs and dgu must be smaller than 2 GiB");
+  HMOE_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31),
+               "grouped_wgrad_gate_up: rows_cap must fit in int32");
   HMOE_REQUIRE(xs && dgu && offsets && dw_gate && dw_up,
                "grouped_wgrad_gate_up: null pointer argument");
   return launch_wgrad(true, xs, dgu, offsets, n_experts, d_model, 2 * d_ff, dw_gate, dw_up,

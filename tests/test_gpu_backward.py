@@ -620,3 +620,45 @@ def test_module_autograd_saved_tensors(gpu):
     torch.cuda.synchronize()
     assert torch.equal(xg2.grad, dx_first)
     assert all(getattr(m, n).value.grad is None for n in names)
+
+
+def test_wgrad_gemms_past_2gib(gpu):
+    """Weight gradients on dispatched buffers larger than 2 GiB (the skewed
+    workload's backward: 65536 tokens x top-8 rows of d_model 2048 are 2 GiB
+    of bf16): each K step's buffer resource starts at its own first row, so
+    experts whose rows lie past byte 2^31 are computed like the first ones.
+    Sampled experts (the first, one in the middle, the last two, an empty
+    one) against float64 on the same bf16 operands."""
+    D, F, N = 2048, 768, 128
+    rng = np.random.default_rng(77)
+    sizes = rng.integers(4000, 4800, N)
+    sizes[5] = 0                                     # an empty expert
+    offsets = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(offsets[-1])
+    assert R * D * 2 > 2 ** 31 and int(offsets[-3]) * D * 2 > 2 ** 31
+    print(f"wgrad past 2 GiB: R={R} D={D} F={F} N={N}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    xs = torch.randn(R, D, generator=g, device=gpu).to(torch.bfloat16)
+    dgu = torch.randn(R, 2 * F, generator=g, device=gpu).to(torch.bfloat16)
+    h = torch.randn(R, F, generator=g, device=gpu).to(torch.bfloat16)
+    d_ys = torch.randn(R, D, generator=g, device=gpu).to(torch.bfloat16)
+    off_d = torch.from_numpy(offsets).to(gpu)
+    dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, off_d)
+    dwd = K.grouped_wgrad_down(h, d_ys, off_d)
+    torch.cuda.synchronize()
+    col = np.arange(F)
+    gc = (col // 32) * 64 + col % 32
+    for e in (0, 5, N // 2, N - 2, N - 1):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if b == a:
+            assert torch.all(dwg[e] == 0) and torch.all(dwu[e] == 0) and torch.all(dwd[e] == 0)
+            continue
+        x64 = host(xs[a:b]).astype(np.float64)
+        g64 = host(dgu[a:b]).astype(np.float64)
+        for name, got, ref in (("dWg", dwg[e], x64.T @ g64[:, gc]),
+                               ("dWu", dwu[e], x64.T @ g64[:, gc + 32]),
+                               ("dWd", dwd[e], host(h[a:b]).astype(np.float64).T
+                                @ host(d_ys[a:b]).astype(np.float64))):
+            err = O.normwise_rel_err(host(got), ref)
+            print(f"  expert {e} rows {a}-{b} {name}: {err:.2e}", flush=True)
+            assert err < 1e-5, (name, e, err)
