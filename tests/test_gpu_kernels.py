@@ -275,6 +275,9 @@ PLAN_CASES = [
     ("cap1", 1000, 4, 16, 0.001),
     ("one_expert", 700, 1, 1, 0.5),
     ("ragged_blocks", 4097, 3, 1000, 1.0),
+    # 128 blocks x 1024 experts: past the fused rank's histogram limit, so
+    # the three-pass plan (histogram, column scan, rank)
+    ("wide_histogram", 16384, 8, 1024, 1.25),
 ]
 
 

@@ -79,3 +79,16 @@ def test_noalloc_plan_rejects_oversized_plan(gpu):
     rc = lib.hmoe_dispatch_plan_noalloc(p, T, K, N, T * K, p, p, p, p, p, stream)
     assert rc == _lib.ERR_WORKSPACE
     assert "scratch" in lib.hmoe_last_error().decode()
+
+
+def test_noalloc_plan_first_call_inside_graph_capture(gpu):
+    """In a fresh process, the first hmoe_dispatch_plan_noalloc call (which
+    looks the scratch array's address up) is made during a HIP graph capture;
+    the graph's replays match hmoe_dispatch_plan bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    child = Path(__file__).with_name("noalloc_capture_child.py")
+    r = subprocess.run([sys.executable, str(child)], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "noalloc capture ok" in r.stdout
