@@ -85,6 +85,8 @@ def algorithmic(wl, kept_rows: int) -> dict:
             # h (bf16) read once, codes and row scales written
             w["quant_h"] = ("hbm", kept_rows * F * 2 + kept_rows * F + kept_rows * 4, HBM_PEAK_GBS)
         w["down"] = ("mfma", 2 * kept_rows * F * D, mfma_peak)
+        # gate/up and down in one persistent launch (--fused-ffn)
+        w["ffn"] = ("mfma", 6 * kept_rows * D * F, mfma_peak)
     # combine: read kept rows (bf16), write tokens, read slot map and gates
     w["combine"] = ("hbm", kept_rows * D * 2 + T * D * out_b + R * 8, HBM_PEAK_GBS)
     return w
@@ -194,6 +196,9 @@ def main():
                          "default is the whole headline workload, ~10 s of CPU work)")
     ap.add_argument("--train", action="store_true",
                     help="time one training step of the MoE module (forward, backward, update)")
+    ap.add_argument("--fused-ffn", action="store_true",
+                    help="run the bf16 gate/up and down GEMMs as one persistent launch "
+                         "(hmoe_grouped_swiglu_fused) instead of two")
     ap.add_argument("--backward", action="store_true",
                     help="time the data-gradient backward pass instead of the forward")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -219,7 +224,7 @@ def main():
     log(f"[bench] workload {name}: T={wl.tokens} D={wl.d_model} N={wl.n_experts} "
         f"K={wl.top_k} F={wl.d_ff} CF={wl.capacity_factor}")
     inp = W.make_inputs(wl, seed=args.seed)
-    layer = DeviceLayer(inp, dev)
+    layer = DeviceLayer(inp, dev, fused_ffn=args.fused_ffn)
     del inp
     torch.cuda.synchronize()
 
@@ -237,7 +242,8 @@ def main():
     fp8_gather = layer.fp8_gather
     stages = ["router", "plan"] + (["quant_x"] if fp8_gather else [] if fused else ["permute"])
     if wl.expert == "swiglu":
-        stages += ["gate_up", "quant_h", "down"] if fp8 else ["gate_up", "down"]
+        stages += (["gate_up", "quant_h", "down"] if fp8 else
+                   ["ffn"] if layer.fused_ffn else ["gate_up", "down"])
     stages += ["combine"]
 
     def step(ev=None):
@@ -272,6 +278,10 @@ def main():
             h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
             mark()
             ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, layer.w_down, layer.w_down_scale)
+            mark()
+        elif layer.fused_ffn:
+            h, ys, _ = K.grouped_swiglu_fused(layer.x, plan, layer.w_gate_up, layer.w_down,
+                                              layer.fused_ws)
             mark()
         elif fused:
             h = K.grouped_gate_up_gather(layer.x, plan, layer.w_gate_up)
@@ -392,7 +402,19 @@ def main():
     tokens_per_s = wl.tokens / (ms_per_step / 1e3)
     traffic = measured_traffic(name)
     grouped_gemm = None
-    if wl.expert == "swiglu":
+    if wl.expert == "swiglu" and layer.fused_ffn:
+        # Dominant kernel: the one launch of both grouped GEMMs.
+        kname = "grouped_swiglu_fused"
+        flop, peak = work["ffn"][1], work["ffn"][2]
+        ach = flop / (stage_ms["ffn"] / 1e3) / 1e12
+        roofline = {"kernel": kname, "bound": "mfma", "achieved": round(ach, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                    "traffic": traffic.get(kname), "flop_per_launch": flop,
+                    "ms": round(stage_ms["ffn"], 4)}
+        grouped_gemm = {"kernels": "gate/up + down (one launch)", "flop": flop,
+                        "ms": round(stage_ms["ffn"], 4), "achieved": round(ach, 1),
+                        "unit": "TFLOP/s", "frac": round(ach / peak, 4)}
+    elif wl.expert == "swiglu":
         # Dominant kernel: the gate/up grouped GEMM with the fused SwiGLU
         # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1

@@ -995,15 +995,14 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
 // the 32x32x16 operand.  Tiles: every expert (an empty one too, whose
 // gradient is zero) x (M / 256) x (N / 256), persistent as in the forward.
 // Rows past the segment read zeros: the loads are raw buffer loads whose
-// resource starts at the K step's first row and ends at the segment's last
-// row (the row within the step is in the range-checked VGPR offset), so a
-// tile runs max(2, ceil(rows / 64)) steps, rounded up to even, with no
-// masking, and neither a segment nor the operand buffers are limited to
-// 2 GiB.  The output is float32; SPLIT: B's
+// resource ends at the segment's last row (the row offset is in the
+// range-checked VGPR offset; a segment of 2 GiB or more rebases its
+// resources at every K step), so a tile runs max(2, ceil(rows / 64)) steps,
+// rounded up to even, with no masking, and no buffer size limits it.  The output is float32; SPLIT: B's
 // columns are in the gate/up order (blocks of 32 gate columns, then the 32 up
 // columns of the same h columns) and C goes to out0 (gate) and out1 (up) as
 // [e][m][F].
-template <bool SPLIT>
+template <bool SPLIT, bool BIG>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const int32_t* __restrict__ offsets, int n_experts, int M, int N, float* __restrict__ out0,
@@ -1053,32 +1052,53 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
   auto swz = [](int k, int byte) __attribute__((always_inline)) {
     return (((byte >> 5) ^ (2 * (k & 3))) << 5) | (byte & 31);
   };
-  // The buffer resources of a K step start at its first row and end at the
-  // segment's last row (or hold nothing past it), so every offset is within
-  // 64 rows of the base and no segment or buffer size limits the kernel.
+  // A tile's buffer resources start at its segment's first row and end at
+  // its last (the row offset k * row_bytes is in the range-checked VGPR
+  // offset), which holds while the segment is below 2 GiB, whatever the size
+  // of the whole buffer.  BIG (chosen by the host when the buffer could hold
+  // a segment of 2 GiB or more): a tile whose segment is that large rebases
+  // both resources at every K step instead, so its offsets stay within 64
+  // rows.  (The two loaders are separate instantiations: the BIG one's extra
+  // bookkeeping costs the common case about a third of its speed.)
   __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, 0, kBufferWord3);
   __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, 0, kBufferWord3);
   Tile lt = decode(first);
   int ld_t = first, ld_kb = 0;
   bool ld_more = true;
-  auto set_step_rsrc = [&]() __attribute__((always_inline)) {
-    const int64_t r0 = lt.seg0 + static_cast<int64_t>(ld_kb) * 64;
-    int left = lt.rows - ld_kb * 64;
-    left = left < 0 ? 0 : (left > 64 ? 64 : left);
-    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A + r0 * M + lt.m0), 0,
-                                               left * a_row_bytes, kBufferWord3);
-    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B + r0 * N + lt.n0), 0,
-                                               left * b_row_bytes, kBufferWord3);
+  int ld_koff = 0;      // BIG: row of the current K step relative to the resources' base
+  bool ld_big = false;  // BIG: the load tile's segment is rebased per K step
+  const int max_row_bytes = a_row_bytes > b_row_bytes ? a_row_bytes : b_row_bytes;
+  auto set_rsrc = [&](int row_from) __attribute__((always_inline)) {
+    const int64_t r0 = lt.seg0 + row_from;
+    int left = lt.rows - row_from;
+    left = left < 0 ? 0 : left;
+    if (ld_big) left = left > 64 ? 64 : left;
+    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(A + r0 * M + lt.m0), 0,
+        static_cast<int>(static_cast<uint32_t>(left) * a_row_bytes), kBufferWord3);
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(B + r0 * N + lt.n0), 0,
+        static_cast<int>(static_cast<uint32_t>(left) * b_row_bytes), kBufferWord3);
   };
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     lt = decode(t);
-    set_step_rsrc();
+    if constexpr (BIG) {
+      ld_big = static_cast<int64_t>(lt.kpad) * 64 * max_row_bytes >= (int64_t(1) << 31);
+      ld_koff = 0;
+      set_rsrc(0);
+    } else {
+      const uint32_t nr = static_cast<uint32_t>(lt.rows);
+      a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(A + lt.seg0 * M + lt.m0), 0, static_cast<int>(nr * a_row_bytes), kBufferWord3);
+      b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(B + lt.seg0 * N + lt.n0), 0, static_cast<int>(nr * b_row_bytes), kBufferWord3);
+    }
   };
   auto issue_part = [&](u32x4* ra, u32x4* rb, int p) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int i = 2 * p + q;
-      const int k = 8 * i + ld_r;
+      const int k = (BIG ? ld_koff : ld_kb * 64) + 8 * i + ld_r;
       ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             a_rsrc, k * a_row_bytes + ld_c * 16, 0, 0));
       rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -1095,8 +1115,11 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_wgrad(
         ld_kb = lt.kpad - 1;
         ld_more = false;
       }
-    } else if (ld_more) {
-      set_step_rsrc();
+    } else if (BIG && ld_more) {
+      if (ld_big)
+        set_rsrc(ld_kb * 64);
+      else
+        ld_koff = ld_kb * 64;
     }
   };
   auto park_part = [&](const u32x4* ra, const u32x4* rb, int stage, int p) __attribute__((always_inline)) {
@@ -1694,8 +1717,10 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, false, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<false, false, true, true>),
       reinterpret_cast<const void*>(grouped_gemm_regs<false, true, true, true>),
-      reinterpret_cast<const void*>(grouped_gemm_wgrad<false>),
-      reinterpret_cast<const void*>(grouped_gemm_wgrad<true>),
+      reinterpret_cast<const void*>(grouped_gemm_wgrad<false, false>),
+      reinterpret_cast<const void*>(grouped_gemm_wgrad<true, false>),
+      reinterpret_cast<const void*>(grouped_gemm_wgrad<false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_wgrad<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, false>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<false, false>),
@@ -2148,7 +2173,8 @@ extern "C" int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale,
 namespace hmoe {
 namespace {
 int launch_wgrad(bool split, const void* A, const void* B, const int32_t* offsets, int n_experts,
-                 int M, int N, float* out0, float* out1, hipStream_t s, const char* what) {
+                 int64_t rows_cap, int M, int N, float* out0, float* out1, hipStream_t s,
+                 const char* what) {
   HMOE_REQUIRE(static_cast<int64_t>(64) * (M > N ? M : N) * 2 < (int64_t(1) << 31),
                "%s: rows too wide", what);
   HMOE_REQUIRE(static_cast<int64_t>(n_experts) * (M / kBM) * (N / kBN) < (int64_t(1) << 31),
@@ -2160,12 +2186,18 @@ int launch_wgrad(bool split, const void* A, const void* B, const int32_t* offset
   const size_t lds = 2 * kStageBytes;
   const uint16_t* a = static_cast<const uint16_t*>(A);
   const uint16_t* b = static_cast<const uint16_t*>(B);
-  if (split)
-    hipLaunchKernelGGL((grouped_gemm_wgrad<true>), dim3(grid), dim3(kThreads), lds, s, a, b,
-                       offsets, n_experts, M, N, out0, out1);
-  else
-    hipLaunchKernelGGL((grouped_gemm_wgrad<false>), dim3(grid), dim3(kThreads), lds, s, a, b,
-                       offsets, n_experts, M, N, out0, out1);
+  // A segment holds at most rows_cap rows and a tile reads up to 127 rows past
+  // it (its padding steps); below 2 GiB for that the per-tile resources hold.
+  const int64_t max_row_bytes = 2 * static_cast<int64_t>(M > N ? M : N);
+  const bool big = (rows_cap + 128) * max_row_bytes >= (int64_t(1) << 31);
+#define HMOE_LAUNCH_WGRAD(SP, BG)                                                               \
+  hipLaunchKernelGGL((grouped_gemm_wgrad<SP, BG>), dim3(grid), dim3(kThreads), lds, s, a, b,     \
+                     offsets, n_experts, M, N, out0, out1)
+  if (split && big) HMOE_LAUNCH_WGRAD(true, true);
+  else if (split) HMOE_LAUNCH_WGRAD(true, false);
+  else if (big) HMOE_LAUNCH_WGRAD(false, true);
+  else HMOE_LAUNCH_WGRAD(false, false);
+#undef HMOE_LAUNCH_WGRAD
   return check_launch(what);
 }
 }  // namespace
@@ -2184,8 +2216,8 @@ extern "C" int hmoe_grouped_wgrad_down(const void* h, const void* d_ys, const in
   HMOE_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31),
                "grouped_wgrad_down: rows_cap must fit in int32");
   HMOE_REQUIRE(h && d_ys && offsets && dw_down, "grouped_wgrad_down: null pointer argument");
-  return launch_wgrad(false, h, d_ys, offsets, n_experts, d_ff, d_model, dw_down, nullptr,
-                      static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_down");
+  return launch_wgrad(false, h, d_ys, offsets, n_experts, rows_cap, d_ff, d_model, dw_down,
+                      nullptr, static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_down");
 }
 
 extern "C" int hmoe_grouped_wgrad_gate_up(const void* xs, const void* dgu, const int32_t* offsets,
@@ -2203,6 +2235,6 @@ extern "C" int hmoe_grouped_wgrad_gate_up(const void* xs, const void* dgu, const
                "grouped_wgrad_gate_up: rows_cap must fit in int32");
   HMOE_REQUIRE(xs && dgu && offsets && dw_gate && dw_up,
                "grouped_wgrad_gate_up: null pointer argument");
-  return launch_wgrad(true, xs, dgu, offsets, n_experts, d_model, 2 * d_ff, dw_gate, dw_up,
-                      static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_gate_up");
+  return launch_wgrad(true, xs, dgu, offsets, n_experts, rows_cap, d_model, 2 * d_ff, dw_gate,
+                      dw_up, static_cast<hipStream_t>(stream), "hmoe_grouped_wgrad_gate_up");
 }

@@ -72,12 +72,15 @@ class DeviceLayer:
                            and self.x.dtype == torch.bfloat16)
         ws = int(_lib.lib().hmoe_plan_workspace_bytes(wl.tokens, wl.top_k, wl.n_experts))
         self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
-        # The gathered gate/up GEMM and the down GEMM in one persistent launch
-        # (hmoe_grouped_swiglu_fused) where its shape rules hold; fused_ffn=False
-        # keeps the two launches.
+        # fused_ffn=True: the gathered gate/up GEMM and the down GEMM in one
+        # persistent launch (hmoe_grouped_swiglu_fused) where its shape rules
+        # hold.  Off by default: measured end to end it is within noise of the
+        # two launches at the full bf16 workload and ~2 % slower at the skewed
+        # one (the per-XCD split of whole m-tiles leaves up to one m-tile of
+        # imbalance, about what the two launches' tails cost).
         can_fuse = (self.fused_dispatch and wl.d_model % 256 == 0 and wl.d_ff % 128 == 0
                     and wl.d_ff >= 256)
-        self.fused_ffn = can_fuse if fused_ffn is None else (bool(fused_ffn) and can_fuse)
+        self.fused_ffn = bool(fused_ffn) and can_fuse
         self.fused_ws = None
         if self.fused_ffn:
             rc = K.rows_cap(wl.tokens, wl.top_k, wl.n_experts, self.capacity)

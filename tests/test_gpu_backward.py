@@ -662,3 +662,38 @@ def test_wgrad_gemms_past_2gib(gpu):
             err = O.normwise_rel_err(host(got), ref)
             print(f"  expert {e} rows {a}-{b} {name}: {err:.2e}", flush=True)
             assert err < 1e-5, (name, e, err)
+
+
+def test_wgrad_gate_up_segment_past_2gib(gpu):
+    """One expert whose own segment is larger than 2 GiB (530000 rows of
+    d_model 2048 bf16: the buffer resources are then rebased at every K
+    step), beside a small one; dWg and dWu against float64, summed over
+    65536-row chunks on the host."""
+    D, F = 2048, 128
+    sizes = np.array([530_000, 100])
+    offsets = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(offsets[-1])
+    assert int(sizes[0]) * D * 2 > 2 ** 31
+    print(f"wgrad gate/up segment past 2 GiB: rows {sizes.tolist()}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(4)
+    xs = torch.randn(R, D, generator=g, device=gpu).to(torch.bfloat16)
+    dgu = torch.randn(R, 2 * F, generator=g, device=gpu).to(torch.bfloat16)
+    dwg, dwu = K.grouped_wgrad_gate_up(xs, dgu, torch.from_numpy(offsets).to(gpu))
+    torch.cuda.synchronize()
+    col = np.arange(F)
+    gc = (col // 32) * 64 + col % 32
+    for e in range(2):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        ref_g = np.zeros((D, F))
+        ref_u = np.zeros((D, F))
+        for c in range(a, b, 65536):
+            d = min(b, c + 65536)
+            x64 = host(xs[c:d]).astype(np.float64)
+            g64 = host(dgu[c:d]).astype(np.float64)
+            ref_g += x64.T @ g64[:, gc]
+            ref_u += x64.T @ g64[:, gc + 32]
+        for name, got, ref in (("dWg", dwg[e], ref_g), ("dWu", dwu[e], ref_u)):
+            err = O.normwise_rel_err(host(got), ref)
+            print(f"  expert {e} rows {b - a} {name}: {err:.2e}", flush=True)
+            # float32 accumulation over 8282 K steps: ~4e-7 x sqrt(530000 / 4500)
+            assert err < 3e-5, (name, e, err)

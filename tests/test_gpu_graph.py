@@ -40,12 +40,19 @@ def assert_same(got, want, what):
                            v.view(torch.uint8) if v.dtype.is_floating_point else v), (what, k)
 
 
-@pytest.mark.parametrize("name,tokens", [("full_bf16", 2048), ("fp8_experts", 1024),
-                                         ("dispatch_identity", 4096), ("skewed_bf16", 4096)])
-def test_forward_graph_replays(gpu, name, tokens):
+@pytest.mark.parametrize("name,tokens,fused_ffn", [("full_bf16", 2048, False),
+                                                   ("fp8_experts", 1024, False),
+                                                   ("dispatch_identity", 4096, False),
+                                                   ("skewed_bf16", 4096, False),
+                                                   # the one-launch gate/up + down: its
+                                                   # counters clear themselves, no memset
+                                                   ("full_bf16", 2048, True),
+                                                   ("skewed_bf16", 4096, True)])
+def test_forward_graph_replays(gpu, name, tokens, fused_ffn):
     wl = W.WORKLOADS[name].scaled(tokens)
-    print(f"graph {name} T={wl.tokens}", flush=True)
-    layer = DeviceLayer(W.make_inputs(wl, seed=0), gpu)
+    print(f"graph {name} T={wl.tokens} fused_ffn={fused_ffn}", flush=True)
+    layer = DeviceLayer(W.make_inputs(wl, seed=0), gpu, fused_ffn=fused_ffn)
+    assert layer.fused_ffn == fused_ffn
     src = layer.logits_in if wl.router_from_logits else layer.x
     other = W.make_inputs(wl, seed=1)
     src_b = torch.from_numpy(other.logits if wl.router_from_logits else other.x)
