@@ -81,9 +81,6 @@ def algorithmic(wl, kept_rows: int) -> dict:
     w["quant_x"] = ("hbm", T * D * x_in + T * D + T * 4, HBM_PEAK_GBS)
     if wl.expert == "swiglu":
         w["gate_up"] = ("mfma", 2 * 2 * kept_rows * D * F, mfma_peak)
-        if fp8:
-            # h (bf16) read once, codes and row scales written
-            w["quant_h"] = ("hbm", kept_rows * F * 2 + kept_rows * F + kept_rows * 4, HBM_PEAK_GBS)
         w["down"] = ("mfma", 2 * kept_rows * F * D, mfma_peak)
         # gate/up and down in one persistent launch (--fused-ffn)
         w["ffn"] = ("mfma", 6 * kept_rows * D * F, mfma_peak)
@@ -242,7 +239,7 @@ def main():
     fp8_gather = layer.fp8_gather
     stages = ["router", "plan"] + (["quant_x"] if fp8_gather else [] if fused else ["permute"])
     if wl.expert == "swiglu":
-        stages += (["gate_up", "quant_h", "down"] if fp8 else
+        stages += (["gate_up", "down"] if fp8 else
                    ["ffn"] if layer.fused_ffn else ["gate_up", "down"])
     stages += ["combine"]
 
@@ -263,21 +260,18 @@ def main():
         if fp8 and fp8_gather:
             x_q, x_s = K.quantize_rows_fp8(layer.x)
             mark()
-            h = K.grouped_gate_up_fp8_gather(x_q, x_s, plan, layer.w_gate_up,
-                                             layer.w_gate_up_scale)
+            h_q, h_e = K.grouped_gate_up_fp8_gather_qh(x_q, x_s, plan, layer.w_gate_up,
+                                                       layer.w_gate_up_scale)
             mark()
-            h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
-            mark()
-            ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, layer.w_down, layer.w_down_scale)
+            ys = K.grouped_down_fp8_mx(h_q, h_e, plan.offsets, layer.w_down, layer.w_down_scale)
             mark()
         elif fp8:
             xs_q, xs_s = K.permute_rows_fp8(layer.x, plan)
             mark()
-            h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, layer.w_gate_up, layer.w_gate_up_scale)
+            h_q, h_e = K.grouped_gate_up_fp8_qh(xs_q, xs_s, plan.offsets, layer.w_gate_up,
+                                                layer.w_gate_up_scale)
             mark()
-            h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
-            mark()
-            ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, layer.w_down, layer.w_down_scale)
+            ys = K.grouped_down_fp8_mx(h_q, h_e, plan.offsets, layer.w_down, layer.w_down_scale)
             mark()
         elif layer.fused_ffn:
             h, ys, _ = K.grouped_swiglu_fused(layer.x, plan, layer.w_gate_up, layer.w_down,

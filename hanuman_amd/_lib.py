@@ -66,6 +66,12 @@ SIGNATURES = {
     "hmoe_grouped_gate_up_fp8_gather": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i64, _i32,
                                                _i32, _vp, _vp, _vp, _vp]),
     "hmoe_grouped_down_fp8": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "hmoe_grouped_gate_up_fp8_qh": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp,
+                                           _vp, _vp]),
+    "hmoe_grouped_gate_up_fp8_gather_qh": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i64,
+                                                  _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "hmoe_grouped_down_fp8_mx": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp,
+                                        _vp]),
     "hmoe_aux_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "hmoe_router_aux": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "hmoe_combine_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _f32, _vp]),

@@ -399,6 +399,7 @@ constexpr int kW8StepBytes = 64;
 constexpr int kW8Stages = 4;
 constexpr int kW8StageBytes = 2 * kBM * kW8StepBytes;  // A 16 KB | B 16 KB
 constexpr int kW8Lds = kW8Stages * kW8StageBytes;       // 128 KB
+constexpr int kW8MxLds = kW8Lds + 2 * 2048;              // + exponents of A
 static_assert(kW8Lds <= 2 * kStageBytes, "allow_dynamic_lds grants 2 * kStageBytes");
 
 // 64-byte LDS rows: chunk c of row r sits at c ^ swz64(r), so the 16 lanes
@@ -414,13 +415,20 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
 }
 
-template <bool SWIGLU, bool GATHER>
+template <bool SWIGLU, bool GATHER, bool MX = false>
 __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
     const float* __restrict__ a_scale, const float* __restrict__ b_scale,
     const int32_t* __restrict__ offsets, int n_experts, int64_t a_rows, int kdim, int ncols,
     uint16_t* __restrict__ C, int64_t ldc, int n_tiles_n, const int32_t* __restrict__ gather_src,
-    int gather_k, int gather_rows) {
+    int gather_k, int gather_rows, uint8_t* __restrict__ mx_exp) {
+  // MX with SWIGLU: h leaves as block-scaled e4m3 (codes into C, ldc bytes a
+  // row; biased exponents into mx_exp, ldc / 32 bytes a row).  MX without
+  // SWIGLU: A is block-scaled (a_scale unused; A's exponents in mx_exp,
+  // kdim / 32 bytes a row) and the MFMA applies them.
+  constexpr bool kQuantH = MX && SWIGLU;
+  constexpr bool kScaledA = MX && !SWIGLU;
+  static_assert(!(kScaledA && GATHER), "the block-scaled A operand is not gathered");
   typedef GemmElem<true> E;
   typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -459,6 +467,9 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, tile_bytes, kBufferWord3);
   const uint32_t b_voff0 = static_cast<uint32_t>(dma_row * row_bytes + dma_byte);
   uint32_t a_voff[2];
+  const int ex_row_bytes = kdim / 32;  // kScaledA: exponent bytes per row of A
+  __amdgpu_buffer_rsrc_t e_rsrc = b_rsrc;
+  uint32_t e_voff = 0;
   int ld_kb = 0, ld_g = 0, ld_t = first;
   int32_t pf_src[2];  // GATHER: sources of this lane's rows in the next tile
   auto fetch_src = [&](int t) __attribute__((always_inline)) {
@@ -505,6 +516,13 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
         rr = rr < lim ? rr : static_cast<int>(lim);
         a_voff[j] = static_cast<uint32_t>(rr * row_bytes + dma_byte);
       }
+      if (kScaledA) {
+        e_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            mx_exp + static_cast<int64_t>(r0) * ex_row_bytes, 0, kBM * ex_row_bytes, kBufferWord3);
+        int rr = wave * 32 + (lane & 31);
+        rr = rr < lim ? rr : static_cast<int>(lim);
+        e_voff = static_cast<uint32_t>(rr * ex_row_bytes);
+      }
     }
   };
   auto issue_dma = [&](int stage, int j) __attribute__((always_inline)) {
@@ -514,6 +532,16 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kBM * kW8StepBytes), 16,
                                              b_voff0 + static_cast<uint32_t>(16 * j * row_bytes),
                                              koff, 0, 0);
+  };
+  // kScaledA: A's exponents for two K steps (4 bytes of a row: blocks
+  // 2 kb .. 2 kb + 3) go into one of two 2 KB LDS regions past the stages,
+  // by one 4-byte DMA per wave issued with the data of an even step: wave w
+  // lane L fills bytes 4 L of the wave's 256 (row 32 w + L % 32 of the tile;
+  // lanes 32..63 repeat lanes 0..31 into bytes 128..255, which nothing reads).
+  // Issued before that step's data DMA, it is covered by the same waits.
+  auto issue_exp_dma = [&]() __attribute__((always_inline)) {
+    uint8_t* base = smem + kW8Lds + ((ld_g >> 1) & 1) * 2048 + wave * 256;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(e_rsrc, (lds_ptr_t)base, 4, e_voff, ld_kb * 2, 0, 0);
   };
   // Once every step is loaded the load side repeats the last one (into a
   // stage nothing reads), so every step issues the same DMA count.
@@ -530,16 +558,24 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
 
   // ---- MFMA fragments ------------------------------------------------------
   // Wave w: rows 128 (w & 1) .. +128, columns 64 (w >> 1) .. +64 of the tile.
-  // Lane L: row L & 31 of each 32-row fragment, bytes 32 (L / 32) .. + 32 of
-  // the step (chunks 2 (L / 32) and 2 (L / 32) + 1).
+  // Lane L: row L & 31 of each 32-row fragment; VGPRs 0..3 hold 16-byte
+  // chunk L / 32 of the step and VGPRs 4..7 chunk 2 + L / 32.  The MFMA takes
+  // VGPR half v of lane group g as K values 32 v + 16 g .. + 16 (measured:
+  // with per-block operand scales only this assignment reproduces exact
+  // float64 sums), so its 32-value scale block v is bytes 32 v .. + 32 of the
+  // step, and lane L's operand scale is that of block L / 32.
   const int wm = wave & 1, wn = wave >> 1;
   const int frow = lane & 31;
   const int fhalf = lane >> 5;
   const int fsw = swz64(frow);
-  const int p0 = ((2 * fhalf) ^ fsw) * 16, p1 = ((2 * fhalf + 1) ^ fsw) * 16;
+  const int p0 = (fhalf ^ fsw) * 16, p1 = ((2 + fhalf) ^ fsw) * 16;
   const int fa_off = (wm * 128 + frow) * kW8StepBytes;
   const int fb_off = kBM * kW8StepBytes + (wn * 64 + frow) * kW8StepBytes;
   E::frag_t fa[2][4], fb[2][2];
+  // kScaledA: fragment i's exponent word (blocks 2 kb .. 2 kb + 3 of row
+  // 128 wm + 32 i + L % 32), shifted right by 8 (L / 32) so that byte 0 is
+  // the lane's block of the even step and byte 2 that of the odd step.
+  uint32_t ex_cur[4], ex_nxt[4];
   auto read_frag = [&](const uint8_t* row) __attribute__((always_inline)) {
     const u32x4 lo4 = *reinterpret_cast<const u32x4*>(row + p0);
     const u32x4 hi4 = *reinterpret_cast<const u32x4*>(row + p1);
@@ -551,13 +587,19 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     }
     return f;
   };
-  auto read_frags = [&](auto Bc, int stage) __attribute__((always_inline)) {
+  auto read_frags = [&](auto Bc, int stage, int s) __attribute__((always_inline)) {
     constexpr int b = decltype(Bc)::value;
     const uint8_t* base = smem + stage * kW8StageBytes;
 #pragma unroll
     for (int i = 0; i < 4; ++i) fa[b][i] = read_frag(base + fa_off + i * 32 * kW8StepBytes);
 #pragma unroll
     for (int j = 0; j < 2; ++j) fb[b][j] = read_frag(base + fb_off + j * 32 * kW8StepBytes);
+    if (kScaledA && b == 0) {
+      const uint8_t* ex = smem + kW8Lds + ((s >> 1) & 1) * 2048 + wm * 1024 + frow * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ex_nxt[i] = *reinterpret_cast<const uint32_t*>(ex + i * 256) >> (8 * fhalf);
+    }
   };
   f32x16 acc[4][2];
 
@@ -565,21 +607,37 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   // g + 1 into buffer B ^ 1, the MFMAs of step g, one barrier.
   auto step = [&](auto Bc, int g, auto Wc) __attribute__((always_inline)) {
     constexpr int b = decltype(Bc)::value;
+    // odd g: the load side is at an even step (or, done, repeats an odd one)
+    if (kScaledA && b == 1 && (ld_kb & 1) == 0) issue_exp_dma();
 #pragma unroll
     for (int j = 0; j < 2; ++j) issue_dma((g + 3) & 3, j);
     advance();
-    read_frags(IntC<b ^ 1>{}, (g + 1) & 3);
+    read_frags(IntC<b ^ 1>{}, (g + 1) & 3, g + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = E::mfma(fb[b][j], fa[b][i], acc[i][j]);
+      for (int j = 0; j < 2; ++j) {
+        if (kScaledA)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              fb[b][j], fa[b][i], acc[i][j], 0, 0, 0, 127, 2 * b, static_cast<int>(ex_cur[i]));
+        else
+          acc[i][j] = E::mfma(fb[b][j], fa[b][i], acc[i][j]);
+      }
+    // The accumulators are used here, before the step's barrier: otherwise
+    // the compiler sinks this step's MFMAs into the next step (past the
+    // barrier), and every other step leaves the matrix cores idle.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) asm volatile("" ::"v"(acc[i][j]));
     // per MFMA: a DMA or fragment reads
+    constexpr int kReads = (kScaledA && b == 1) ? 4 : 3;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // DMA
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // LDS read
     }
     __builtin_amdgcn_sched_barrier(0);
     // this wave's DMA of step g + 2 landed (step g + 3's four may still fly);
@@ -593,13 +651,14 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   set_load_tile(first);
 #pragma unroll
   for (int st = 0; st < 3; ++st) {
+    if (kScaledA && (ld_kb & 1) == 0) issue_exp_dma();
 #pragma unroll
     for (int j = 0; j < 2; ++j) issue_dma(st, j);
     advance();
   }
   wait_vm_lgkm0<4>();
   __builtin_amdgcn_s_barrier();
-  read_frags(IntC<0>{}, 0);
+  read_frags(IntC<0>{}, 0, 0);
 
   // GATHER: the source of tile row tid (tid < 256) of the current tile,
   // loaded one tile ahead so that the scale lookup never waits on it
@@ -620,7 +679,9 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     // this thread's row scale (tid < 256) or column scale (tid >= 256) of the
     // tile, loaded now and staged in LDS after the K loop
     float my_scale;
-    if (tid < kBM) {
+    if (kScaledA && tid < kBM) {
+      my_scale = 1.0f;  // the row scales are in the MFMA's block exponents
+    } else if (tid < kBM) {
       if (GATHER) {
         int tk = my_src >= 0 ? my_src / gather_k : 0;
         tk = tk < gather_rows ? tk : gather_rows - 1;
@@ -639,6 +700,10 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     for (int kb = 0; kb < ks; kb += 2, g += 2) {
+      if (kScaledA) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ex_cur[i] = ex_nxt[i];
+      }
       step(IntC<0>{}, g, IntC<4>{});
       step(IntC<1>{}, g + 1, IntC<4>{});
     }
@@ -654,8 +719,14 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     // of its row: two 16-byte stores per block, each writing 32 contiguous
     // bytes of every row.
     const int64_t nrows = row_end - row0 < kBM ? row_end - row0 : kBM;
+    constexpr int kOutBytes = kQuantH ? 1 : 2;
     const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        C + row0 * ldc, 0, static_cast<int>(nrows * ldc * 2), kBufferWord3);
+        reinterpret_cast<uint8_t*>(C) + row0 * ldc * kOutBytes, 0,
+        static_cast<int>(nrows * ldc * kOutBytes), kBufferWord3);
+    __amdgpu_buffer_rsrc_t e_out = c_rsrc;
+    if (kQuantH)
+      e_out = __builtin_amdgcn_make_buffer_rsrc(mx_exp + row0 * (ldc / 32), 0,
+                                                static_cast<int>(nrows * (ldc / 32)), kBufferWord3);
     auto store_block = [&](uint32_t (&d)[8], int r, int col) __attribute__((always_inline)) {
 #pragma unroll
       for (int w = 0; w < 2; ++w) {
@@ -676,7 +747,56 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     for (int i = 0; i < 4; ++i) {
       const int r = wm * 128 + i * 32 + frow;
       const float sa = sscale[r];
-      if (SWIGLU) {
+      if (kQuantH) {
+        // h of this row's 32 columns n0 / 2 + 32 wn .. + 32 (one scale block):
+        // lane L holds columns 8 q + 4 (L / 32) + k.  Block maximum over
+        // lanes L and L + 32, exponent e = the smallest with max <= 448 * 2^e
+        // (at least -127), codes e4m3(h * 2^-e), an exact scaling.
+        float hv[16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 sg = *reinterpret_cast<const f32x4*>(sscale + kBM + wn * 64 + q * 8 + fhalf * 4);
+          const f32x4 su =
+              *reinterpret_cast<const f32x4*>(sscale + kBM + wn * 64 + 32 + q * 8 + fhalf * 4);
+#pragma unroll
+          for (int k = 0; k < 4; k += 2) {
+            const uint32_t pk = pack_bf16x2_rne(
+                swiglu_bf16_points(acc[i][0][q * 4 + k] * sa * sg[k], acc[i][1][q * 4 + k] * sa * su[k]),
+                swiglu_bf16_points(acc[i][0][q * 4 + k + 1] * sa * sg[k + 1],
+                                   acc[i][1][q * 4 + k + 1] * sa * su[k + 1]));
+            hv[q * 4 + k] = __uint_as_float(pk << 16);
+            hv[q * 4 + k + 1] = __uint_as_float(pk & 0xffff0000u);
+            amax = fmaxf(amax, fmaxf(fabsf(hv[q * 4 + k]), fabsf(hv[q * 4 + k + 1])));
+          }
+        }
+        const uint32_t abits = __float_as_uint(amax);
+        const auto pa = __builtin_amdgcn_permlane32_swap(abits, abits, false, false);
+        const uint32_t bmax = __float_as_uint(fmaxf(__uint_as_float(pa[0]), __uint_as_float(pa[1])));
+        int ex = static_cast<int>(bmax >> 23) - 135 + ((bmax & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+        ex = ex > -127 ? ex : -127;
+        const float inv = __uint_as_float(static_cast<uint32_t>(127 - ex) << 23);
+        uint32_t d[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = fminf(fmaxf(hv[q * 4 + k] * inv, -448.0f), 448.0f);
+          const int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+          d[q] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], w, true));
+        }
+        // lanes L < 32 take columns 0..15 (their groups 0, 2 and the partner's),
+        // lanes L + 32 columns 16..31: one 16-byte store each
+        const auto p02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+        const auto p13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+        const u32x4 codes = {p02[0], p02[1], p13[0], p13[1]};
+        const int col = n0 / 2 + wn * 32;
+        __builtin_amdgcn_raw_buffer_store_b128(codes, c_rsrc, static_cast<int>(r * ldc + col + 16 * fhalf),
+                                               0, 0);
+        if (fhalf == 0)
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(ex + 127), e_out,
+                                               static_cast<int>(r * (ldc / 32) + col / 32), 0, 0);
+      } else if (SWIGLU) {
         // gate columns in acc[i][0], the up columns of the same h columns in acc[i][1]
         uint32_t d[8];
 #pragma unroll
@@ -1724,10 +1844,15 @@ int allow_dynamic_lds(int dev) {
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, false>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, true>),
       reinterpret_cast<const void*>(grouped_gemm_w8_fp8<false, false>),
+      reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, false, true>),
+      reinterpret_cast<const void*>(grouped_gemm_w8_fp8<true, true, true>),
       reinterpret_cast<const void*>(grouped_swiglu_fused),
   };
   bool ok = true;
   for (const void* k : kernels) ok = ok && set_lds_limit(k, bytes);
+  // the block-scaled down GEMM: two 2 KB exponent regions past the stages
+  ok = ok && set_lds_limit(reinterpret_cast<const void*>(grouped_gemm_w8_fp8<false, false, true>),
+                           kW8MxLds);
   if (!ok) {
     set_error("grouped GEMM: cannot allow %d bytes of dynamic LDS on device %d", bytes, dev);
     return HMOE_ERR_HIP;
@@ -1740,8 +1865,9 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
                    const float* b_scale, const int32_t* offsets, int n_experts, int64_t rows_cap,
                    int kdim, int ncols, void* C, int64_t ldc, hipStream_t s, const char* what,
                    const int32_t* gather_src = nullptr, int gather_k = 1, int gather_rows = 1,
-                   const uint16_t* dswiglu_dh = nullptr) {
+                   const uint16_t* dswiglu_dh = nullptr, uint8_t* mx_exp = nullptr) {
   const int n_tiles_n = ncols / kBN;
+  HMOE_REQUIRE(mx_exp == nullptr || fp8, "%s: block exponents belong to the e4m3 GEMM", what);
   HMOE_REQUIRE(dswiglu_dh == nullptr || (!swiglu && !fp8), "%s: SwiGLU VJP epilogue needs the raw bf16 GEMM", what);
   const int64_t max_tiles = (ceil_div(rows_cap, kBM) + n_experts) * n_tiles_n;
   HMOE_REQUIRE(max_tiles < (int64_t(1) << 31), "%s: too many tiles", what);
@@ -1763,14 +1889,18 @@ int launch_grouped(bool swiglu, bool fp8, const void* A, const void* B, const fl
                  "%s: reduction dimension must be a multiple of %d", what, 2 * kW8StepBytes);
     HMOE_REQUIRE(static_cast<int64_t>(gather_rows) * kdim < (int64_t(1) << 31),
                  "%s: gathered matrix too large", what);
-#define HMOE_LAUNCH_W8(SW, GA)                                                                    \
-  hipLaunchKernelGGL((grouped_gemm_w8_fp8<SW, GA>), dim3(grid), dim3(kW8Threads), kW8Lds, s, a,  \
+#define HMOE_LAUNCH_W8(SW, GA, MX, LDS)                                                           \
+  hipLaunchKernelGGL((grouped_gemm_w8_fp8<SW, GA, MX>), dim3(grid), dim3(kW8Threads), LDS, s, a, \
                      b, a_scale, b_scale, offsets, n_experts, rows_cap, kdim, ncols, c, ldc,        \
-                     n_tiles_n, gather_src, gather_k, gather_rows)
+                     n_tiles_n, gather_src, gather_k, gather_rows, mx_exp)
     HMOE_REQUIRE(swiglu || gather_src == nullptr, "%s: the fp8 down GEMM does not gather", what);
-    if (swiglu && gather_src != nullptr) HMOE_LAUNCH_W8(true, true);
-    else if (swiglu) HMOE_LAUNCH_W8(true, false);
-    else HMOE_LAUNCH_W8(false, false);
+    if (mx_exp != nullptr) {
+      if (swiglu && gather_src != nullptr) HMOE_LAUNCH_W8(true, true, true, kW8Lds);
+      else if (swiglu) HMOE_LAUNCH_W8(true, false, true, kW8Lds);
+      else HMOE_LAUNCH_W8(false, false, true, kW8MxLds);
+    } else if (swiglu && gather_src != nullptr) HMOE_LAUNCH_W8(true, true, false, kW8Lds);
+    else if (swiglu) HMOE_LAUNCH_W8(true, false, false, kW8Lds);
+    else HMOE_LAUNCH_W8(false, false, false, kW8Lds);
 #undef HMOE_LAUNCH_W8
   } else {
 #define HMOE_LAUNCH_REGS(SW, OD, GA, ...)                                                         \
@@ -2099,24 +2229,68 @@ extern "C" int hmoe_grouped_dgrad_gate_up(const void* dgu, const int32_t* offset
                         static_cast<hipStream_t>(stream), "hmoe_grouped_dgrad_gate_up");
 }
 
+namespace hmoe {
+namespace {
+
+// The e4m3 gate/up GEMM, plain (perm_src null: A holds the dispatched rows)
+// or gathering (A holds per-token rows, row r is token perm_src[r] / top_k),
+// with bf16 h (h_exp null) or block-scaled e4m3 h (codes into h, exponents
+// into h_exp).
+int gate_up_fp8(const char* what, const uint8_t* x_q, const float* x_scale, int64_t tokens,
+                int top_k, const int32_t* perm_src, const int32_t* offsets, int n_experts,
+                int64_t rows_cap, int d_model, int d_ff, const uint8_t* w_packed,
+                const float* w_scales, void* h, uint8_t* h_exp, hipStream_t stream) {
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "%s: n_experts must be in [1, %d] (got %d)", what, kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "%s: rows_cap must be >= 0", what);
+  if (perm_src != nullptr || tokens >= 0)
+    HMOE_REQUIRE(tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
+                 "%s: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)", what);
+  HMOE_REQUIRE_CODE(d_model % 128 == 0 && d_model >= 128, HMOE_ERR_UNSUPPORTED,
+                    "%s: d_model must be a multiple of 128 (got %d)", what, d_model);
+  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
+                    "%s: d_ff must be a multiple of %d (got %d)", what, kBN / 2, d_ff);
+  if (tokens >= 0)
+    HMOE_REQUIRE(tokens * d_model < (int64_t(1) << 31), "%s: x_q must be smaller than 2 GiB", what);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(x_q && x_scale && offsets && w_packed && w_scales && h, "%s: null pointer argument",
+               what);
+  HMOE_REQUIRE(tokens < 0 || perm_src != nullptr, "%s: null pointer argument", what);
+  return launch_grouped(true, true, x_q, w_packed, x_scale, w_scales, offsets, n_experts, rows_cap,
+                        d_model, 2 * d_ff, h, d_ff, stream, what, perm_src, top_k,
+                        tokens >= 0 ? static_cast<int>(tokens) : 1, nullptr, h_exp);
+}
+
+// The e4m3 down GEMM on h with one float32 scale per row (h_scale) or one
+// power-of-two scale per 32 columns (h_exp, biased exponents).
+int down_fp8(const char* what, const uint8_t* h_q, const float* h_scale, const uint8_t* h_exp,
+             const int32_t* offsets, int n_experts, int64_t rows_cap, int d_ff, int d_model,
+             const uint8_t* w_packed, const float* w_scales, void* ys, hipStream_t stream) {
+  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
+               "%s: n_experts must be in [1, %d] (got %d)", what, kMaxExperts, n_experts);
+  HMOE_REQUIRE(rows_cap >= 0, "%s: rows_cap must be >= 0", what);
+  HMOE_REQUIRE_CODE(d_ff % 128 == 0 && d_ff >= 128, HMOE_ERR_UNSUPPORTED,
+                    "%s: d_ff must be a multiple of 128 (got %d)", what, d_ff);
+  HMOE_REQUIRE_CODE(d_model % kBN == 0 && d_model > 0, HMOE_ERR_UNSUPPORTED,
+                    "%s: d_model must be a multiple of %d (got %d)", what, kBN, d_model);
+  if (rows_cap == 0) return HMOE_OK;
+  HMOE_REQUIRE(h_q && (h_scale || h_exp) && offsets && w_packed && w_scales && ys,
+               "%s: null pointer argument", what);
+  return launch_grouped(false, true, h_q, w_packed, h_scale, w_scales, offsets, n_experts, rows_cap,
+                        d_ff, d_model, ys, d_model, stream, what, nullptr, 1, 1, nullptr,
+                        const_cast<uint8_t*>(h_exp));
+}
+
+}  // namespace
+}  // namespace hmoe
+
 extern "C" int hmoe_grouped_gate_up_fp8(const uint8_t* xs_q, const float* xs_scale,
                                         const int32_t* offsets, int n_experts, int64_t rows_cap,
                                         int d_model, int d_ff, const uint8_t* w_packed,
                                         const float* w_scales, void* h, hmoe_stream_t stream) {
-  using namespace hmoe;
-  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
-               "grouped_gate_up_fp8: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
-  HMOE_REQUIRE(rows_cap >= 0, "grouped_gate_up_fp8: rows_cap must be >= 0");
-  HMOE_REQUIRE_CODE(d_model % 128 == 0 && d_model >= 128, HMOE_ERR_UNSUPPORTED,
-                    "grouped_gate_up_fp8: d_model must be a multiple of 128 (got %d)", d_model);
-  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
-                    "grouped_gate_up_fp8: d_ff must be a multiple of %d (got %d)", kBN / 2, d_ff);
-  if (rows_cap == 0) return HMOE_OK;
-  HMOE_REQUIRE(xs_q && xs_scale && offsets && w_packed && w_scales && h,
-               "grouped_gate_up_fp8: null pointer argument");
-  return launch_grouped(true, true, xs_q, w_packed, xs_scale, w_scales, offsets, n_experts,
-                        rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
-                        "hmoe_grouped_gate_up_fp8");
+  return hmoe::gate_up_fp8("grouped_gate_up_fp8", xs_q, xs_scale, -1, 1, nullptr, offsets,
+                           n_experts, rows_cap, d_model, d_ff, w_packed, w_scales, h, nullptr,
+                           static_cast<hipStream_t>(stream));
 }
 
 extern "C" int hmoe_grouped_gate_up_fp8_gather(const uint8_t* x_q, const float* x_scale,
@@ -2125,47 +2299,68 @@ extern "C" int hmoe_grouped_gate_up_fp8_gather(const uint8_t* x_q, const float* 
                                                int64_t rows_cap, int d_model, int d_ff,
                                                const uint8_t* w_packed, const float* w_scales,
                                                void* h, hmoe_stream_t stream) {
-  using namespace hmoe;
-  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
-               "grouped_gate_up_fp8_gather: n_experts must be in [1, %d] (got %d)", kMaxExperts,
-               n_experts);
-  HMOE_REQUIRE(rows_cap >= 0 && tokens >= 0 && top_k >= 1 && (tokens >= 1 || rows_cap == 0),
-               "grouped_gate_up_fp8_gather: need rows_cap >= 0, tokens >= 0, top_k >= 1 (tokens >= 1 with rows)");
-  HMOE_REQUIRE_CODE(d_model % 128 == 0 && d_model >= 128, HMOE_ERR_UNSUPPORTED,
-                    "grouped_gate_up_fp8_gather: d_model must be a multiple of 128 (got %d)",
-                    d_model);
-  HMOE_REQUIRE_CODE((2 * d_ff) % kBN == 0 && d_ff > 0, HMOE_ERR_UNSUPPORTED,
-                    "grouped_gate_up_fp8_gather: d_ff must be a multiple of %d (got %d)", kBN / 2,
-                    d_ff);
-  HMOE_REQUIRE(tokens * d_model < (int64_t(1) << 31),
-               "grouped_gate_up_fp8_gather: x_q must be smaller than 2 GiB");
-  if (rows_cap == 0) return HMOE_OK;
-  HMOE_REQUIRE(x_q && x_scale && perm_src && offsets && w_packed && w_scales && h,
-               "grouped_gate_up_fp8_gather: null pointer argument");
-  return launch_grouped(true, true, x_q, w_packed, x_scale, w_scales, offsets, n_experts,
-                        rows_cap, d_model, 2 * d_ff, h, d_ff, static_cast<hipStream_t>(stream),
-                        "hmoe_grouped_gate_up_fp8_gather", perm_src, top_k,
-                        static_cast<int>(tokens));
+  if (tokens < 0) {
+    hmoe::set_error("grouped_gate_up_fp8_gather: tokens must be >= 0 (got %lld)",
+                    static_cast<long long>(tokens));
+    return HMOE_ERR_INVALID;
+  }
+  return hmoe::gate_up_fp8("grouped_gate_up_fp8_gather", x_q, x_scale, tokens, top_k, perm_src,
+                           offsets, n_experts, rows_cap, d_model, d_ff, w_packed, w_scales, h,
+                           nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hmoe_grouped_gate_up_fp8_qh(const uint8_t* xs_q, const float* xs_scale,
+                                           const int32_t* offsets, int n_experts, int64_t rows_cap,
+                                           int d_model, int d_ff, const uint8_t* w_packed,
+                                           const float* w_scales, uint8_t* h_q, uint8_t* h_exp,
+                                           hmoe_stream_t stream) {
+  if (rows_cap > 0 && h_exp == nullptr) {
+    hmoe::set_error("grouped_gate_up_fp8_qh: null pointer argument");
+    return HMOE_ERR_INVALID;
+  }
+  return hmoe::gate_up_fp8("grouped_gate_up_fp8_qh", xs_q, xs_scale, -1, 1, nullptr, offsets,
+                           n_experts, rows_cap, d_model, d_ff, w_packed, w_scales, h_q, h_exp,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hmoe_grouped_gate_up_fp8_gather_qh(const uint8_t* x_q, const float* x_scale,
+                                                  int64_t tokens, int top_k,
+                                                  const int32_t* perm_src, const int32_t* offsets,
+                                                  int n_experts, int64_t rows_cap, int d_model,
+                                                  int d_ff, const uint8_t* w_packed,
+                                                  const float* w_scales, uint8_t* h_q,
+                                                  uint8_t* h_exp, hmoe_stream_t stream) {
+  if (tokens < 0 || (rows_cap > 0 && h_exp == nullptr)) {
+    hmoe::set_error("grouped_gate_up_fp8_gather_qh: need tokens >= 0 and a non-null h_exp");
+    return HMOE_ERR_INVALID;
+  }
+  return hmoe::gate_up_fp8("grouped_gate_up_fp8_gather_qh", x_q, x_scale, tokens, top_k, perm_src,
+                           offsets, n_experts, rows_cap, d_model, d_ff, w_packed, w_scales, h_q,
+                           h_exp, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale,
                                      const int32_t* offsets, int n_experts, int64_t rows_cap,
                                      int d_ff, int d_model, const uint8_t* w_packed,
                                      const float* w_scales, void* ys, hmoe_stream_t stream) {
-  using namespace hmoe;
-  HMOE_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts,
-               "grouped_down_fp8: n_experts must be in [1, %d] (got %d)", kMaxExperts, n_experts);
-  HMOE_REQUIRE(rows_cap >= 0, "grouped_down_fp8: rows_cap must be >= 0");
-  HMOE_REQUIRE_CODE(d_ff % 128 == 0 && d_ff >= 128, HMOE_ERR_UNSUPPORTED,
-                    "grouped_down_fp8: d_ff must be a multiple of 128 (got %d)", d_ff);
-  HMOE_REQUIRE_CODE(d_model % kBN == 0 && d_model > 0, HMOE_ERR_UNSUPPORTED,
-                    "grouped_down_fp8: d_model must be a multiple of %d (got %d)", kBN, d_model);
-  if (rows_cap == 0) return HMOE_OK;
-  HMOE_REQUIRE(h_q && h_scale && offsets && w_packed && w_scales && ys,
-               "grouped_down_fp8: null pointer argument");
-  return launch_grouped(false, true, h_q, w_packed, h_scale, w_scales, offsets, n_experts,
-                        rows_cap, d_ff, d_model, ys, d_model, static_cast<hipStream_t>(stream),
-                        "hmoe_grouped_down_fp8");
+  if (rows_cap > 0 && h_scale == nullptr) {
+    hmoe::set_error("grouped_down_fp8: null pointer argument");
+    return HMOE_ERR_INVALID;
+  }
+  return hmoe::down_fp8("grouped_down_fp8", h_q, h_scale, nullptr, offsets, n_experts, rows_cap,
+                        d_ff, d_model, w_packed, w_scales, ys, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hmoe_grouped_down_fp8_mx(const uint8_t* h_q, const uint8_t* h_exp,
+                                        const int32_t* offsets, int n_experts, int64_t rows_cap,
+                                        int d_ff, int d_model, const uint8_t* w_packed,
+                                        const float* w_scales, void* ys, hmoe_stream_t stream) {
+  if (rows_cap > 0 && h_exp == nullptr) {
+    hmoe::set_error("grouped_down_fp8_mx: null pointer argument");
+    return HMOE_ERR_INVALID;
+  }
+  return hmoe::down_fp8("grouped_down_fp8_mx", h_q, nullptr, h_exp, offsets, n_experts, rows_cap,
+                        d_ff, d_model, w_packed, w_scales, ys, static_cast<hipStream_t>(stream));
 }
 
 // ---- backward weight gradients (the VJP of moe.py:70-73 w.r.t. the weights) --

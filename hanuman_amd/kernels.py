@@ -533,6 +533,68 @@ def grouped_down_fp8(h_q: torch.Tensor, h_scale: torch.Tensor, offsets: torch.Te
     return ys
 
 
+def grouped_gate_up_fp8_qh(xs_q: torch.Tensor, xs_scale: torch.Tensor, offsets: torch.Tensor,
+                           w_packed: torch.Tensor, w_scales: torch.Tensor):
+    """Block-scaled e4m3 ``h`` of the fp8 gate/up GEMM, quantised in its
+    epilogue: codes ``[rows, F]`` (uint8) and biased exponents ``[rows, F/32]``
+    (uint8, ``e + 127``; every 32 columns of a row share ``2**e``)."""
+    for t, n in ((xs_q, "xs_q"), (xs_scale, "xs_scale"), (offsets, "offsets"),
+                 (w_packed, "w_packed"), (w_scales, "w_scales")):
+        _check(t, n)
+    N, F2, D = w_packed.shape
+    if (xs_q.dtype != torch.uint8 or w_packed.dtype != torch.uint8 or xs_q.shape[1] != D
+            or xs_scale.numel() != xs_q.shape[0] or tuple(w_scales.shape) != (N, F2)
+            or offsets.numel() != N + 1 or offsets.dtype != torch.int32):
+        raise ValueError("grouped_gate_up_fp8_qh: inconsistent shapes or dtypes")
+    R, F = xs_q.shape[0], F2 // 2
+    h_q = torch.empty((R, F), dtype=torch.uint8, device=xs_q.device)
+    h_exp = torch.empty((R, F // 32), dtype=torch.uint8, device=xs_q.device)
+    call("hmoe_grouped_gate_up_fp8_qh", _ptr(xs_q), _ptr(xs_scale), _ptr(offsets), N, R, D, F,
+         _ptr(w_packed), _ptr(w_scales), _ptr(h_q), _ptr(h_exp), _stream())
+    return h_q, h_exp
+
+
+def grouped_gate_up_fp8_gather_qh(x_q: torch.Tensor, x_scale: torch.Tensor, plan: Plan,
+                                  w_packed: torch.Tensor, w_scales: torch.Tensor):
+    """:func:`grouped_gate_up_fp8_qh` gathering its rows from the per-token
+    codes of ``x`` through ``perm_src`` (as :func:`grouped_gate_up_fp8_gather`)."""
+    for t, n in ((x_q, "x_q"), (x_scale, "x_scale"), (w_packed, "w_packed"),
+                 (w_scales, "w_scales")):
+        _check(t, n)
+    N, F2, D = w_packed.shape
+    T = x_q.shape[0]
+    if (x_q.dtype != torch.uint8 or w_packed.dtype != torch.uint8 or x_q.shape[1] != D
+            or x_scale.numel() != T or tuple(w_scales.shape) != (N, F2)
+            or plan.n_experts != N or plan.slot_pos.numel() != T * plan.top_k):
+        raise ValueError("grouped_gate_up_fp8_gather_qh: inconsistent shapes or dtypes")
+    F = F2 // 2
+    h_q = torch.empty((plan.rows_cap, F), dtype=torch.uint8, device=x_q.device)
+    h_exp = torch.empty((plan.rows_cap, F // 32), dtype=torch.uint8, device=x_q.device)
+    call("hmoe_grouped_gate_up_fp8_gather_qh", _ptr(x_q), _ptr(x_scale), T, plan.top_k,
+         _ptr(plan.perm_src), _ptr(plan.offsets), N, plan.rows_cap, D, F, _ptr(w_packed),
+         _ptr(w_scales), _ptr(h_q), _ptr(h_exp), _stream())
+    return h_q, h_exp
+
+
+def grouped_down_fp8_mx(h_q: torch.Tensor, h_exp: torch.Tensor, offsets: torch.Tensor,
+                        w_packed: torch.Tensor, w_scales: torch.Tensor) -> torch.Tensor:
+    """bf16 ``ys`` of the fp8 down GEMM on block-scaled ``h`` (the MFMA applies
+    ``h_exp``; the accumulators are dequantised by the column scales)."""
+    for t, n in ((h_q, "h_q"), (h_exp, "h_exp"), (offsets, "offsets"), (w_packed, "w_packed"),
+                 (w_scales, "w_scales")):
+        _check(t, n)
+    N, D, F = w_packed.shape
+    if (h_q.dtype != torch.uint8 or h_exp.dtype != torch.uint8 or w_packed.dtype != torch.uint8
+            or h_q.shape[1] != F or tuple(h_exp.shape) != (h_q.shape[0], F // 32)
+            or tuple(w_scales.shape) != (N, D) or offsets.numel() != N + 1
+            or offsets.dtype != torch.int32):
+        raise ValueError("grouped_down_fp8_mx: inconsistent shapes or dtypes")
+    ys = torch.empty((h_q.shape[0], D), dtype=torch.bfloat16, device=h_q.device)
+    call("hmoe_grouped_down_fp8_mx", _ptr(h_q), _ptr(h_exp), _ptr(offsets), N, h_q.shape[0], F, D,
+         _ptr(w_packed), _ptr(w_scales), _ptr(ys), _stream())
+    return ys
+
+
 # ---------------------------------------------------------------- combine --
 
 def combine(ys: torch.Tensor, plan: Plan, gates: torch.Tensor,

@@ -97,21 +97,22 @@ class DeviceLayer:
         return K.router(self.x, self.router_w, None, wl.top_k, self.mode)
 
     def experts_fp8(self, plan):
-        """e4m3 dispatch and expert GEMMs: (xs_q, xs_scale, h, h_q, h_scale, ys).
+        """e4m3 dispatch and expert GEMMs: (xs_q, xs_scale, h_q, h_exp, ys).
         With bf16 tokens x is quantised per token and the gate/up GEMM gathers
         its rows from the codes (``xs_q``/``xs_scale`` are then per token,
-        ``[T, D]``/``[T]``); otherwise they are the dispatched rows."""
+        ``[T, D]``/``[T]``); otherwise they are the dispatched rows.  h leaves
+        the gate/up GEMM block-scaled (codes ``h_q``, biased exponents
+        ``h_exp`` per 32 columns) and the down GEMM's MFMA applies them."""
         if self.fp8_gather:
             xs_q, xs_s = K.quantize_rows_fp8(self.x)
-            h = K.grouped_gate_up_fp8_gather(xs_q, xs_s, plan, self.w_gate_up,
-                                             self.w_gate_up_scale)
+            h_q, h_e = K.grouped_gate_up_fp8_gather_qh(xs_q, xs_s, plan, self.w_gate_up,
+                                                       self.w_gate_up_scale)
         else:
             xs_q, xs_s = K.permute_rows_fp8(self.x, plan)
-            h = K.grouped_gate_up_fp8(xs_q, xs_s, plan.offsets, self.w_gate_up,
-                                      self.w_gate_up_scale)
-        h_q, h_s = K.quantize_rows_fp8(h, plan.offsets)
-        ys = K.grouped_down_fp8(h_q, h_s, plan.offsets, self.w_down, self.w_down_scale)
-        return xs_q, xs_s, h, h_q, h_s, ys
+            h_q, h_e = K.grouped_gate_up_fp8_qh(xs_q, xs_s, plan.offsets, self.w_gate_up,
+                                                self.w_gate_up_scale)
+        ys = K.grouped_down_fp8_mx(h_q, h_e, plan.offsets, self.w_down, self.w_down_scale)
+        return xs_q, xs_s, h_q, h_e, ys
 
     def forward(self) -> dict:
         wl = self.wl
@@ -120,8 +121,8 @@ class DeviceLayer:
         extra = {}
         h = None
         if self.fp8:
-            xs, xs_s, h, h_q, h_s, ys = self.experts_fp8(plan)
-            extra = {"xs_scale": xs_s, "h_q": h_q, "h_scale": h_s,
+            xs, xs_s, h_q, h_e, ys = self.experts_fp8(plan)
+            extra = {"xs_scale": xs_s, "h_q": h_q, "h_exp": h_e,
                      "xs_per_token": self.fp8_gather}
         elif self.f32:
             xs = K.permute_rows(self.x, plan, torch.float32)

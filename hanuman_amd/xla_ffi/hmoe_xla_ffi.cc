@@ -397,6 +397,75 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedDownFp8, GroupedDownFp8Impl,
                                   .Arg<ffi::Buffer<ffi::F32>>()
                                   .Ret<ffi::Buffer<ffi::BF16>>());
 
+// Block-scaled h: the gate/up GEMMs return codes [rows, F] and biased
+// exponents [rows, F / 32]; the down GEMM takes both.
+static ffi::Error GroupedGateUpFp8QhImpl(hipStream_t stream, ffi::Buffer<ffi::U8> xs_q,
+                                         ffi::Buffer<ffi::F32> xs_scale,
+                                         ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+                                         ffi::Buffer<ffi::F32> w_scales,
+                                         ffi::ResultBuffer<ffi::U8> h_q,
+                                         ffi::ResultBuffer<ffi::U8> h_exp) {
+  return Status(hmoe_grouped_gate_up_fp8_qh(
+      xs_q.typed_data(), xs_scale.typed_data(), offsets.typed_data(),
+      static_cast<int>(offsets.element_count() - 1), Rows(xs_q), static_cast<int>(Cols(xs_q)),
+      static_cast<int>(Cols(*h_q)), w.typed_data(), w_scales.typed_data(), h_q->typed_data(),
+      h_exp->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpFp8Qh, GroupedGateUpFp8QhImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>());
+
+static ffi::Error GroupedGateUpFp8GatherQhImpl(
+    hipStream_t stream, ffi::Buffer<ffi::U8> x_q, ffi::Buffer<ffi::F32> x_scale,
+    ffi::Buffer<ffi::S32> perm_src, ffi::Buffer<ffi::S32> offsets, ffi::Buffer<ffi::U8> w,
+    ffi::Buffer<ffi::F32> w_scales, int64_t top_k, ffi::ResultBuffer<ffi::U8> h_q,
+    ffi::ResultBuffer<ffi::U8> h_exp) {
+  return Status(hmoe_grouped_gate_up_fp8_gather_qh(
+      x_q.typed_data(), x_scale.typed_data(), Rows(x_q), static_cast<int>(top_k),
+      perm_src.typed_data(), offsets.typed_data(), static_cast<int>(offsets.element_count() - 1),
+      Rows(*h_q), static_cast<int>(Cols(x_q)), static_cast<int>(Cols(*h_q)), w.typed_data(),
+      w_scales.typed_data(), h_q->typed_data(), h_exp->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedGateUpFp8GatherQh, GroupedGateUpFp8GatherQhImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Attr<int64_t>("top_k")
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>());
+
+static ffi::Error GroupedDownFp8MxImpl(hipStream_t stream, ffi::Buffer<ffi::U8> h_q,
+                                       ffi::Buffer<ffi::U8> h_exp, ffi::Buffer<ffi::S32> offsets,
+                                       ffi::Buffer<ffi::U8> w, ffi::Buffer<ffi::F32> w_scales,
+                                       ffi::ResultBuffer<ffi::BF16> ys) {
+  return Status(hmoe_grouped_down_fp8_mx(
+      h_q.typed_data(), h_exp.typed_data(), offsets.typed_data(),
+      static_cast<int>(offsets.element_count() - 1), Rows(h_q), static_cast<int>(Cols(h_q)),
+      static_cast<int>(Cols(*ys)), w.typed_data(), w_scales.typed_data(), ys->untyped_data(),
+      S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeGroupedDownFp8Mx, GroupedDownFp8MxImpl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::S32>>()
+                                  .Arg<ffi::Buffer<ffi::U8>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::BF16>>());
+
 // float32 compute dtype: masters as they are.
 static ffi::Error GroupedGateUpF32Impl(hipStream_t stream, ffi::Buffer<ffi::F32> xs,
                                        ffi::Buffer<ffi::S32> offsets,

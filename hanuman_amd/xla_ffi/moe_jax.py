@@ -68,6 +68,9 @@ TARGETS = {
     "hmoe_grouped_gate_up_fp8": "HmoeGroupedGateUpFp8",
     "hmoe_grouped_gate_up_fp8_gather": "HmoeGroupedGateUpFp8Gather",
     "hmoe_grouped_down_fp8": "HmoeGroupedDownFp8",
+    "hmoe_grouped_gate_up_fp8_qh": "HmoeGroupedGateUpFp8Qh",
+    "hmoe_grouped_gate_up_fp8_gather_qh": "HmoeGroupedGateUpFp8GatherQh",
+    "hmoe_grouped_down_fp8_mx": "HmoeGroupedDownFp8Mx",
     "hmoe_grouped_gate_up_f32": "HmoeGroupedGateUpF32",
     "hmoe_grouped_down_f32": "HmoeGroupedDownF32",
     "hmoe_combine": "HmoeCombine",

@@ -261,6 +261,33 @@ int hmoe_grouped_down_fp8(const uint8_t* h_q, const float* h_scale, const int32_
                           int n_experts, int64_t rows_cap, int d_ff, int d_model,
                           const uint8_t* w_packed, const float* w_scales, void* ys,
                           hmoe_stream_t stream);
+/* Block-scaled h (the fp8 workload's rule for the down GEMM's operand, the
+ * re-quantisation the reference's bf16 path has no counterpart of; it
+ * replaces hmoe_quantize_rows_fp8 of h between the two GEMMs of
+ * moe.py:70-72).  The gate/up GEMM's epilogue computes h as the _fp8 entries
+ * do (bf16-rounded), then every 32 consecutive h columns of a row share a
+ * power-of-two scale 2^e, e the smallest integer with max|h| <= 448 * 2^e
+ * over the block (at least -127), and the codes are e4m3(h * 2^-e) rounded
+ * to nearest even: h_q [rows_cap, F] uint8 and h_exp [rows_cap, F / 32]
+ * uint8 biased exponents e + 127 (E8M0).  Rows past offsets[N] are not
+ * written.  The down GEMM feeds h_exp to the MFMA's per-32-value operand
+ * scales and dequantises the accumulators by the column scales only.
+ * Shape rules as for the _fp8 entries. */
+int hmoe_grouped_gate_up_fp8_qh(const uint8_t* xs_q, const float* xs_scale,
+                                const int32_t* offsets, int n_experts, int64_t rows_cap,
+                                int d_model, int d_ff, const uint8_t* w_packed,
+                                const float* w_scales, uint8_t* h_q, uint8_t* h_exp,
+                                hmoe_stream_t stream);
+int hmoe_grouped_gate_up_fp8_gather_qh(const uint8_t* x_q, const float* x_scale, int64_t tokens,
+                                       int top_k, const int32_t* perm_src,
+                                       const int32_t* offsets, int n_experts, int64_t rows_cap,
+                                       int d_model, int d_ff, const uint8_t* w_packed,
+                                       const float* w_scales, uint8_t* h_q, uint8_t* h_exp,
+                                       hmoe_stream_t stream);
+int hmoe_grouped_down_fp8_mx(const uint8_t* h_q, const uint8_t* h_exp, const int32_t* offsets,
+                             int n_experts, int64_t rows_cap, int d_ff, int d_model,
+                             const uint8_t* w_packed, const float* w_scales, void* ys,
+                             hmoe_stream_t stream);
 
 /* Float32 compute dtype (moe.py:70-74 with dtype = float32): the grouped
  * GEMMs on the float32 matrix cores with the masters as they are.

@@ -47,6 +47,7 @@ __all__ = [
     "capacity_of", "rows_cap_of", "dispatch_plan", "dispatch_plan_bruteforce",
     "permute_rows", "silu", "expert_ffn", "combine", "combine_identity", "aux_losses",
     "shared_expert", "moe_forward", "quantize_rows_e4m3", "quantize_cols_e4m3",
+    "block_exponent_e8m0", "quantize_blocks_e4m3", "dequantize_blocks_e4m3",
     "expert_ffn_fp8", "quantize_expert_weights", "dequantized_weights", "normwise_rel_err",
 ]
 
@@ -446,17 +447,66 @@ def quantize_cols_e4m3(w):
     return q, s
 
 
-def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s):
+E4M3_BLOCK = 32          # columns per power-of-two scale block of h
+
+
+def block_exponent_e8m0(amax) -> np.ndarray:
+    """Smallest integer ``e`` with ``amax <= 448 * 2**e``, at least -127 (the
+    bottom of the E8M0 scale range; an all-zero block gets -127).
+
+    From the float32 fields of ``amax = 1.m * 2**(E-127)``: ``amax * 2**-e =
+    1.m * 2**(8-c)`` for ``e = E - 135 + c``, which is at most 448 exactly when
+    ``c = 0`` and ``1.m <= 1.75`` (mantissa field <= 0x600000), else ``c = 1``
+    (``1.m * 2**7 < 256``); one less than that ``e`` exceeds 448 either way.
+    Returns int64."""
+    bits = np.asarray(amax, dtype=F32).view(np.uint32).astype(np.int64)
+    E = (bits >> 23) & 0xFF
+    e = E - 135 + ((bits & 0x7FFFFF) > 0x600000)
+    return np.maximum(e, -127)
+
+
+def quantize_blocks_e4m3(a, block: int = E4M3_BLOCK):
+    """Block-scaled e4m3 (the fp8 workload's rule for ``h``): every ``block``
+    consecutive columns of a row share a power-of-two scale ``2**e``,
+    ``e = block_exponent_e8m0(max |a| over the block)``, and the codes are
+    ``e4m3(a * 2**-e)`` (an exact scaling, then round-to-nearest-even; the
+    scaled magnitudes are at most 448 by the choice of ``e``, so nothing
+    saturates).  Returns (codes uint8 [..., C], biased exponents uint8
+    [..., C/block] = ``e + 127``, the E8M0 encoding of ``2**e``)."""
+    a = np.asarray(a, dtype=F32)
+    C = a.shape[-1]
+    if C % block:
+        raise ValueError(f"{C} columns are not a whole number of {block}-column blocks")
+    blk = a.reshape(a.shape[:-1] + (C // block, block))
+    e = block_exponent_e8m0(np.max(np.abs(blk), axis=-1))
+    scaled = (blk.astype(F64) * np.ldexp(1.0, -e)[..., None]).astype(F32)
+    return e4m3_encode(scaled).reshape(a.shape), (e + 127).astype(np.uint8)
+
+
+def dequantize_blocks_e4m3(q, e8, block: int = E4M3_BLOCK) -> np.ndarray:
+    """float64 values of block-scaled codes: ``decode(q) * 2**(e8 - 127)``."""
+    scale = np.ldexp(1.0, np.asarray(e8, np.int64) - 127)
+    return e4m3_decode(q).astype(F64) * np.repeat(scale, block, axis=-1)
+
+
+def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s, h_rule: str = "block32"):
     """Grouped SwiGLU on e4m3 operands (the fp8 workload's expert rule).
 
     ``xs_q [R, D]`` codes with per-row scales ``xs_s``; ``wg_q/wu_q [N, D, F]``
     codes with per-column scales ``[N, F]``; ``wd_q [N, F, D]`` with ``[N, D]``.
     ``g = bf16((x.wg) * sx * sg)``, ``u`` likewise (rounded to bf16 as the
     bf16 path's ``ragged_dot`` outputs are, ``moe.py:70-71``),
-    ``h = bf16(silu(g) * u)``; h is
-    re-quantised per row (:func:`quantize_rows_e4m3`) and
-    ``ys = bf16((hq.wd) * sh * sd)``.  Dot products of decoded codes in
-    float64.  Returns (ys float32 of bf16 values, h, hq, hs)."""
+    ``h = bf16(silu(g) * u)``.  h is re-quantised for the down GEMM by
+    ``h_rule``: ``"block32"`` (the workload's rule,
+    :func:`quantize_blocks_e4m3`: a power-of-two scale per 32 columns, which
+    the gate/up GEMM applies in its epilogue and the down GEMM's scaled MFMA
+    consumes) or ``"row"`` (:func:`quantize_rows_e4m3`, one float32 scale per
+    row; the per-row kernels' rule).  ``ys = bf16((deq(hq).wd) * sd)``.  Dot
+    products of decoded codes in float64.  Returns (ys float32 of bf16 values,
+    h, hq, h_scale) with ``h_scale`` the biased exponents ``[R, F/32]``
+    (uint8) or the row scales ``[R]`` (float32)."""
+    if h_rule not in ("block32", "row"):
+        raise ValueError(h_rule)
     offsets = np.asarray(offsets, dtype=np.int64)
     N = len(offsets) - 1
     R = xs_q.shape[0]
@@ -475,15 +525,20 @@ def expert_ffn_fp8(xs_q, xs_s, offsets, wg_q, wg_s, wu_q, wu_s, wd_q, wd_s):
         h[a:b] = bf16_round((silu(g) * u).astype(F32))
     total = int(offsets[-1])
     hq = np.zeros((R, F), np.uint8)
-    hs = np.ones(R, F32)
-    hq[:total], hs[:total] = quantize_rows_e4m3(h[:total])
+    if h_rule == "block32":
+        hs = np.full((R, F // E4M3_BLOCK), 127, np.uint8)
+        hq[:total], hs[:total] = quantize_blocks_e4m3(h[:total])
+        hh_all = dequantize_blocks_e4m3(hq, hs)
+    else:
+        hs = np.ones(R, F32)
+        hq[:total], hs[:total] = quantize_rows_e4m3(h[:total])
+        hh_all = e4m3_decode(hq).astype(F64) * hs.astype(F64)[:, None]
     ys = np.zeros((R, D), F32)
     for e in range(N):
         a, b = int(offsets[e]), int(offsets[e + 1])
         if b <= a:
             continue
-        hh = e4m3_decode(hq[a:b]).astype(F64) * hs[a:b].astype(F64)[:, None]
-        y = (hh @ e4m3_decode(wd_q[e]).astype(F64)) * np.asarray(wd_s[e], F64)[None, :]
+        y = (hh_all[a:b] @ e4m3_decode(wd_q[e]).astype(F64)) * np.asarray(wd_s[e], F64)[None, :]
         ys[a:b] = bf16_round(y.astype(F32))
     return ys, h, hq, hs
 
@@ -641,7 +696,8 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
                 routed_scaling_factor: float = 2.5, capacity_factor=None,
                 expert: str = "swiglu", n_shared: int = 0, dtype: str = "bf16",
                 precision: str = "fp32", logits=None, fast_router: bool = False,
-                batch_shape=None, out_dtype: str = "f32", x_dtype: str | None = None) -> dict:
+                batch_shape=None, out_dtype: str = "f32", x_dtype: str | None = None,
+                fp8_h_rule: str = "block32") -> dict:
     """Whole-layer forward (``MoE.__call__``, ``moe.py:170-294``).
 
     ``x`` [T,D] float32 values (bf16-representable when ``dtype="bf16"``).
@@ -651,7 +707,8 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
     ``logits``: precomputed router logits (identity-expert workload).
     ``expert``: ``"swiglu"``, ``"identity"`` or ``"swiglu_fp8"`` (e4m3 operands,
     :func:`expert_ffn_fp8`; quantised weights from ``params["fp8"]`` or
-    :func:`quantize_expert_weights`).  ``out_dtype="bf16"`` rounds the output.
+    :func:`quantize_expert_weights`; ``fp8_h_rule`` picks how ``h`` is
+    re-quantised, see there).  ``out_dtype="bf16"`` rounds the output.
     ``x_dtype``: the dtype ``x`` arrives in (``"bf16"`` or ``"f32"``; default
     the compute ``dtype``, as ``model/transformer.py`` passes it).  The
     routed path casts ``x`` to the compute dtype (``moe.py:198``); the shared
@@ -692,7 +749,8 @@ def moe_forward(x, params: dict, *, top_k: int, routing: str = "sigmoid",
         xs_s[valid] = xsc[perm[valid] // K]
         wq = params["fp8"] if "fp8" in params else quantize_expert_weights(params)
         ys, h, hq, hs = expert_ffn_fp8(xs_q, xs_s, plan["offsets"], wq["wg_q"], wq["wg_s"],
-                                       wq["wu_q"], wq["wu_s"], wq["wd_q"], wq["wd_s"])
+                                       wq["wu_q"], wq["wu_s"], wq["wd_q"], wq["wd_s"],
+                                       h_rule=fp8_h_rule)
         xs = xs_q
         extra = {"x_q": xq, "x_s": xsc, "xs_s": xs_s, "h": h, "hq": hq, "hs": hs, "fp8": wq}
     elif expert == "identity":

@@ -54,7 +54,10 @@ def test_zero_tokens_is_a_no_op(gpu):
     h_q, h_s = K.quantize_rows_fp8(h8, plan.offsets)
     ys8 = K.grouped_down_fp8(h_q, h_s, plan.offsets, fd, sd)
     out8 = K.combine(ys8, plan, gates, None, torch.bfloat16)
+    hb_q, hb_e = K.grouped_gate_up_fp8_gather_qh(x_q, x_s, plan, fgu, sgu)
+    ysb = K.grouped_down_fp8_mx(hb_q, hb_e, plan.offsets, fd, sd)
     torch.cuda.synchronize()
+    assert hb_q.shape[0] == 0 and hb_e.shape[0] == 0 and ysb.shape[0] == 0
     assert tuple(logits.shape) == (0, N) and tuple(idx.shape) == (0, Kk)
     assert plan.rows_cap == 0
     assert host(plan.counts).tolist() == [0] * N and host(plan.offsets).tolist() == [0] * (N + 1)

@@ -125,9 +125,8 @@ def test_random_fp8_layer_matches_oracle(gpu, i):
     fgu, sgu = K.pack_fp8_gate_up(dev(wg), dev(wu))
     fd, sd = K.pack_fp8_down(dev(wd))
     x_q, x_s = K.quantize_rows_fp8(xt)
-    h8 = K.grouped_gate_up_fp8_gather(x_q, x_s, plan, fgu, sgu)
-    h_q, h_s = K.quantize_rows_fp8(h8, plan.offsets)
-    ys8 = K.grouped_down_fp8(h_q, h_s, plan.offsets, fd, sd)
+    h_q, h_e = K.grouped_gate_up_fp8_gather_qh(x_q, x_s, plan, fgu, sgu)
+    ys8 = K.grouped_down_fp8_mx(h_q, h_e, plan.offsets, fd, sd)
     out = K.combine(ys8, plan, gates, None, torch.bfloat16)
     torch.cuda.synchronize()
 

@@ -500,6 +500,77 @@ def test_quantization_error_bound():
     assert np.all(err <= bound)
 
 
+def _min_exponent_bruteforce(amax):
+    """Smallest integer e >= -127 with amax <= 448 * 2**e, by search in float64
+    (exact: 448 * 2**e is a float64 for every e in range)."""
+    e = -127
+    if amax > 448.0 * 2.0 ** -127:
+        e = int(np.floor(np.log2(amax / 448.0))) - 2
+        while amax > np.ldexp(448.0, e):
+            e += 1
+    return e
+
+
+def test_block_exponent_is_minimal_power_of_two_cover():
+    """e is the smallest exponent whose 448 * 2**e covers the block maximum,
+    on the edges the field formula turns on: exactly 448 * 2**k, one float32
+    ulp either side, the 1.75 mantissa boundary, zero, subnormals, the
+    largest float32."""
+    rng = np.random.default_rng(90)
+    vals = [0.0, 1e-45, 1e-40, 2.0 ** -126, 448.0, 3.4e38, 1.0, 1.75, 1.7500001, 2.0]
+    for k in (-140, -130, -127, -20, -3, 0, 1, 9, 60, 118):
+        base = np.float32(np.ldexp(448.0, k)) if k > -150 else np.float32(0)
+        vals += [float(base), float(np.nextafter(base, np.float32(np.inf))),
+                 float(np.nextafter(base, np.float32(0)))]
+    vals += list(np.exp(rng.uniform(-95, 85, 4000)))
+    amax = np.array(vals, dtype=np.float32)
+    got = O.block_exponent_e8m0(amax)
+    want = np.array([_min_exponent_bruteforce(float(v)) for v in amax])
+    assert np.array_equal(got, want)
+    assert got.min() >= -127 and got.max() <= 127
+
+
+def test_quantize_blocks_e4m3_rule_against_torch_per_block():
+    """Codes are torch's float8_e4m3fn conversion of a * 2**-e block by block
+    (32 columns, e from the brute-force search), nothing saturates, every
+    nonzero block's largest code lies in (224, 448], and an all-zero block
+    gets exponent byte 0 and zero codes."""
+    rng = np.random.default_rng(91)
+    a = (rng.standard_normal((6, 256)) * np.exp(rng.uniform(-30, 30, (6, 8))).repeat(32, axis=1))
+    a = a.astype(np.float32)
+    a[2, 64:96] = 0.0
+    a[3, 0:32] = -0.0
+    a[4, 32:64] = 1e-40                        # subnormal block
+    a[5, 96:128] = np.float32(448.0 * 2.0 ** 5)  # exactly on a power-of-two cover
+    q, e8 = O.quantize_blocks_e4m3(a)
+    assert q.shape == a.shape and e8.shape == (6, 8) and e8.dtype == np.uint8
+    for r in range(a.shape[0]):
+        for j in range(8):
+            blk = a[r, 32 * j:32 * j + 32]
+            e = _min_exponent_bruteforce(float(np.abs(blk).max()))
+            assert e8[r, j] == e + 127
+            scaled = (blk.astype(np.float64) * 2.0 ** -e).astype(np.float32)
+            assert np.abs(scaled).max() <= 448.0
+            ref = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            assert np.array_equal(q[r, 32 * j:32 * j + 32], ref), (r, j)
+            top = np.abs(O.e4m3_decode(q[r, 32 * j:32 * j + 32])).max()
+            if np.abs(blk).max() > 448.0 * 2.0 ** -127:
+                assert 224.0 <= top <= 448.0, (r, j, top)
+    assert e8[2, 2] == 0 and not O.e4m3_decode(q[2, 64:96]).any()
+    assert e8[5, 3] == 5 + 127 and (q[5, 96:128] == 0x7E).all()
+
+
+def test_block_quantization_error_bound():
+    """Dequantised values are within 2^-4 relative (e4m3 normal range) or half
+    a subnormal step, 2^-10, times the block's power of two."""
+    rng = np.random.default_rng(92)
+    a = (rng.standard_normal((16, 512)) * np.exp(rng.uniform(-8, 8, (16, 1)))).astype(np.float32)
+    q, e8 = O.quantize_blocks_e4m3(a)
+    deq = O.dequantize_blocks_e4m3(q, e8)
+    scale = np.repeat(2.0 ** (e8.astype(np.int64) - 127), 32, axis=1)
+    assert np.all(np.abs(deq - a) <= np.maximum(np.abs(a) * 2.0 ** -4, scale * 2.0 ** -10))
+
+
 def _e4m3_grid_matrix(rng, shape, axis):
     """Values on the e4m3 grid whose maximum |v| along `axis` is exactly 448,
     so per-row/column quantisation is the identity with scale 1."""
@@ -524,8 +595,11 @@ def test_expert_ffn_fp8_reduces_to_library_matmul_on_exact_operands():
     assert np.array_equal(O.e4m3_decode(xq), x) and np.all(xs == 1.0)
     wq = O.quantize_expert_weights({"expert_w_gate": wg, "expert_w_up": wu, "expert_w_down": wd})
     assert all(np.all(wq[k] == 1.0) for k in ("wg_s", "wu_s", "wd_s"))
-    ys, h, hq, hs = O.expert_ffn_fp8(xq, xs, offsets, wq["wg_q"], wq["wg_s"], wq["wu_q"],
+    ys, h, hq, he = O.expert_ffn_fp8(xq, xs, offsets, wq["wg_q"], wq["wg_s"], wq["wu_q"],
                                      wq["wu_s"], wq["wd_q"], wq["wd_s"])
+    ys_r, h_r, hq_r, hs = O.expert_ffn_fp8(xq, xs, offsets, wq["wg_q"], wq["wg_s"], wq["wu_q"],
+                                           wq["wu_s"], wq["wd_q"], wq["wd_s"], h_rule="row")
+    assert np.array_equal(h_r, h) and he.shape == (R, F // 32) and hs.shape == (R,)
     for e in range(N):
         a, b = offsets[e], offsets[e + 1]
         if b == a:
@@ -536,9 +610,14 @@ def test_expert_ffn_fp8_reduces_to_library_matmul_on_exact_operands():
         g = O.bf16_round(g.astype(np.float32)).astype(np.float64)
         u = O.bf16_round(u.astype(np.float32)).astype(np.float64)
         assert np.array_equal(h[a:b], O.bf16_round((g / (1 + np.exp(-g)) * u).astype(np.float32)))
-        hh = O.e4m3_decode(hq[a:b]).astype(np.float64) * hs[a:b, None]
+        # block rule: each 32-column block of h times its power of two
+        scale = np.repeat(2.0 ** (he[a:b].astype(np.int64) - 127), 32, axis=1)
+        hh = O.e4m3_decode(hq[a:b]).astype(np.float64) * scale
         y = np.matmul(hh, wd[e].astype(np.float64))
         assert np.array_equal(ys[a:b], O.bf16_round(y.astype(np.float32)))
+        hh = O.e4m3_decode(hq_r[a:b]).astype(np.float64) * hs[a:b, None]
+        y = np.matmul(hh, wd[e].astype(np.float64))
+        assert np.array_equal(ys_r[a:b], O.bf16_round(y.astype(np.float32)))
 
 
 def test_fp8_layer_within_tolerance_of_fp32_on_dequantised_weights():
