@@ -135,6 +135,37 @@ __device__ __forceinline__ void decode_tile(int t, int n_tiles_n, const int32_t*
   n0 = n_tile * kBN;
 }
 
+// Tile order of the persistent grouped GEMMs: an expert's tiles are taken in
+// groups of kTileGroupM row tiles, each group swept column tile by column
+// tile (row tile fastest), so that the ~32 consecutive tiles one XCD's
+// workgroups hold at a time share kTileGroupM A row-blocks and 32 /
+// kTileGroupM B column-blocks instead of 2 row-blocks and every column
+// block: less traffic past the XCD's L2.  The set of tiles and their
+// results are those of decode_tile.
+constexpr int kTileGroupM = 4;
+
+__device__ __forceinline__ void decode_tile_grouped(int t, int n_tiles_n, const int32_t* tstart,
+                                                    const int32_t* __restrict__ offsets,
+                                                    int n_experts, int& e, int64_t& row0,
+                                                    int64_t& row_end, int& n0) {
+  const int m_any = t / n_tiles_n;  // some row tile of t's expert
+  int lo = 0, hi = n_experts;       // largest e with tstart[e] <= m_any (it has >= 1 tile)
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (tstart[mid] <= m_any) lo = mid; else hi = mid;
+  }
+  e = lo;
+  const int u = t - tstart[e] * n_tiles_n;  // tile within the expert
+  const int me = tstart[e + 1] - tstart[e];
+  const int g = u / (kTileGroupM * n_tiles_n);
+  const int gm = me - g * kTileGroupM < kTileGroupM ? me - g * kTileGroupM : kTileGroupM;
+  const int v = u - g * kTileGroupM * n_tiles_n;
+  const int n_tile = v / gm;
+  row0 = offsets[e] + static_cast<int64_t>(g * kTileGroupM + (v - n_tile * gm)) * kBM;
+  row_end = offsets[e + 1];
+  n0 = n_tile * kBN;
+}
+
 // Position of the 16-byte chunks of LDS row r: chunk c sits at c ^ lds_swz(r).
 // A fragment read has lanes 0..31 on 32 consecutive rows (128 bytes apart)
 // at the same chunk; the LDS serves 16 lanes of a 16-byte read per pass from
@@ -475,7 +506,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto fetch_src = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
     const int64_t lim = row_end - 1 - r0;
 #pragma unroll
@@ -488,7 +519,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
@@ -665,7 +696,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto row_src = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     return gather_src[row0 + tid < row_end ? row0 + tid : row_end - 1];
   };
   int32_t my_src = 0;
@@ -675,7 +706,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   for (int t = first; t < hi; t += per_xcd) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     // this thread's row scale (tid < 256) or column scale (tid >= 256) of the
     // tile, loaded now and staged in LDS after the K loop
     float my_scale;
@@ -903,7 +934,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   auto fetch_src = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
     // rows past the segment repeat its last row (its token row stays cached)
     const int64_t lim = row_end - 1 - r0;
@@ -917,7 +948,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
@@ -1085,7 +1116,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
 
     int e, n0;
     int64_t row0, row_end;
-    decode_tile(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     // stage 1 is idle here: the tile's last step (odd) read it, step 0 of the
     // next tile writes it only after the epilogue's last barrier
     if constexpr (DSWIGLU)
