@@ -412,7 +412,7 @@ def main():
         # Dominant kernel: the gate/up grouped GEMM with the fused SwiGLU
         # (register-staged bf16 kernel; direct-to-LDS kernel for e4m3).
         odd = (wl.d_model * (1 if fp8 else 2) // 128) % 2 == 1
-        kname = (f"grouped_gemm_w8_fp8<true, {'true' if fp8_gather else 'false'}>" if fp8
+        kname = (f"grouped_gemm_w8_fp8<true, {'true' if fp8_gather else 'false'}, true>" if fp8
                  else "grouped_gemm_f32_kernel<1, false>" if wl.expert_dtype == "f32"
                  else f"grouped_gemm_regs<true, {'true' if odd else 'false'}, "
                       f"{'true' if fused else 'false'}, false>")
