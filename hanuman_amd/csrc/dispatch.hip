@@ -120,12 +120,106 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(int32_t* __restrict__ h
   if (tid == 0) offsets[0] = 0;
 }
 
+// Column scan of the per-block histogram for plans past the fused rank pass,
+// one wave per expert over the whole chip (plan_scan_kernel's one workgroup
+// walked 128 blocks per lane at 512 blocks x 128 experts: 42 us).  Lane j
+// takes blocks [j L, (j + 1) L), L = ceil(nblk / 64), eight loads in flight;
+// the wave scans the 64 partial sums, each lane rewrites its blocks' counts
+// as exclusive bases, and lane 0 writes the expert's total to counts.  The
+// kept-row offsets are formed by every rank workgroup from counts.
+constexpr int kScanColWaves = 4;
+
+__global__ __launch_bounds__(64 * kScanColWaves) void plan_scan_cols_kernel(
+    int32_t* __restrict__ hist, int nblk, int n_experts, int32_t* __restrict__ counts) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * kScanColWaves + (threadIdx.x >> 6);
+  if (e >= n_experts) return;  // uniform per wave
+  const int L = (nblk + 63) / 64;
+  const int b0 = lane * L < nblk ? lane * L : nblk;
+  const int b1 = b0 + L < nblk ? b0 + L : nblk;
+  constexpr int kU = 8;
+  int32_t part = 0;
+  {
+    int b = b0;
+    for (; b + kU <= b1; b += kU) {
+      int32_t v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = hist[static_cast<int64_t>(b + u) * n_experts + e];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) part += v[u];
+    }
+    for (; b < b1; ++b) part += hist[static_cast<int64_t>(b) * n_experts + e];
+  }
+  int32_t incl = part;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  const int32_t total = __shfl(incl, 63, 64);
+  int32_t run = incl - part;  // exclusive base of block b0
+  int b = b0;
+  for (; b + kU <= b1; b += kU) {
+    int32_t v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = hist[static_cast<int64_t>(b + u) * n_experts + e];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      hist[static_cast<int64_t>(b + u) * n_experts + e] = run;
+      run += v[u];
+    }
+  }
+  for (; b < b1; ++b) {
+    const int64_t idx = static_cast<int64_t>(b) * n_experts + e;
+    const int32_t c = hist[idx];
+    hist[idx] = run;
+    run += c;
+  }
+  if (lane == 0) counts[e] = total;
+}
+
+// Kept-row offsets from the per-expert totals, in LDS: on entry s_off[e]
+// holds min(total, capacity) for e < n_experts; on exit the exclusive scan,
+// with the kept total in s_off[n_experts].  Each thread scans a run of kPer
+// consecutive experts, then a Hillis-Steele scan over the kPlanThreads run
+// sums (s_scan).  Ends with a barrier.
+__device__ void kept_offsets_lds(int32_t* s_off, int32_t* s_scan, int n_experts) {
+  const int tid = threadIdx.x;
+  constexpr int kPer = kMaxExperts / kPlanThreads;
+  int32_t local[kPer];
+  int32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid * kPer + j;
+    local[j] = e < n_experts ? s_off[e] : 0;
+    sum += local[j];
+  }
+  s_scan[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int32_t v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  int32_t run = s_scan[tid] - sum;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid * kPer + j;
+    if (e < n_experts) s_off[e] = run;
+    run += local[j];
+  }
+  if (tid == kPlanThreads - 1) s_off[n_experts] = s_scan[kPlanThreads - 1];
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(
     const int32_t* __restrict__ top_idx, int64_t rows, int n_experts, int64_t capacity,
-    const int32_t* __restrict__ bases, const int32_t* __restrict__ offsets,
-    int32_t* __restrict__ slot_pos, int32_t* __restrict__ perm_src, uint8_t* __restrict__ keep,
-    int64_t rows_cap) {
+    const int32_t* __restrict__ bases, const int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ slot_pos, int32_t* __restrict__ perm_src,
+    uint8_t* __restrict__ keep, int64_t rows_cap) {
   __shared__ int32_t whist[4][kMaxExperts];
+  __shared__ int32_t s_off[kMaxExperts + 1];  // kept-row offsets
+  __shared__ int32_t s_scan[kPlanThreads];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -150,8 +244,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(
       whist[w][e] = run;
       run += c;
     }
+    const int32_t tot = counts[e];
+    s_off[e] = static_cast<int32_t>(tot < capacity ? tot : capacity);
   }
   __syncthreads();
+  kept_offsets_lds(s_off, s_scan, n_experts);
+  if (blockIdx.x == 0)
+    for (int e = tid; e <= n_experts; e += kPlanThreads) offsets[e] = s_off[e];
 
   const int nbits = n_experts > 1 ? 32 - __builtin_clz(static_cast<unsigned>(n_experts - 1)) : 0;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -180,7 +279,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(
       const bool kept = rank < capacity;
       keep[s] = kept ? 1 : 0;
       if (kept) {
-        const int32_t pos = offsets[e] + rank;
+        const int32_t pos = s_off[e] + rank;
         slot_pos[s] = pos;
         perm_src[pos] = static_cast<int32_t>(s);
       } else {
@@ -189,7 +288,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_rank_kernel(
     }
   }
   // Rows past the kept total hold -1.
-  const int64_t total = offsets[n_experts];
+  const int64_t total = s_off[n_experts];
   for (int64_t j = total + static_cast<int64_t>(blockIdx.x) * kPlanThreads + tid; j < rows_cap;
        j += static_cast<int64_t>(gridDim.x) * kPlanThreads)
     perm_src[j] = -1;
@@ -292,36 +391,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_rank_fused_kernel(
     s_off[e] = static_cast<int32_t>(tot < capacity ? tot : capacity);
   }
   __syncthreads();
-  // Exclusive scan of the kept counts over the experts: each thread a run of
-  // kPer consecutive experts, a Hillis-Steele scan over the 256 run sums.
-  constexpr int kPer = kMaxExperts / kPlanThreads;
-  int32_t local[kPer];
-  int32_t sum = 0;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = tid * kPer + j;
-    local[j] = e < n_experts ? s_off[e] : 0;
-    sum += local[j];
-  }
-  s_scan[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const int32_t v = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
-  }
-  {
-    int32_t run = s_scan[tid] - sum;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = tid * kPer + j;
-      if (e < n_experts) s_off[e] = run;
-      run += local[j];
-    }
-    if (tid == kPlanThreads - 1) s_off[n_experts] = s_scan[kPlanThreads - 1];
-  }
-  __syncthreads();
+  kept_offsets_lds(s_off, s_scan, n_experts);
   if (b == 0)
     for (int e = tid; e <= n_experts; e += kPlanThreads) offsets[e] = s_off[e];
 
@@ -715,11 +785,12 @@ int launch_plan(const int32_t* top_idx, int64_t tokens, int top_k, int n_experts
     hipLaunchKernelGGL(plan_histogram_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
                        n_experts, hist);
     if (int rc = check_launch("dispatch_plan/histogram")) return rc;
-    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, hist, nblk, n_experts, capacity,
-                       counts, offsets);
+    hipLaunchKernelGGL(plan_scan_cols_kernel, dim3(ceil_div(n_experts, kScanColWaves)),
+                       dim3(64 * kScanColWaves), 0, s, hist, nblk, n_experts, counts);
     if (int rc = check_launch("dispatch_plan/scan")) return rc;
     hipLaunchKernelGGL(plan_rank_kernel, dim3(nblk), dim3(kPlanThreads), 0, s, top_idx, rows,
-                       n_experts, capacity, hist, offsets, slot_pos, perm_src, keep, rows_cap);
+                       n_experts, capacity, hist, counts, offsets, slot_pos, perm_src, keep,
+                       rows_cap);
     return check_launch("dispatch_plan/rank");
   }
   // No slots: zero counts and offsets.
