@@ -136,14 +136,18 @@ __device__ __forceinline__ void decode_tile(int t, int n_tiles_n, const int32_t*
 }
 
 // Tile order of the persistent grouped GEMMs: an expert's tiles are taken in
-// groups of kTileGroupM row tiles, each group swept column tile by column
-// tile (row tile fastest), so that the ~32 consecutive tiles one XCD's
-// workgroups hold at a time share kTileGroupM A row-blocks and 32 /
-// kTileGroupM B column-blocks instead of 2 row-blocks and every column
-// block: less traffic past the XCD's L2.  The set of tiles and their
-// results are those of decode_tile.
-constexpr int kTileGroupM = 4;
+// groups of G row tiles, each group swept column tile by column tile (row
+// tile fastest), so that the ~32 consecutive tiles one XCD's workgroups hold
+// at a time share G A row-blocks and 32 / G B column-blocks instead of 2
+// row-blocks and every column block: less traffic past the XCD's L2.  The
+// set of tiles and their results are those of decode_tile.  Measured (one
+// process, A/B over G = 1, 2, 4, 8): the bf16 kernels are best at 4 (down
+// 553 us against 562-567 at 8), the e4m3 ones at 8 (down 333-335 against
+// 342 at 4; gate/up 557-560 at 4 and 8, 590-597 at 1).
+constexpr int kTileGroupBf16 = 4;
+constexpr int kTileGroupFp8 = 8;
 
+template <int G>
 __device__ __forceinline__ void decode_tile_grouped(int t, int n_tiles_n, const int32_t* tstart,
                                                     const int32_t* __restrict__ offsets,
                                                     int n_experts, int& e, int64_t& row0,
@@ -157,11 +161,11 @@ __device__ __forceinline__ void decode_tile_grouped(int t, int n_tiles_n, const 
   e = lo;
   const int u = t - tstart[e] * n_tiles_n;  // tile within the expert
   const int me = tstart[e + 1] - tstart[e];
-  const int g = u / (kTileGroupM * n_tiles_n);
-  const int gm = me - g * kTileGroupM < kTileGroupM ? me - g * kTileGroupM : kTileGroupM;
-  const int v = u - g * kTileGroupM * n_tiles_n;
+  const int g = u / (G * n_tiles_n);
+  const int gm = me - g * G < G ? me - g * G : G;
+  const int v = u - g * G * n_tiles_n;
   const int n_tile = v / gm;
-  row0 = offsets[e] + static_cast<int64_t>(g * kTileGroupM + (v - n_tile * gm)) * kBM;
+  row0 = offsets[e] + static_cast<int64_t>(g * G + (v - n_tile * gm)) * kBM;
   row_end = offsets[e + 1];
   n0 = n_tile * kBN;
 }
@@ -506,7 +510,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto fetch_src = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupFp8>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
     const int64_t lim = row_end - 1 - r0;
 #pragma unroll
@@ -519,7 +523,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupFp8>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
@@ -696,7 +700,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto row_src = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupFp8>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     return gather_src[row0 + tid < row_end ? row0 + tid : row_end - 1];
   };
   int32_t my_src = 0;
@@ -706,7 +710,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   for (int t = first; t < hi; t += per_xcd) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupFp8>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     // this thread's row scale (tid < 256) or column scale (tid >= 256) of the
     // tile, loaded now and staged in LDS after the K loop
     float my_scale;
@@ -934,7 +938,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   auto fetch_src = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupBf16>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
     // rows past the segment repeat its last row (its token row stays cached)
     const int64_t lim = row_end - 1 - r0;
@@ -948,7 +952,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   auto set_load_tile = [&](int t) __attribute__((always_inline)) {
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupBf16>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     e = __builtin_amdgcn_readfirstlane(e);
     n0 = __builtin_amdgcn_readfirstlane(n0);
     const int r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row0));
@@ -1116,7 +1120,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
 
     int e, n0;
     int64_t row0, row_end;
-    decode_tile_grouped(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
+    decode_tile_grouped<kTileGroupBf16>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     // stage 1 is idle here: the tile's last step (odd) read it, step 0 of the
     // next tile writes it only after the epilogue's last barrier
     if constexpr (DSWIGLU)
