@@ -81,6 +81,18 @@ __device__ __forceinline__ float swiglu_bf16_points(float g, float u) {
   return silu_f32(__uint_as_float(gu << 16)) * __uint_as_float(gu & 0xffff0000u);
 }
 
+// Byte offset of gathered token row tk: tk * row_bytes + add, as a 24-bit
+// multiply-add (the hosts bound tk * row_bytes below 2^31 and row_bytes below
+// 2^23).  Written as a plain 32-bit expression it compiled to a 64-bit
+// multiply-add whose unused high addend half the register allocator placed on
+// the destination of a gather-source load still in flight; the wait-count
+// pass then waited for that load, which (loads complete in order) drained
+// every operand load of the pipeline at each tile switch.
+__device__ __forceinline__ uint32_t gather_offset(int tk, int row_bytes, int add) {
+  return __umul24(static_cast<uint32_t>(tk), static_cast<uint32_t>(row_bytes)) +
+         static_cast<uint32_t>(add);
+}
+
 // Exclusive scan of per-expert m-tile counts into tstart[0..n_experts];
 // returns the total.  NT threads, each taking kMaxExperts / NT experts.
 template <int NT = kThreads>
@@ -535,8 +547,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
       for (int j = 0; j < 2; ++j) {
         int tk = pf_src[j] >= 0 ? pf_src[j] / gather_k : 0;
         tk = tk < gather_rows ? tk : gather_rows - 1;
-        a_voff[j] = static_cast<uint32_t>(tk) * static_cast<uint32_t>(row_bytes) +
-                    static_cast<uint32_t>(dma_byte);
+        a_voff[j] = gather_offset(tk, row_bytes, dma_byte);
       }
       if (t + per_xcd < hi) fetch_src(t + per_xcd);
     } else {
@@ -972,8 +983,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
       for (int i = 0; i < 8; ++i) {
         int tk = pf_src[i] >= 0 ? pf_src[i] / gather_k : 0;
         tk = tk < gather_rows ? tk : gather_rows - 1;
-        a_off[i] = static_cast<uint32_t>(tk) * static_cast<uint32_t>(row_bytes) +
-                   static_cast<uint32_t>(ld_c * 16);
+        a_off[i] = gather_offset(tk, row_bytes, ld_c * 16);
       }
       if (t + per_xcd < hi) fetch_src(t + per_xcd);
     } else {
@@ -999,14 +1009,25 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     }
   };
   // Once every step is loaded the load side repeats the last one, so every
-  // K step issues the same loads.
-  auto advance = [&]() __attribute__((always_inline)) {
+  // K step issues the same loads.  The load side runs two steps ahead and
+  // kpad is even, so it crosses into the next tile only in the advance that
+  // follows an odd step's loads (WRAP): the even steps' advance has no tile
+  // switch on its path, and the compiler's wait counts for the next tile's
+  // gather sources then see a whole step of loads between their issue and
+  // their use.  The gate/up kernels use it (with the gather offset below
+  // it took the gathered gate/up GEMM 1.0-1.6 % faster, bit-identical); the
+  // others keep the switch check in every step, which measured 0.3-0.6 %
+  // faster for the down GEMM.
+  auto advance = [&](auto Wc) __attribute__((always_inline)) {
     if (ld_g + 1 < iters) {
       ++ld_g;
-      if (++ld_kb == kpad) {
-        ld_kb = 0;
-        ld_t += per_xcd;
-        set_load_tile(ld_t);
+      ++ld_kb;
+      if constexpr (decltype(Wc)::value) {
+        if (ld_kb == kpad) {
+          ld_kb = 0;
+          ld_t += per_xcd;
+          set_load_tile(ld_t);
+        }
       }
     }
   };
@@ -1048,6 +1069,23 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   };
   f32x16 acc[4][4];
 
+  // With the SwiGLU epilogue (gate/up) the last sub-step's 16 MFMAs run after
+  // the step's barrier (tail_mfma), beside the next step's first fragment
+  // reads, which otherwise leave the matrix core idle until they land
+  // (measured 1.1 % on the gathered gate/up GEMM at both bf16 workloads,
+  // bit-identical; the down GEMM was unchanged or 0.7 % slower, so it keeps
+  // every MFMA before the barrier).
+  constexpr bool kTailAfterBarrier = SWIGLU;
+  auto tail_mfma = [&]() __attribute__((always_inline)) {
+    if constexpr (kTailAfterBarrier) {
+      constexpr int b = (E::kSub - 1) & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[b][j], fa[b][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   // K step kb of a tile on stage P (= parity of the global step g; fragments
   // for sub-step 0 are already in buffer 0).  Each sub-step issues a quarter
   // of step g+2's loads into the free register slot, writes a quarter of step
@@ -1068,10 +1106,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
 #pragma unroll
       for (int pp = 0; pp < kParts; ++pp) park_part(pk_a, pk_b, P ^ 1, s * kParts + pp, keep);
       if (s + 1 < E::kSub) read_frags((s + 1) & 1, P, s + 1);
+      if (!kTailAfterBarrier || s + 1 < E::kSub) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
+          for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma(fb[s & 1][j], fa[s & 1][i], acc[i][j]);
+      }
       // Per 4 MFMAs: kParts global loads, kParts LDS writes, 2 * kParts LDS reads.
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1085,7 +1125,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    advance();
+    advance(IntC<SWIGLU ? P : 1>{});
     barrier_lds();
   };
 
@@ -1093,10 +1133,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
   set_load_tile(first);
 #pragma unroll
   for (int p = 0; p < 4; ++p) issue_part(ra0, rb0, p);
-  advance();
+  advance(IntC<SWIGLU ? 0 : 1>{});
 #pragma unroll
   for (int p = 0; p < 4; ++p) issue_part(ra1, rb1, p);
-  advance();
+  advance(IntC<1>{});
 #pragma unroll
   for (int p = 0; p < 4; ++p) park_part(ra0, rb0, 0, p, ODD && ksteps == 0 ? 0u : ~0u);
   __syncthreads();
@@ -1113,8 +1153,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_regs(
     for (int kb = 0; kb < kpad; kb += 2) {
       step(IntC<0>{}, kb);
       read_frags(0, 1, 0);
+      tail_mfma();
       step(IntC<1>{}, kb + 1);
       if (kb + 2 < kpad) read_frags(0, 0, 0);
+      tail_mfma();
     }
     g += kpad;
 
@@ -1563,8 +1605,7 @@ __device__ __forceinline__ void fused_phase(
       for (int i = 0; i < 8; ++i) {
         int tk = pf_src[i] >= 0 ? pf_src[i] / gather_k : 0;
         tk = tk < gather_rows ? tk : gather_rows - 1;
-        a_off[i] = static_cast<uint32_t>(tk) * static_cast<uint32_t>(row_bytes) +
-                   static_cast<uint32_t>(ld_c * 16);
+        a_off[i] = gather_offset(tk, row_bytes, ld_c * 16);
       }
       if (mine(p_next)) fetch_src(p_next);
     } else {
