@@ -590,14 +590,22 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     __builtin_amdgcn_raw_ptr_buffer_load_lds(e_rsrc, (lds_ptr_t)base, 4, e_voff, ld_kb * 2, 0, 0);
   };
   // Once every step is loaded the load side repeats the last one (into a
-  // stage nothing reads), so every step issues the same DMA count.
-  auto advance = [&]() __attribute__((always_inline)) {
+  // stage nothing reads), so every step issues the same DMA count.  The load
+  // side runs three steps ahead and ks is even, so it crosses into the next
+  // tile only in the advance of an even step (and of the prologue's second
+  // step): with the tile switch (WRAP) only there, the compiler's wait for
+  // the next tile's gather sources no longer lands mid-step on a path with a
+  // few DMAs since their issue (it drained the DMA ring once per tile).
+  auto advance = [&](auto Wc) __attribute__((always_inline)) {
     if (ld_g + 1 < iters) {
       ++ld_g;
-      if (++ld_kb == ks) {
-        ld_kb = 0;
-        ld_t += per_xcd;
-        set_load_tile(ld_t);
+      ++ld_kb;
+      if constexpr (decltype(Wc)::value) {
+        if (ld_kb == ks) {
+          ld_kb = 0;
+          ld_t += per_xcd;
+          set_load_tile(ld_t);
+        }
       }
     }
   };
@@ -657,7 +665,7 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     if (kScaledA && b == 1 && (ld_kb & 1) == 0) issue_exp_dma();
 #pragma unroll
     for (int j = 0; j < 2; ++j) issue_dma((g + 3) & 3, j);
-    advance();
+    advance(IntC<b == 0>{});
     read_frags(IntC<b ^ 1>{}, (g + 1) & 3, g + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -692,20 +700,6 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     __builtin_amdgcn_s_barrier();
   };
 
-  // Prologue: steps 0, 1, 2 into stages 0, 1, 2; steps 0 and 1 complete.
-  if (GATHER) fetch_src(first);
-  set_load_tile(first);
-#pragma unroll
-  for (int st = 0; st < 3; ++st) {
-    if (kScaledA && (ld_kb & 1) == 0) issue_exp_dma();
-#pragma unroll
-    for (int j = 0; j < 2; ++j) issue_dma(st, j);
-    advance();
-  }
-  wait_vm_lgkm0<4>();
-  __builtin_amdgcn_s_barrier();
-  read_frags(IntC<0>{}, 0, 0);
-
   // GATHER: the source of tile row tid (tid < 256) of the current tile,
   // loaded one tile ahead so that the scale lookup never waits on it
   auto row_src = [&](int t) __attribute__((always_inline)) {
@@ -714,8 +708,26 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
     decode_tile_grouped<kTileGroupFp8>(t, n_tiles_n, tstart, offsets, n_experts, e, row0, row_end, n0);
     return gather_src[row0 + tid < row_end ? row0 + tid : row_end - 1];
   };
+  // (loaded before the prologue's DMAs, so that its use at the first tile's
+  // start finds them between its issue and its use, as at every later tile)
   int32_t my_src = 0;
   if (GATHER && tid < kBM) my_src = row_src(first);
+  // Prologue: steps 0, 1, 2 into stages 0, 1, 2; steps 0 and 1 complete.
+  if (GATHER) fetch_src(first);
+  set_load_tile(first);
+  auto prologue_step = [&](int st, auto Wc) __attribute__((always_inline)) {
+    if (kScaledA && (ld_kb & 1) == 0) issue_exp_dma();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) issue_dma(st, j);
+    advance(Wc);
+  };
+  prologue_step(0, IntC<0>{});
+  prologue_step(1, IntC<1>{});
+  prologue_step(2, IntC<0>{});
+  wait_vm_lgkm0<4>();
+  __builtin_amdgcn_s_barrier();
+  read_frags(IntC<0>{}, 0, 0);
+
 
   int g = 0;
   for (int t = first; t < hi; t += per_xcd) {
@@ -745,14 +757,20 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    for (int kb = 0; kb < ks; kb += 2, g += 2) {
+    // ks >= 2: a do-while, so that no path skips the K loop between a load
+    // issued at the tile's start and its use in the epilogue (the
+    // compiler's wait counts then need not drain the DMA ring there)
+    int kb = 0;
+    do {
       if (kScaledA) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) ex_cur[i] = ex_nxt[i];
       }
       step(IntC<0>{}, g, IntC<4>{});
       step(IntC<1>{}, g + 1, IntC<4>{});
-    }
+      kb += 2;
+      g += 2;
+    } while (kb < ks);
     // the previous tile's epilogue read sscale before this tile's barriers
     sscale[tid] = my_scale;
     barrier_lds();
