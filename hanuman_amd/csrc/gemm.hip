@@ -644,10 +644,15 @@ __global__ __launch_bounds__(kW8Threads) void grouped_gemm_w8_fp8(
   auto read_frags = [&](auto Bc, int stage, int s) __attribute__((always_inline)) {
     constexpr int b = decltype(Bc)::value;
     const uint8_t* base = smem + stage * kW8StageBytes;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[b][i] = read_frag(base + fa_off + i * 32 * kW8StepBytes);
+    // B's two fragments first: the MFMAs run row fragment by row fragment
+    // (i outer), so fragment (i, j) needs B's j early and A's i only from
+    // MFMA 2 i on, and the last read issued is needed two MFMAs from the end
+    // (measured: gate/up 2.2 % and down 1 % faster than A first; the bf16
+    // kernel, four B fragments per sub-step, was 1 % slower with it)
 #pragma unroll
     for (int j = 0; j < 2; ++j) fb[b][j] = read_frag(base + fb_off + j * 32 * kW8StepBytes);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[b][i] = read_frag(base + fa_off + i * 32 * kW8StepBytes);
     if (kScaledA && b == 0) {
       const uint8_t* ex = smem + kW8Lds + ((s >> 1) & 1) * 2048 + wm * 1024 + frow * 4;
 #pragma unroll
