@@ -79,6 +79,9 @@ def algorithmic(wl, kept_rows: int) -> dict:
                     HBM_PEAK_GBS)
     # fp8 on bf16 tokens: x quantised per token (read once, codes and scales written)
     w["quant_x"] = ("hbm", T * D * x_in + T * D + T * 4, HBM_PEAK_GBS)
+    # the same quantisation in the router's launch, beside its float64 MFMA
+    # chains, which bound the launch: priced by the router's work
+    w["router_quant_x"] = w["router"]
     if wl.expert == "swiglu":
         w["gate_up"] = ("mfma", 2 * 2 * kept_rows * D * F, mfma_peak)
         w["down"] = ("mfma", 2 * kept_rows * F * D, mfma_peak)
@@ -237,7 +240,13 @@ def main():
     # own loads (no dispatched copy of x), so there is no separate stage.
     fused = layer.fused_dispatch
     fp8_gather = layer.fp8_gather
-    stages = ["router", "plan"] + (["quant_x"] if fp8_gather else [] if fused else ["permute"])
+    # fp8 on bf16 tokens: x's quantisation runs inside the router's launch
+    quant_in_router = fp8_gather and layer.logits_in is None
+    if fp8_gather:
+        dispatch_stages = [] if quant_in_router else ["quant_x"]
+    else:
+        dispatch_stages = [] if fused else ["permute"]
+    stages = ["router_quant_x" if quant_in_router else "router", "plan"] + dispatch_stages
     if wl.expert == "swiglu":
         stages += (["gate_up", "down"] if fp8 else
                    ["ffn"] if layer.fused_ffn else ["gate_up", "down"])
@@ -253,13 +262,16 @@ def main():
                 next(marks).record()
 
         mark()
-        logits, top_idx, gates = layer.route()
+        logits, top_idx, gates, xq = layer.route_quant()
         mark()
         plan = K.dispatch_plan(top_idx, wl.n_experts, layer.capacity, layer.workspace)
         mark()
         if fp8 and fp8_gather:
-            x_q, x_s = K.quantize_rows_fp8(layer.x)
-            mark()
+            if xq is None:
+                x_q, x_s = K.quantize_rows_fp8(layer.x)
+                mark()
+            else:
+                x_q, x_s = xq
             h_q, h_e = K.grouped_gate_up_fp8_gather_qh(x_q, x_s, plan, layer.w_gate_up,
                                                        layer.w_gate_up_scale)
             mark()

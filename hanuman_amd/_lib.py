@@ -37,6 +37,8 @@ SIGNATURES = {
     "hmoe_plan_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "hmoe_router": (_i32, [_vp, _i32, _vp, _i32, _vp, _i64, _i32, _i32, _i32, _i32, _f32,
                            _vp, _vp, _vp, _vp]),
+    "hmoe_router_quant_fp8": (_i32, [_vp, _i32, _vp, _i32, _vp, _i64, _i32, _i32, _i32, _i32,
+                                     _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hmoe_router_from_logits": (_i32, [_vp, _vp, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
     "hmoe_dispatch_plan": (_i32, [_vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _sz, _vp]),

@@ -10,6 +10,7 @@
 #include <atomic>
 
 #include "hmoe_common.h"
+#include "quant_e4m3.h"
 
 namespace hmoe {
 namespace {
@@ -338,14 +339,37 @@ struct alignas(16) RouterLds {
 // WV: n_experts is a multiple of the W elements in 16 bytes, so a chunk of W
 // (kRDc consecutive rows of n_experts values, contiguous in memory) is staged
 // with 16-byte loads and LDS writes.
-template <int NT, int ES, int NW, typename XT, typename WT, bool WV>
+//
+// QX: the launch also quantises x to e4m3 per token (the rule and code of
+// hmoe_quantize_rows_fp8): workgroups past the first router_blocks take NW
+// rows of x each, one wave per row.  They start once the router's workgroups
+// are placed and run beside them, whose float64 MFMA chains leave the memory
+// system and most of the VALU issue idle.
+template <int NT, int ES, int NW, typename XT, typename WT, bool WV, bool QX = false>
 __global__ __launch_bounds__(64 * NW) void router_kernel(const XT* __restrict__ x, const WT* __restrict__ w,
                                                      const float* __restrict__ bias, int64_t tokens,
                                                      int d_model, int n_experts, int top_k, int mode,
                                                      float rsf, float* __restrict__ logits,
                                                      int32_t* __restrict__ top_idx,
-                                                     float* __restrict__ gates) {
+                                                     float* __restrict__ gates,
+                                                     uint8_t* __restrict__ x_q,
+                                                     float* __restrict__ x_scale, int router_blocks) {
   static_assert(NT % ES == 0, "expert tiles must split evenly");
+  static_assert(!QX || sizeof(XT) == 2, "x is quantised from bf16");
+  if constexpr (QX) {
+    if (static_cast<int>(blockIdx.x) >= router_blocks) {
+      const int64_t r = static_cast<int64_t>(static_cast<int>(blockIdx.x) - router_blocks) * NW +
+                        (threadIdx.x >> 6);
+      if (r < tokens) {
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(x) + r * d_model;
+        if (d_model <= 64 * kRowRegs * 8)
+          quant_row_e4m3<true>(xr, d_model, x_q + r * d_model, x_scale + r);
+        else
+          quant_row_e4m3<false>(xr, d_model, x_q + r * d_model, x_scale + r);
+      }
+      return;
+    }
+  }
   constexpr int kThr = 64 * NW;
   constexpr int kNP = RouterLds<NT, ES, NW, WV>::kNP;
   constexpr int kTB = RouterLds<NT, ES, NW, WV>::kTB;
@@ -664,21 +688,47 @@ int stream_cus(hipStream_t s) {
   return cus > 0 ? cus : 0;
 }
 
+// Optional e4m3 quantisation of x in the router's launch (router_kernel QX).
+struct XQuant {
+  uint8_t* q = nullptr;
+  float* scale = nullptr;
+};
+
 template <int NT, int NW, typename XT, typename WT>
 void launch_router_nw(const void* x, const void* w, const float* bias, int64_t tokens,
                       int d_model, int n_experts, int top_k, int mode, float rsf, float* logits,
-                      int32_t* top_idx, float* gates, hipStream_t stream) {
+                      int32_t* top_idx, float* gates, hipStream_t stream, XQuant xq) {
   constexpr int ES = NT >= 2 ? 2 : 1;
-  const dim3 grid(static_cast<unsigned>(ceil_div(tokens, RouterLds<NT, ES, NW>::kTB)));
-  if (n_experts % (16 / static_cast<int>(sizeof(WT))) == 0 &&
-      reinterpret_cast<uintptr_t>(w) % 16 == 0)
+  const int rblocks = static_cast<int>(ceil_div(tokens, RouterLds<NT, ES, NW>::kTB));
+  const bool wv = n_experts % (16 / static_cast<int>(sizeof(WT))) == 0 &&
+                  reinterpret_cast<uintptr_t>(w) % 16 == 0;
+  if constexpr (sizeof(XT) == 2) {
+    if (xq.q != nullptr) {
+      const dim3 grid(static_cast<unsigned>(rblocks + ceil_div(tokens, NW)));
+      if (wv)
+        hipLaunchKernelGGL((router_kernel<NT, ES, NW, XT, WT, true, true>), grid, dim3(64 * NW), 0,
+                           stream, static_cast<const XT*>(x), static_cast<const WT*>(w), bias,
+                           tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates,
+                           xq.q, xq.scale, rblocks);
+      else
+        hipLaunchKernelGGL((router_kernel<NT, ES, NW, XT, WT, false, true>), grid, dim3(64 * NW), 0,
+                           stream, static_cast<const XT*>(x), static_cast<const WT*>(w), bias,
+                           tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates,
+                           xq.q, xq.scale, rblocks);
+      return;
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(rblocks));
+  if (wv)
     hipLaunchKernelGGL((router_kernel<NT, ES, NW, XT, WT, true>), grid, dim3(64 * NW), 0, stream,
                        static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
-                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
+                       n_experts, top_k, mode, rsf, logits, top_idx, gates, nullptr, nullptr,
+                       rblocks);
   else
     hipLaunchKernelGGL((router_kernel<NT, ES, NW, XT, WT, false>), grid, dim3(64 * NW), 0, stream,
                        static_cast<const XT*>(x), static_cast<const WT*>(w), bias, tokens, d_model,
-                       n_experts, top_k, mode, rsf, logits, top_idx, gates);
+                       n_experts, top_k, mode, rsf, logits, top_idx, gates, nullptr, nullptr,
+                       rblocks);
 }
 
 // From 64 experts up, workgroups of 8 waves (64 tokens) when they still give
@@ -689,31 +739,32 @@ void launch_router_nw(const void* x, const void* w, const float* bias, int64_t t
 template <int NT, typename XT, typename WT>
 void launch_router(const void* x, const void* w, const float* bias, int64_t tokens, int d_model,
                    int n_experts, int top_k, int mode, float rsf, float* logits, int32_t* top_idx,
-                   float* gates, hipStream_t stream) {
+                   float* gates, hipStream_t stream, XQuant xq) {
   if constexpr (NT >= 4) {
     const int cus = stream_cus(stream);
     if (cus > 0 && ceil_div(tokens, RouterLds<NT, 2, 8>::kTB) >= cus) {
       launch_router_nw<NT, 8, XT, WT>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf,
-                                      logits, top_idx, gates, stream);
+                                      logits, top_idx, gates, stream, xq);
       return;
     }
   }
   launch_router_nw<NT, 4, XT, WT>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits,
-                                  top_idx, gates, stream);
+                                  top_idx, gates, stream, xq);
 }
 
 template <int NT>
 void dispatch_router(int x_dtype, int w_dtype, const void* x, const void* w, const float* bias,
                      int64_t tokens, int d_model, int n_experts, int top_k, int mode, float rsf,
-                     float* logits, int32_t* top_idx, float* gates, hipStream_t s) {
+                     float* logits, int32_t* top_idx, float* gates, hipStream_t s,
+                     XQuant xq = XQuant()) {
   if (x_dtype == HMOE_BF16 && w_dtype == HMOE_F32)
-    launch_router<NT, uint16_t, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, uint16_t, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
   else if (x_dtype == HMOE_F32 && w_dtype == HMOE_F32)
-    launch_router<NT, float, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, float, float>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
   else if (x_dtype == HMOE_BF16 && w_dtype == HMOE_BF16)
-    launch_router<NT, uint16_t, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, uint16_t, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
   else
-    launch_router<NT, float, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
+    launch_router<NT, float, uint16_t>(x, w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
 }
 
 int validate_routing(int64_t tokens, int n_experts, int top_k, int mode) {
@@ -756,6 +807,39 @@ extern "C" int hmoe_router(const void* x, int x_dtype, const void* router_w, int
   else
     dispatch_router<16>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s);
   return check_launch("hmoe_router");
+}
+
+extern "C" int hmoe_router_quant_fp8(const void* x, int x_dtype, const void* router_w, int w_dtype,
+                                     const float* bias, int64_t tokens, int d_model, int n_experts,
+                                     int top_k, int mode, float routed_scaling_factor,
+                                     float* logits, int32_t* top_idx, float* gates, uint8_t* x_q,
+                                     float* x_scale, hmoe_stream_t stream) {
+  using namespace hmoe;
+  if (int rc = validate_routing(tokens, n_experts, top_k, mode)) return rc;
+  HMOE_REQUIRE(d_model >= 8 && d_model % 8 == 0,
+               "router_quant_fp8: d_model must be a positive multiple of 8 (got %d)", d_model);
+  HMOE_REQUIRE(x_dtype == HMOE_BF16, "router_quant_fp8: x dtype must be BF16");
+  HMOE_REQUIRE(w_dtype == HMOE_F32 || w_dtype == HMOE_BF16,
+               "router_quant_fp8: weight dtype must be F32 or BF16");
+  if (tokens == 0) return HMOE_OK;
+  HMOE_REQUIRE(x && router_w && logits && top_idx && gates && x_q && x_scale,
+               "router_quant_fp8: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float rsf = routed_scaling_factor;
+  XQuant xq;
+  xq.q = x_q;
+  xq.scale = x_scale;
+  if (n_experts <= 16)
+    dispatch_router<1>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
+  else if (n_experts <= 32)
+    dispatch_router<2>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
+  else if (n_experts <= 64)
+    dispatch_router<4>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
+  else if (n_experts <= 128)
+    dispatch_router<8>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
+  else
+    dispatch_router<16>(x_dtype, w_dtype, x, router_w, bias, tokens, d_model, n_experts, top_k, mode, rsf, logits, top_idx, gates, s, xq);
+  return check_launch("hmoe_router_quant_fp8");
 }
 
 extern "C" int hmoe_router_from_logits(const float* logits, const float* bias, int64_t tokens,

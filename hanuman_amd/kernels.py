@@ -82,6 +82,38 @@ def router(x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None, t
     return logits, top_idx, gates
 
 
+def router_quant_fp8(x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None,
+                     top_k: int, mode: int = _lib.ROUTE_SIGMOID_BIAS,
+                     routed_scaling_factor: float = 1.0):
+    """:func:`router` and :func:`quantize_rows_fp8` of ``x`` in one launch
+    (``hmoe_router_quant_fp8``): the per-token e4m3 quantisation runs in
+    workgroups beside the router's.  ``x`` is bf16 ``[T,D]``.  Returns
+    (logits, top_idx, gates, x_q uint8 [T,D], x_scale f32 [T]), bit-identical
+    to the two calls."""
+    _check(x, "x", 2)
+    _check(router_w, "router_w", 2)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("router_quant_fp8 takes bf16 tokens")
+    T, D = x.shape
+    if router_w.shape[0] != D:
+        raise ValueError(f"router_w has {router_w.shape[0]} rows, x has d_model {D}")
+    N = router_w.shape[1]
+    if bias is not None:
+        _check(bias, "bias", 1)
+        if bias.dtype != torch.float32 or bias.shape[0] != N:
+            raise ValueError("bias must be float32 [n_experts]")
+    dev = x.device
+    logits = torch.empty((T, N), dtype=torch.float32, device=dev)
+    top_idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    gates = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    x_q = torch.empty((T, D), dtype=torch.uint8, device=dev)
+    x_s = torch.empty(T, dtype=torch.float32, device=dev)
+    call("hmoe_router_quant_fp8", _ptr(x), _dtype_code(x), _ptr(router_w), _dtype_code(router_w),
+         _ptr(bias), T, D, N, top_k, mode, float(routed_scaling_factor), _ptr(logits),
+         _ptr(top_idx), _ptr(gates), _ptr(x_q), _ptr(x_s), _stream())
+    return logits, top_idx, gates, x_q, x_s
+
+
 def router_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int,
                        mode: int = _lib.ROUTE_SOFTMAX, routed_scaling_factor: float = 1.0):
     """Top-k indices and gates from given float32 logits [T,N]."""

@@ -96,15 +96,28 @@ class DeviceLayer:
             return self.logits_in, top_idx, gates
         return K.router(self.x, self.router_w, None, wl.top_k, self.mode)
 
-    def experts_fp8(self, plan):
+    def route_quant(self):
+        """The router and, for fp8 experts gathering from per-token codes, x's
+        e4m3 quantisation in the same launch (``hmoe_router_quant_fp8``: the
+        quantisation runs beside the router's float64 MFMA chains).  Returns
+        (logits, top_idx, gates, (x_q, x_scale) or None)."""
+        wl = self.wl
+        if self.fp8_gather and self.logits_in is None:
+            logits, top_idx, gates, x_q, x_s = K.router_quant_fp8(self.x, self.router_w, None,
+                                                                   wl.top_k, self.mode)
+            return logits, top_idx, gates, (x_q, x_s)
+        return (*self.route(), None)
+
+    def experts_fp8(self, plan, xq=None):
         """e4m3 dispatch and expert GEMMs: (xs_q, xs_scale, h_q, h_exp, ys).
         With bf16 tokens x is quantised per token and the gate/up GEMM gathers
         its rows from the codes (``xs_q``/``xs_scale`` are then per token,
         ``[T, D]``/``[T]``); otherwise they are the dispatched rows.  h leaves
         the gate/up GEMM block-scaled (codes ``h_q``, biased exponents
-        ``h_exp`` per 32 columns) and the down GEMM's MFMA applies them."""
+        ``h_exp`` per 32 columns) and the down GEMM's MFMA applies them.
+        ``xq``: x's codes and scales when the router's launch made them."""
         if self.fp8_gather:
-            xs_q, xs_s = K.quantize_rows_fp8(self.x)
+            xs_q, xs_s = xq if xq is not None else K.quantize_rows_fp8(self.x)
             h_q, h_e = K.grouped_gate_up_fp8_gather_qh(xs_q, xs_s, plan, self.w_gate_up,
                                                        self.w_gate_up_scale)
         else:
@@ -116,12 +129,12 @@ class DeviceLayer:
 
     def forward(self) -> dict:
         wl = self.wl
-        logits, top_idx, gates = self.route()
+        logits, top_idx, gates, xq = self.route_quant()
         plan = K.dispatch_plan(top_idx, wl.n_experts, self.capacity, self.workspace)
         extra = {}
         h = None
         if self.fp8:
-            xs, xs_s, h_q, h_e, ys = self.experts_fp8(plan)
+            xs, xs_s, h_q, h_e, ys = self.experts_fp8(plan, xq)
             extra = {"xs_scale": xs_s, "h_q": h_q, "h_exp": h_e,
                      "xs_per_token": self.fp8_gather}
         elif self.f32:

@@ -95,6 +95,41 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeRouter, RouterImpl,
                                   .Ret<ffi::Buffer<ffi::S32>>()
                                   .Ret<ffi::Buffer<ffi::F32>>());
 
+// The router and the per-token e4m3 quantisation of x in one launch (fp8
+// experts on bf16 tokens): x [T, D] bf16, router_w [D, N] (f32/bf16), bias
+// [N] f32 -> logits, top_idx, gates as hmoe_router, x_q [T, D] u8, x_scale
+// [T] f32 as hmoe_quantize_rows_fp8.
+static ffi::Error RouterQuantFp8Impl(hipStream_t stream, ffi::Buffer<ffi::BF16> x,
+                                     ffi::AnyBuffer w, ffi::Buffer<ffi::F32> bias, int64_t mode,
+                                     float rsf, ffi::ResultBuffer<ffi::F32> logits,
+                                     ffi::ResultBuffer<ffi::S32> top_idx,
+                                     ffi::ResultBuffer<ffi::F32> gates,
+                                     ffi::ResultBuffer<ffi::U8> x_q,
+                                     ffi::ResultBuffer<ffi::F32> x_scale) {
+  const int wd = DtypeCode(w.element_type());
+  if (wd < 0) return BadDtype("hmoe_router_quant_fp8 router_w");
+  const int64_t T = Rows(x);
+  const int D = static_cast<int>(Cols(x)), N = static_cast<int>(Cols(w));
+  const int K = static_cast<int>(Cols(*top_idx));
+  return Status(hmoe_router_quant_fp8(
+      x.untyped_data(), HMOE_BF16, w.untyped_data(), wd, bias.typed_data(), T, D, N, K,
+      static_cast<int>(mode), rsf, logits->typed_data(), top_idx->typed_data(),
+      gates->typed_data(), x_q->typed_data(), x_scale->typed_data(), S(stream)));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(HmoeRouterQuantFp8, RouterQuantFp8Impl,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Attr<int64_t>("mode")
+                                  .Attr<float>("routed_scaling_factor")
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::S32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::U8>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>());
+
 // logits [T, N] f32, bias [N] f32 -> top_idx [T, K] s32, gates [T, K] f32.
 static ffi::Error RouterFromLogitsImpl(hipStream_t stream, ffi::Buffer<ffi::F32> logits,
                                        ffi::Buffer<ffi::F32> bias, int64_t mode, float rsf,

@@ -52,6 +52,7 @@ ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX = 0, 1
 TARGETS = {
     # forward
     "hmoe_router": "HmoeRouter",
+    "hmoe_router_quant_fp8": "HmoeRouterQuantFp8",
     "hmoe_router_from_logits": "HmoeRouterFromLogits",
     "hmoe_dispatch_plan": "HmoeDispatchPlan",
     "hmoe_permute_rows": "HmoePermuteRows",

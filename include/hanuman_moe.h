@@ -145,6 +145,18 @@ int hmoe_permute_rows_fp8(const void* x, int x_dtype, int64_t tokens, int d_mode
 int hmoe_quantize_rows_fp8(const void* a, int64_t rows, int cols, const int32_t* offsets,
                            int n_experts, uint8_t* q, float* scale, hmoe_stream_t stream);
 
+/* hmoe_router (moe.py:175-192) and hmoe_quantize_rows_fp8(x, T, D, NULL, 0,
+ * x_q, x_scale) in one launch, for the fp8 experts on bf16 tokens: the
+ * quantisation runs in workgroups beside the router's, whose float64 matrix
+ * chains leave the memory system idle.  Outputs are bit-identical to the two
+ * calls.  x [T,D] HMOE_BF16 only; x_q [T,D] uint8, x_scale [T] f32; the
+ * router's arguments and limits as for hmoe_router. */
+int hmoe_router_quant_fp8(const void* x, int x_dtype, const void* router_w, int w_dtype,
+                          const float* bias, int64_t tokens, int d_model, int n_experts,
+                          int top_k, int mode, float routed_scaling_factor, float* logits,
+                          int32_t* top_idx, float* gates, uint8_t* x_q, float* x_scale,
+                          hmoe_stream_t stream);
+
 /* ---- expert weights: moe.py:204-206 (replaces the per-call `.astype(dtype)`
  *      of the stacked fp32 masters) ---------------------------------------- */
 

@@ -66,6 +66,18 @@ def test_router_rejects_bad_arguments(lib):
     # zero tokens is a no-op
     assert lib.hmoe_router(None, _lib.BF16, None, _lib.F32, None, 0, 64, 8, 2, 0, 1.0,
                            None, None, None, None) == _lib.OK
+    # the router with x's e4m3 quantisation: bf16 x only, every output given
+    rc = lib.hmoe_router_quant_fp8(p, _lib.F32, p, _lib.F32, None, 10, 64, 8, 2, 0, 1.0,
+                                   p, p, p, p, p, None)
+    assert rc == _lib.ERR_INVALID and "BF16" in _err(lib)
+    rc = lib.hmoe_router_quant_fp8(p, _lib.BF16, p, _lib.F32, None, 10, 64, 8, 2, 0, 1.0,
+                                   p, p, p, p, None, None)
+    assert rc == _lib.ERR_INVALID and "null" in _err(lib)
+    rc = lib.hmoe_router_quant_fp8(p, _lib.BF16, p, _lib.F32, None, 10, 60, 8, 2, 0, 1.0,
+                                   p, p, p, p, p, None)
+    assert rc == _lib.ERR_INVALID and "d_model" in _err(lib)
+    assert lib.hmoe_router_quant_fp8(None, _lib.BF16, None, _lib.F32, None, 0, 64, 8, 2, 0, 1.0,
+                                     None, None, None, None, None, None) == _lib.OK
 
 
 def test_plan_rejects_small_workspace_and_bad_sizes(lib):

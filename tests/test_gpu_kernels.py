@@ -102,6 +102,80 @@ def test_router_bit_exact(gpu, case):
     assert_bits_equal(host(g), g_ref, "gates")
 
 
+# The router with x's per-token e4m3 quantisation in the same launch: every
+# bf16-token router case above, plus rows past 4096 values (the two-pass
+# quantisation), a single token and the 8-wave router configuration.
+ROUTER_QUANT_CASES = [c for c in ROUTER_CASES if c[4] == "bf16"] + [
+    (2048, 4096, 32, 4, "bf16", "bf16", "softmax", 1.0, False),
+    (101, 4104, 16, 2, "bf16", "f32", "sigmoid", 2.5, True),
+    (1, 512, 8, 2, "bf16", "bf16", "softmax", 1.0, False),
+]
+
+
+@pytest.mark.parametrize("case", ROUTER_QUANT_CASES,
+                         ids=lambda c: f"T{c[0]}_D{c[1]}_N{c[2]}_K{c[3]}_{c[6]}")
+def test_router_quant_fp8_bit_exact(gpu, case):
+    """hmoe_router_quant_fp8 against the oracle's router and per-row e4m3
+    rule, bit for bit (rows of zeros and a wide dynamic range included)."""
+    T, D, N, Kk, _, wd, mode, rsf, with_bias = case
+    print(f"router+quant case {case}", flush=True)
+    rng = np.random.default_rng(T + D + N + 7)
+    x = rng.standard_normal((T, D)) * np.exp(rng.uniform(-12, 6, (T, 1)))
+    x = O.bf16_round(x.astype(np.float32))
+    x[T // 3] = 0.0
+    w = (0.02 * rng.standard_normal((D, N))).astype(np.float32)
+    if wd == "bf16":
+        w = O.bf16_round(w)
+    bias = (0.05 * rng.standard_normal(N)).astype(np.float32) if with_bias else None
+    logits_ref = O.router_logits(x, w)
+    if mode == "softmax":
+        idx_ref, g_ref = O.route_softmax(logits_ref, Kk)
+    else:
+        idx_ref, g_ref, _ = O.route_sigmoid(logits_ref, bias, Kk, rsf)
+    q_ref, s_ref = O.quantize_rows_e4m3(x)
+    wt = dev_bf16(w, gpu) if wd == "bf16" else dev_f32(w, gpu)
+    bt = dev_f32(bias, gpu) if bias is not None else None
+    m = _lib.ROUTE_SOFTMAX if mode == "softmax" else _lib.ROUTE_SIGMOID_BIAS
+    logits, idx, g, x_q, x_s = K.router_quant_fp8(dev_bf16(x, gpu), wt, bt, Kk, m, rsf)
+    torch.cuda.synchronize()
+    assert_bits_equal(host(logits), logits_ref, "logits")
+    assert_bits_equal(host(idx), idx_ref, "top_idx")
+    assert_bits_equal(host(g), g_ref, "gates")
+    assert_bits_equal(x_q.cpu().numpy(), q_ref, "x codes")
+    assert_bits_equal(x_s.cpu().numpy(), s_ref, "x scales")
+
+
+def test_router_quant_fp8_equals_separate_launches_at_fp8_workload(gpu):
+    """At the fp8 experts workload's shape (8192 tokens, d_model 4096, 32
+    experts, top-4, bf16 router weight) the one launch gives the bits of
+    hmoe_router followed by hmoe_quantize_rows_fp8."""
+    print("router+quant at 8192 x 4096, 32 experts", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    x = torch.randn(8192, 4096, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(4096, 32, generator=g) * 4096 ** -0.5).to(torch.bfloat16).to(gpu)
+    a = K.router(x, w, None, 4, _lib.ROUTE_SOFTMAX)
+    q, s = K.quantize_rows_fp8(x)
+    b = K.router_quant_fp8(x, w, None, 4, _lib.ROUTE_SOFTMAX)
+    torch.cuda.synchronize()
+    for name, u, v in zip(("logits", "top_idx", "gates", "x codes", "x scales"), (*a, q, s), b):
+        assert torch.equal(u, v), name
+
+
+def test_router_quant_fp8_refusals(gpu):
+    x = torch.zeros(8, 64, dtype=torch.float32, device=gpu)
+    w = torch.zeros(64, 8, dtype=torch.float32, device=gpu)
+    with pytest.raises(TypeError):
+        K.router_quant_fp8(x, w, None, 2)
+    lib = _lib.lib()
+    p = x.data_ptr()
+    rc = lib.hmoe_router_quant_fp8(p, _lib.F32, p, _lib.F32, None, 8, 64, 8, 2, 0, 1.0, p, p, p,
+                                   p, p, None)
+    assert rc == _lib.ERR_INVALID and "BF16" in lib.hmoe_last_error().decode()
+    rc = lib.hmoe_router_quant_fp8(p, _lib.BF16, p, _lib.F32, None, 8, 64, 8, 2, 0, 1.0, p, p, p,
+                                   None, p, None)
+    assert rc == _lib.ERR_INVALID and "null" in lib.hmoe_last_error().decode()
+
+
 @pytest.mark.parametrize("T,N,Kk,mode", [(16400, 64, 8, "softmax"), (700, 64, 8, "sigmoid"),
                                          (333, 50, 6, "softmax"), (16390, 40, 4, "sigmoid")])
 def test_router_ties_through_logits(gpu, T, N, Kk, mode):
