@@ -359,6 +359,12 @@ def main():
     stage_ms = {st: float(np.mean([evs[s][j].elapsed_time(evs[s][j + 1]) for s in range(args.steps)]))
                 for j, st in enumerate(stages)}
     stage_pass_ms = float(np.mean([evs[s][0].elapsed_time(evs[s][-1]) for s in range(args.steps)]))
+    if layer.fused_ffn:
+        import hanuman_amd.kernels as K
+        # the status word holds the last launch's outcome (bit 0: a down
+        # tile's bounded wait gave up and computed from an incomplete h)
+        if K.fused_status(layer.fused_ws) != 0:
+            raise SystemExit("bench: the fused gate/up + down launch reported a timed-out wait")
     kept = int(plan.offsets[-1].item())
     work = algorithmic(wl, kept)
     # The bf16 layer gathers its rows inside the gate/up GEMM, so the layer

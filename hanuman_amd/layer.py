@@ -143,8 +143,14 @@ class DeviceLayer:
             ys = K.grouped_down_f32(h, plan.offsets, self.w_down_f32)
         elif self.fused_ffn:
             xs = None
-            h, ys, _ = K.grouped_swiglu_fused(self.x, plan, self.w_gate_up, self.w_down,
-                                              self.fused_ws)
+            h, ys, ws = K.grouped_swiglu_fused(self.x, plan, self.w_gate_up, self.w_down,
+                                               self.fused_ws)
+            # a down tile whose bounded wait gave up computed from an
+            # incomplete h: refuse the result (reading the status synchronises,
+            # so not while a graph is being captured)
+            if not torch.cuda.is_current_stream_capturing() and K.fused_status(ws) != 0:
+                raise RuntimeError("grouped_swiglu_fused: a down tile's wait for its gate/up "
+                                   "tiles timed out; h and ys are not valid")
         elif self.fused_dispatch:
             xs = None
             h = K.grouped_gate_up_gather(self.x, plan, self.w_gate_up)
