@@ -148,7 +148,11 @@ class MoEConfig:
     routed_scaling_factor: float = 1.0
     routing: str = "sigmoid"          # "sigmoid" (moe.py:179-192) or "softmax"
     capacity_factor: float | None = None
-    fused: bool = True                # one launch for gate/up and down where the shapes allow
+    # fused: gate/up and down in one persistent launch where the shapes allow.
+    # Off by default, as in the torch layer: the two launches measure within
+    # noise of it, and its bounded wait reports a give-up only in the status
+    # word (uint32 8 of its workspace result), which this module does not read.
+    fused: bool = False
 
     @property
     def mode(self) -> int:
@@ -386,7 +390,7 @@ PARAM_NAMES = ("router", "bias", "expert_w_gate", "expert_w_up", "expert_w_down"
                "shared_w_gate", "shared_w_up", "shared_w_down")
 
 
-def moe_call(module, x, *, routing: str = "sigmoid", capacity_factor=None, fused: bool = True):
+def moe_call(module, x, *, routing: str = "sigmoid", capacity_factor=None, fused: bool = False):
     """Drop-in body of the reference ``MoE.__call__``: reads the module's
     parameters by their pytree names and runs :func:`moe_layer`."""
     params = {k: getattr(module, k).value for k in PARAM_NAMES}
