@@ -4,7 +4,8 @@ JAX and its FFI headers are absent from this image, so the handlers
 (``hanuman_amd/xla_ffi/hmoe_xla_ffi.cc``) and the JAX module
 (``hanuman_amd/xla_ffi/moe_jax.py``) cannot be built or run here.  These
 checks read their text: every compute entry point of the C ABI has a
-handler, every step INTEGRATION.md binds for training has one, and the JAX
+handler, every step of the training sequence that the integration guide
+at the repository root binds has one, and the JAX
 module's target table, its calls and the handler symbols agree.
 """
 import ast
