@@ -147,3 +147,47 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
     assert r.stdout.strip() == ""   # no JSON line
+
+
+def test_bench_algorithmic_work_closed_forms():
+    """The roofline denominators bench.py reports, from the closed forms:
+    grouped GEMM 6 R D F FLOP (gate 2 R D F, up 2 R D F, down 2 R F D); the
+    dispatch reads every token row once, writes every kept row and reads the
+    slot map; the combine reads every kept row, writes every token row and
+    reads the slot map and gates; the router's float64 dot products 2 T D N."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+    from hanuman_amd import workloads as W
+
+    wl = W.WORKLOADS["full_bf16"]   # 16384 tokens, D 2048, 64 experts, top-8, F 1024
+    T, D, N, K, F = 16384, 2048, 64, 8, 1024
+    kept = T * K
+    w = bench.algorithmic(wl, kept)
+    assert w["gate_up"][1] + w["down"][1] == 6 * kept * D * F == w["ffn"][1]
+    assert abs(w["ffn"][1] / 1e12 - 1.649) < 1e-3
+    assert w["permute"][1] == T * D * 2 + kept * D * 2 + kept * 4
+    assert w["combine"][1] == kept * D * 2 + T * D * 4 + kept * 8   # float32 output
+    assert w["router"] == ("fp64", 2 * T * D * N, bench.FP64_PEAK_TFLOPS)
+    assert w["gate_up"][2] == bench.BF16_PEAK_TFLOPS == 2500.0
+    # fewer kept rows (capacity drops) lower the GEMM and row traffic only
+    w2 = bench.algorithmic(wl, kept - 1000)
+    assert w["ffn"][1] - w2["ffn"][1] == 6 * 1000 * D * F
+    assert w["combine"][1] - w2["combine"][1] == 1000 * D * 2
+
+    wl = W.WORKLOADS["fp8_experts"]  # 8192 tokens, D 4096, 32 experts, top-4, F 2048, e4m3
+    T, D, N, K, F = 8192, 4096, 32, 4, 2048
+    kept = T * K
+    w = bench.algorithmic(wl, kept)
+    assert w["ffn"][1] == 6 * kept * D * F and w["ffn"][2] == bench.FP8_PEAK_TFLOPS == 5000.0
+    # codes and one float32 scale per dispatched row
+    assert w["permute"][1] == T * D * 2 + kept * (D + 4) + kept * 4
+    assert w["quant_x"][1] == T * D * 2 + T * D + T * 4
+    assert w["combine"][1] == kept * D * 2 + T * D * 2 + kept * 8   # bf16 output
+
+    wl = W.WORKLOADS["dispatch_identity"]  # logits given: the router is a read of them
+    T, N, K = 32768, 64, 8
+    w = bench.algorithmic(wl, T * K)
+    assert w["router"] == ("hbm", T * N * 4 + T * K * 8, bench.HBM_PEAK_GBS)
+    assert "gate_up" not in w
